@@ -1,0 +1,197 @@
+"""Benchmark of the MI355X-native quantized linear-layer hot path (one JSON line on stdout).
+
+Workload: the Q4_K decode GEMV at the Llama-3-8B layer shapes, batch 1 — one step is one
+decoder layer's linear products: QKV 4096->6144, O 4096->4096, gate 4096->14336, up 4096->14336, down 14336->4096.
+Weights are N(0, 0.02) from SplitMix64/Box-Muller (seed 0) quantized to Q4_K super-blocks; x is N(0, 1) (seed 1).
+Inputs are resident in HBM; the activations are quantized once before the timed region (the quant_act launch is timed
+separately and reported beside). Weight copies rotate over more than 2x the 256 MB Infinity Cache so every call
+streams its weights from HBM.
+
+value = algorithmic bytes (weights + 4*K fp32 x + 4*N fp32 y per GEMV) per step / seconds per step, in GB/s.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+MALL_BYTES = 256 << 20
+LAYER = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096)]
+METRIC = "Q4_K GEMV GB/s (% of HBM peak) + int8 GEMM TOPS, 1×MI355X"
+
+
+def gemv_bytes(ty, n, n_out, rows=1):
+    import kungfu_amd as kf
+
+    return kf.row_bytes(ty, n) * n_out + 4 * n * rows + 4 * n_out * rows
+
+
+def make_weights(ty, n, n_out, seed=0):
+    import kungfu_amd as kf
+
+    return kf.quantize(ty, kf.synth_normal(seed, 0.02, n * n_out).reshape(n_out, n))
+
+
+class Shape:
+    """One GEMV shape with its rotating device weight copies and resident quantized activations."""
+
+    def __init__(self, name, ty, n, n_out, copies, dev):
+        import torch
+
+        import kungfu_amd as kf
+
+        self.name, self.ty, self.n, self.n_out = name, ty, n, n_out
+        self.host_w = make_weights(ty, n, n_out, seed=0)
+        self.host_x = kf.synth_normal(1, 1.0, n).reshape(1, n)
+        w = torch.from_numpy(self.host_w).to(dev)
+        self.w = [w] + [w.clone() for _ in range(copies - 1)]
+        self.x = torch.from_numpy(self.host_x).to(dev)
+        self.act = kf.alloc_act(1, n, dev)
+        self.y = torch.empty((1, n_out), device=dev)
+        kf.quant_act(self.x, self.act, kf.act_kind(ty))
+        self.bytes = gemv_bytes(ty, n, n_out)
+
+    def gemv(self, i):
+        import kungfu_amd as kf
+
+        kf.gemv(self.ty, self.w[i % len(self.w)], self.act, self.y, 1, self.n, self.n_out)
+
+    def matmul(self, i):
+        import kungfu_amd as kf
+
+        kf.matmul(self.ty, self.w[i % len(self.w)], self.x, self.act, self.y, self.n_out)
+
+
+def time_launches(fn, iters, warm=3):
+    """Mean µs per call of fn(i) over iters back-to-back calls, bracketed by HIP events on the launch stream."""
+    import torch
+
+    for i in range(warm):
+        fn(i)
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(s)
+    for i in range(iters):
+        fn(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / iters
+
+
+def cpu_baseline(shapes, budget_s):
+    """The CPU backend's product (oracle restatement of ops::matmul_slice, OpenMP over output rows) on the same
+    weights and input: whole layer passes until budget_s of wall time is spent."""
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    oracle.lib()
+    total_bytes, passes, t0 = 0, 0, time.perf_counter()
+    while True:
+        for sh in shapes:
+            oracle.matmul_slice(sh.ty, sh.host_w, sh.n, sh.n_out, sh.host_x, threads=threads)
+            total_bytes += sh.bytes
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    return {"value": round(total_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} full layer passes (5 Q4_K GEMVs at M=1) of oracle matmul_slice in {el:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-seconds", type=float, default=5.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
+              "which this build does not run", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import kungfu_amd as kf
+
+    dev = torch.device("cuda:0")
+    kf.lib()
+    layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
+    copies = max(2, -(-2 * MALL_BYTES // layer_w_bytes) + 1)
+    shapes = [Shape(nm, kf.TYPE_Q4_K, n, no, copies, dev) for nm, n, no in LAYER]
+    step_bytes = sum(s.bytes for s in shapes)
+
+    def step(i):
+        for s in shapes:
+            s.gemv(i)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    for i in range(args.steps):
+        step(i)
+    e1.record(s)
+    torch.cuda.synchronize()
+    ms_step = e0.elapsed_time(e1) / args.steps
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+
+    # per-shape µs/call of the GEMV kernel alone and of the whole matmul (quant_act + GEMV)
+    per = {}
+    k1_bytes = k1_us = 0.0
+    for sh in shapes:
+        us = time_launches(sh.gemv, 200)
+        us_mm = time_launches(sh.matmul, 200)
+        per[sh.name] = {"n_in": sh.n, "n_out": sh.n_out, "us": round(us, 3), "GBs": round(sh.bytes / us / 1e3, 1),
+                        "frac": round(sh.bytes / us / 1e3 / HBM_PEAK_GBS, 4), "us_with_quant": round(us_mm, 3)}
+        if sh.n <= 4096:  # the launches of gemv_q4k_kernel<1>, the kernel with most of the step's time
+            k1_bytes += sh.bytes
+            k1_us += us
+    achieved = k1_bytes / k1_us / 1e3
+
+    # Q8_0 GEMV of configs[0] (4096x4096) on the GPU, rotating copies
+    q8 = Shape("q8_0", kf.TYPE_Q8_0, 4096, 4096, max(2, -(-2 * MALL_BYTES // (kf.row_bytes(8, 4096) * 4096)) + 1), dev)
+    us_q8 = time_launches(q8.gemv, 200)
+    del q8
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 x q4_K (int32 dot, f32 scale)",
+        "data": "synthetic: SplitMix64/Box-Muller N(0,0.02) weights quantized to Q4_K, N(0,1) activations",
+        "config": {"workload": "Q4_K decode GEMV, Llama-3-8B layer shapes, batch 1 (QKV, O, gate, up, down)",
+                   "bytes_per_step": step_bytes, "weight_copies": copies,
+                   "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "kernel": "gemv_q4k_kernel<1> (QKV, O, gate, up launches)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "shapes": per,
+        "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1)},
+        "int8_gemm_tops": None,
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

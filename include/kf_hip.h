@@ -1,0 +1,136 @@
+/*
+ * kf_hip.h — C ABI of the MI355X-native (gfx950) quantized linear-layer hot path of kungfu.
+ *
+ * This is the drop-in boundary a Rust `kf-backend-hip` crate binds (extern "C", plain pointers and sizes). It
+ * replaces, entry point for entry point, what the reference's CUDA backend launches for `Op::MatMul` on int8-capable
+ * weights (crates/kf-backend-cuda/src/exec.rs:2061-2109) and the backend trait methods around it
+ * (crates/kf-core/src/backend.rs:206-269). Paths are relative to the reference repository root.
+ *
+ * Conventions
+ *   - Weights are GGUF block bytes in their on-disk layout, unchanged: row-major [n_out][row_bytes], row_bytes =
+ *     n_in / block * block_bytes (crates/kf-quant/src/lib.rs:17-20). Supported: q8_0 (id 8), q4_K (id 12).
+ *   - Device pointers are HIP device addresses; `stream` is a hipStream_t (NULL = the null stream).
+ *   - Every call returns 0 on success or a negative KF_E_* code; kf_hip_last_error() then describes the failure
+ *     (per calling thread). No exception crosses the ABI. Shape checks mirror the reference's ensure!/bail! sites
+ *     (crates/kf-backend-cpu/src/ops.rs:309-320, crates/kf-backend-cuda/src/exec.rs:2017,2066-2071).
+ *   - Kernel-level entry points are stateless and asynchronous on `stream`; any number of threads may call them,
+ *     one stream per thread.
+ */
+#ifndef KF_HIP_H
+#define KF_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KF_HIP_ABI_VERSION 1
+
+/* ggml type ids (crates/kf-quant/src/types/q8_0.rs:4, types/q4_k.rs:4) */
+#define KF_TYPE_Q8_0 8u
+#define KF_TYPE_Q4_K 12u
+
+/* activation rounding kinds, the reference's round codes (crates/kf-backend-cuda/src/exec.rs:103-113) */
+#define KF_ACT_Q8_0 3
+#define KF_ACT_Q8K 4
+
+/* status codes */
+#define KF_OK 0
+#define KF_E_INVALID (-1)     /* bad shape, pointer or argument */
+#define KF_E_UNSUPPORTED (-2) /* weight type or kind not on this path */
+#define KF_E_HIP (-3)         /* a HIP runtime call or launch failed */
+#define KF_E_NOMEM (-4)       /* device or host allocation failed */
+
+/* ABI version of the loaded library (KF_HIP_ABI_VERSION it was built with). No reference counterpart. */
+int kf_hip_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). Plays the role of the anyhow::Error text the reference
+ * returns from Backend::run (crates/kf-core/src/backend.rs:212). */
+const char* kf_hip_last_error(void);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Activation quantization.
+ * The int8 activation scratch of `rows` rows of `n` columns (the reference's ActI8, crates/kf-quant/src/lib.rs:48-78,
+ * as laid out on the device by act_scratch_all, crates/kf-backend-cuda/src/kf8.rs:338-357):
+ *   q int8 [rows][n] | d16 f32 [rows][n/16] | s16 int32 [rows][n/16] | d32 f32 [rows][n/32] | s32 int32 [rows][n/32]
+ * each section 256-byte aligned from the base. */
+
+/* Bytes of that scratch. */
+size_t kf_hip_act_bytes(int rows, int n);
+
+/* Byte offsets of the five sections inside it (out[0..4] = q, d16, s16, d32, s32). */
+void kf_hip_act_offsets(int rows, int n, size_t out[5]);
+
+/* Activation kind the reference pairs with a weight type (act_kind, crates/kf-quant/src/lib.rs:154-163), or
+ * KF_E_UNSUPPORTED. */
+int kf_hip_act_kind(uint32_t ty);
+
+/* Quantizes x [rows][n] f32 (device, 16-byte aligned) into the scratch at `act` (device, 256-byte aligned).
+ * Replaces quant_act (crates/kf-backend-cuda/src/kernels/fused.cu:12-21) and quant_launch (exec.rs:2053-2056);
+ * bit-exact with quantize_activations (crates/kf-quant/src/lib.rs:81-140). n must be a multiple of 32 (Q8_0 kind) or
+ * 256 (Q8K kind). */
+int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Products on native block bytes against quantized activations.
+ * y[r][o] = sum of the row's blocks (d_w * d_x * int32 dot, minus the q4_K min term) + bias[o] + res[r][o]
+ * bias [n_out] and res [rows][n_out] are nullable device pointers. The weight base must be 16-byte aligned and
+ * row_bytes must equal the type's row size for n (rows are packed). */
+
+/* Decode and small-batch product of `rows` activation rows. Replaces matvec_i8_launch (exec.rs:1996-2039) with the
+ * kernels matvec_i8 / matvec_i8_1 / matvec_i8_1s / mm_i8_{8,16,32} / mm_frag_{8,16,24,32}
+ * (crates/kf-backend-cuda/src/kernels/quant.cuh:604-627, mm_frag.cuh:294-300). */
+int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
+                int rows, int n, int n_out, void* stream);
+
+/* The whole Op::MatMul of one weight: quantize x into `act` (device scratch of kf_hip_act_bytes(rows, n_in)) and run
+ * the product the row count selects. Replaces matmul_launch (exec.rs:2061-2093). */
+int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
+                  const float* res, float* y, void* stream);
+
+/* Per-block int32 results of n_out weight rows against the `rows` activation rows of `act`: q8_0 one int32 per 32-block
+ * (out [n_out][rows][n/32]); q4_K (sumi, mins) per super-block (out [n_out][rows][n/256][2]). The integers of
+ * dot_i8 (crates/kf-quant/src/types/q8_0.rs:10-29, types/q4_k.rs:10-58), computed by the same lane code as the
+ * product kernels. No reference counterpart: it exists so the integer results can be checked bit-exact. */
+int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out, int32_t* out,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Backend mirror (crates/kf-core/src/backend.rs:206-269 Backend; WeightSource :7-13). Host buffers in and out; the
+ * backend owns device copies of its weights (ensure_weight, crates/kf-backend-cuda/src/exec.rs:1347-1359) and a
+ * stream. Not thread-safe per handle (Backend is Send, not Sync). */
+typedef struct kf_hip_backend kf_hip_backend;
+
+/* A backend on HIP device `device`, or NULL (see kf_hip_last_error). */
+kf_hip_backend* kf_hip_backend_new(int device);
+void kf_hip_backend_free(kf_hip_backend* b);
+
+/* Copies one weight tensor to the device. dims[0] = n_in (innermost), dims[1] = n_out, further dims stack matrices
+ * (WeightSource::dims). Returns a weight id >= 0 or a negative status. */
+int kf_hip_backend_add_weight(kf_hip_backend* b, uint32_t ty, const int64_t* dims, int ndims, const void* bytes, size_t nbytes);
+
+/* Op::MatMul{weight, bias} on host rows: y [rows][n_out] = x [rows][cols] times the weight (+ bias [n_out], nullable).
+ * The ops::matmul contract (crates/kf-backend-cpu/src/ops.rs:299-346): cols must equal n_in. Synchronous. */
+int kf_hip_backend_matmul(kf_hip_backend* b, int wid, const float* x, int rows, int cols, const float* bias, float* y);
+
+/* Op::MatMulSlice{weight, index} (ops.rs:304-346 with index): slice `index` of a weight whose third dim stacks matrices */
+int kf_hip_backend_matmul_slice(kf_hip_backend* b, int wid, int index, const float* x, int rows, int cols, float* y);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * Host utilities (CPU).
+ * kf_quantize_q8_0: q8_0::quantize_row (crates/kf-quant/src/types/q8_0.rs:33-42, re-exported at lib.rs:2) over rows.
+ * kf_quantize_q4_k: a q4_K encoder of this library's own. The reference has none (it only reads q4_K); this one fits
+ *   per sub-block an affine min/max, then 6-bit scales and mins against f16 super-block d/dmin, rounding to nearest
+ *   even. Any valid encoder suffices: parity is defined on the bytes.
+ * kf_synth_normal: SplitMix64 (the generator of crates/kf-quant/tests/parity.rs:75-88) feeding Box-Muller pairs,
+ *   sigma * N(0,1) as f32: the synthetic data of the benchmark configs. */
+int kf_quantize_q8_0(const float* x, int64_t rows, int n, uint8_t* dst);
+int kf_quantize_q4_k(const float* x, int64_t rows, int n, uint8_t* dst);
+void kf_synth_normal(uint64_t seed, float sigma, float* out, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

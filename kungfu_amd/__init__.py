@@ -1,0 +1,247 @@
+"""kungfu_amd — MI355X-native (gfx950) quantized linear-layer hot path of kungfu.
+
+The product is the C-ABI library ``kungfu_amd/lib/libkf_hip.so`` (declared in ``include/kf_hip.h``): hand-written HIP
+kernels for the dequant-fused GEMV and the int8 products on GGUF q8_0 / q4_K block bytes, plus a C++ backend object
+mirroring kungfu's ``Backend`` trait for ``Op::MatMul``. This module binds it with ctypes for Python callers (tests and
+the benchmark), passing torch device tensors as plain device pointers. It never falls back to any CPU path: if the
+library is missing, or a call fails, it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "lib", "libkf_hip.so")
+HEADER = os.path.join(ROOT, "include", "kf_hip.h")
+
+TYPE_Q8_0 = 8
+TYPE_Q4_K = 12
+ACT_Q8_0 = 3
+ACT_Q8K = 4
+BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144)}
+
+KF_OK = 0
+KF_E_INVALID = -1
+KF_E_UNSUPPORTED = -2
+KF_E_HIP = -3
+KF_E_NOMEM = -4
+
+_lib = None
+
+
+class KfError(RuntimeError):
+    """A failed kf-hip call: the status code and the library's message."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"kf-hip error {code}: {msg}")
+        self.code = code
+
+
+def build(verbose: bool = False) -> str:
+    from . import _build
+
+    return _build.build(verbose=verbose)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises if it has not been built (the product path has no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    P, I, U, L64, S = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_int64, ctypes.c_size_t
+    sig = {
+        "kf_hip_abi_version": ([], I),
+        "kf_hip_last_error": ([], ctypes.c_char_p),
+        "kf_hip_act_bytes": ([I, I], S),
+        "kf_hip_act_offsets": ([I, I, P], None),
+        "kf_hip_act_kind": ([U], I),
+        "kf_hip_quant_act": ([P, P, I, I, I, P], I),
+        "kf_hip_gemv": ([U, P, L64, P, P, P, P, I, I, I, P], I),
+        "kf_hip_matmul": ([U, P, I, I, P, I, P, P, P, P, P], I),
+        "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
+        "kf_hip_backend_new": ([I], P),
+        "kf_hip_backend_free": ([P], None),
+        "kf_hip_backend_add_weight": ([P, U, P, I, P, S], I),
+        "kf_hip_backend_matmul": ([P, I, P, I, I, P, P], I),
+        "kf_hip_backend_matmul_slice": ([P, I, I, P, I, I, P], I),
+        "kf_quantize_q8_0": ([P, L64, I, P], I),
+        "kf_quantize_q4_k": ([P, L64, I, P], I),
+        "kf_synth_normal": ([ctypes.c_uint64, ctypes.c_float, P, S], None),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+
+
+def declared_symbols() -> list[str]:
+    """Every function include/kf_hip.h declares."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kf_[a-z0-9_]+)\s*\(", text)))
+
+
+def check(rc: int) -> int:
+    if rc < 0:
+        raise KfError(rc, last_error())
+    return rc
+
+
+def last_error() -> str:
+    return lib().kf_hip_last_error().decode()
+
+
+def row_bytes(ty: int, n: int) -> int:
+    block, size = BLOCK[ty]
+    return n // block * size
+
+
+def act_kind(ty: int) -> int:
+    return check(lib().kf_hip_act_kind(ty))
+
+
+def act_bytes(rows: int, n: int) -> int:
+    return lib().kf_hip_act_bytes(rows, n)
+
+
+def act_offsets(rows: int, n: int) -> list[int]:
+    out = (ctypes.c_size_t * 5)()
+    lib().kf_hip_act_offsets(rows, n, out)
+    return list(out)
+
+
+# ------------------------------------------------------------------ host utilities (numpy in, numpy out)
+
+def _np():
+    import numpy as np
+
+    return np
+
+
+def synth_normal(seed: int, sigma: float, n: int):
+    np = _np()
+    out = np.empty(n, np.float32)
+    lib().kf_synth_normal(seed, sigma, out.ctypes.data_as(ctypes.c_void_p), n)
+    return out
+
+
+def quantize(ty: int, x):
+    """Host encoder: q8_0 (quantize_row of the reference) or q4_K (this library's encoder); x [rows][n] f32."""
+    np = _np()
+    x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+    rows, n = x.shape
+    out = np.empty((rows, row_bytes(ty, n)), np.uint8)
+    fn = lib().kf_quantize_q8_0 if ty == TYPE_Q8_0 else lib().kf_quantize_q4_k
+    rc = fn(x.ctypes.data_as(ctypes.c_void_p), rows, n, out.ctypes.data_as(ctypes.c_void_p))
+    if rc != 0:
+        raise KfError(rc, f"quantize type {ty} of {rows}x{n}")
+    return out
+
+
+# ------------------------------------------------------------------ device calls on torch tensors
+
+def _ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(stream) -> int | None:
+    if stream is not None:
+        return stream
+    import torch
+
+    return torch.cuda.current_stream().cuda_stream
+
+
+def quant_act(x, act, kind: int, stream=None) -> None:
+    rows, n = x.shape
+    check(lib().kf_hip_quant_act(_ptr(x), _ptr(act), rows, n, kind, _stream(stream)))
+
+
+def gemv(ty: int, w, act, y, rows: int, n: int, n_out: int, bias=None, res=None, stream=None) -> None:
+    check(lib().kf_hip_gemv(ty, _ptr(w), row_bytes(ty, n), _ptr(act), _ptr(bias), _ptr(res), _ptr(y), rows, n, n_out, _stream(stream)))
+
+
+def matmul(ty: int, w, x, act, y, n_out: int, bias=None, res=None, stream=None) -> None:
+    rows, n = x.shape
+    check(lib().kf_hip_matmul(ty, _ptr(w), n, n_out, _ptr(x), rows, _ptr(act), _ptr(bias), _ptr(res), _ptr(y), _stream(stream)))
+
+
+def block_ints(ty: int, w, act, out, rows: int, n: int, n_out: int, stream=None) -> None:
+    check(lib().kf_hip_block_ints(ty, _ptr(w), row_bytes(ty, n), _ptr(act), rows, n, n_out, _ptr(out), _stream(stream)))
+
+
+def alloc_act(rows: int, n: int, device="cuda"):
+    """A device scratch for quantized activations (uint8 tensor, 256-byte aligned by the caching allocator)."""
+    import torch
+
+    t = torch.empty(act_bytes(rows, n), dtype=torch.uint8, device=device)
+    assert t.data_ptr() % 256 == 0
+    return t
+
+
+def act_views(act, rows: int, n: int):
+    """(q, d16, s16, d32, s32) torch views of a scratch filled by quant_act."""
+    import torch
+
+    o = act_offsets(rows, n)
+    q = act[o[0] : o[0] + rows * n].view(torch.int8).view(rows, n)
+    d16 = act[o[1] : o[1] + rows * (n // 16) * 4].view(torch.float32).view(rows, n // 16)
+    s16 = act[o[2] : o[2] + rows * (n // 16) * 4].view(torch.int32).view(rows, n // 16)
+    d32 = act[o[3] : o[3] + rows * (n // 32) * 4].view(torch.float32).view(rows, n // 32)
+    s32 = act[o[4] : o[4] + rows * (n // 32) * 4].view(torch.int32).view(rows, n // 32)
+    return q, d16, s16, d32, s32
+
+
+class Backend:
+    """The Backend-trait mirror of the library (kf_hip_backend_*): owns device weights, host rows in and out."""
+
+    def __init__(self, device: int = 0):
+        self._h = lib().kf_hip_backend_new(device)
+        if not self._h:
+            raise KfError(KF_E_INVALID, last_error())
+
+    def close(self) -> None:
+        if self._h:
+            lib().kf_hip_backend_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def add_weight(self, ty: int, dims, data) -> int:
+        np = _np()
+        data = np.ascontiguousarray(data, np.uint8)
+        d = (ctypes.c_int64 * len(dims))(*dims)
+        return check(lib().kf_hip_backend_add_weight(self._h, ty, d, len(dims), data.ctypes.data_as(ctypes.c_void_p), data.nbytes))
+
+    def matmul(self, wid: int, x, n_out: int, bias=None):
+        np = _np()
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        rows, cols = x.shape
+        y = np.empty((rows, n_out), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+        check(lib().kf_hip_backend_matmul(self._h, wid, x.ctypes.data_as(ctypes.c_void_p), rows, cols,
+                                          None if b is None else b.ctypes.data_as(ctypes.c_void_p), y.ctypes.data_as(ctypes.c_void_p)))
+        return y
+
+    def matmul_slice(self, wid: int, index: int, x, n_out: int):
+        np = _np()
+        x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
+        rows, cols = x.shape
+        y = np.empty((rows, n_out), np.float32)
+        check(lib().kf_hip_backend_matmul_slice(self._h, wid, index, x.ctypes.data_as(ctypes.c_void_p), rows, cols,
+                                                y.ctypes.data_as(ctypes.c_void_p)))
+        return y

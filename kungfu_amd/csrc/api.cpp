@@ -1,0 +1,308 @@
+// C ABI of kf-hip: argument checks, kernel selection and the backend mirror. Declared in include/kf_hip.h.
+//
+// The selection logic plays the part of the reference's matmul_launch / matvec_i8_launch
+// (crates/kf-backend-cuda/src/exec.rs:1850-2109): quantize the activations with the weight type's kind, then one
+// product kernel chosen by the number of activation rows.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/kf_hip.h"
+#include "kf_layout.h"
+
+// Launchers in the .hip translation units
+hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s);
+hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
+                           const float* bias, const float* res, float* y, int n, int n_out, int blocks_per_cu, hipStream_t s);
+hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
+                                int32_t* out, hipStream_t s);
+int kf_gemv_max_n();
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) { return fail(KF_E_HIP, "%s: %s", what, hipGetErrorString(e)); }
+
+bool type_info(uint32_t ty, int& block, int& bytes) {
+    if (ty == KF_TYPE_Q8_0) {
+        block = KF_Q8_0_BLOCK;
+        bytes = KF_Q8_0_BYTES;
+        return true;
+    }
+    if (ty == KF_TYPE_Q4_K) {
+        block = KF_Q4_K_BLOCK;
+        bytes = KF_Q4_K_BYTES;
+        return true;
+    }
+    return false;
+}
+
+int kind_of(uint32_t ty) { return ty == KF_TYPE_Q8_0 ? KF_ACT_Q8_0 : KF_ACT_Q8K; }
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Blocks per CU of the GEMV grid; KF_GEMV_BPC overrides (tuning knob, like the reference's KF_* env knobs)
+int gemv_bpc() {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("KF_GEMV_BPC");
+        v = e ? atoi(e) : 0;
+        if (v < 0) v = 0;
+    }
+    return v;
+}
+
+int check_product(uint32_t ty, const void* w, int64_t row_bytes, const void* act, float* y, int rows, int n, int n_out) {
+    int block, bytes;
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12)", ty);
+    if (n <= 0 || n % block != 0) return fail(KF_E_INVALID, "%d columns against blocks of %d", n, block);
+    if (rows < 1) return fail(KF_E_INVALID, "%d activation rows", rows);
+    if (n_out < 0) return fail(KF_E_INVALID, "%d output rows", n_out);
+    if (row_bytes != (int64_t)(n / block) * bytes)
+        return fail(KF_E_INVALID, "row_bytes %lld for %d columns of type %u, want %lld", (long long)row_bytes, n, ty,
+                    (long long)(n / block) * bytes);
+    if (!w || !act || !y) return fail(KF_E_INVALID, "null weight, activation or output pointer");
+    if (!aligned(w, 16)) return fail(KF_E_INVALID, "weight base must be 16-byte aligned");
+    if (!aligned(act, KF_ACT_ALIGN)) return fail(KF_E_INVALID, "activation scratch must be %d-byte aligned", KF_ACT_ALIGN);
+    return KF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kf_hip_abi_version(void) { return KF_HIP_ABI_VERSION; }
+
+const char* kf_hip_last_error(void) { return g_err.c_str(); }
+
+size_t kf_hip_act_bytes(int rows, int n) {
+    if (rows < 0 || n < 0) return 0;
+    return kf_act_layout((size_t)rows, (size_t)n).total;
+}
+
+void kf_hip_act_offsets(int rows, int n, size_t out[5]) {
+    const kf_act_offsets o = kf_act_layout((size_t)(rows < 0 ? 0 : rows), (size_t)(n < 0 ? 0 : n));
+    out[0] = o.q;
+    out[1] = o.d16;
+    out[2] = o.s16;
+    out[3] = o.d32;
+    out[4] = o.s32;
+}
+
+int kf_hip_act_kind(uint32_t ty) {
+    int block, bytes;
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path", ty);
+    return kind_of(ty);
+}
+
+int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void* stream) {
+    if (kind != KF_ACT_Q8_0 && kind != KF_ACT_Q8K) return fail(KF_E_UNSUPPORTED, "activation kind %d (3=Q8_0, 4=Q8K)", kind);
+    const int block = kind == KF_ACT_Q8_0 ? 32 : 256;
+    if (rows < 1 || n <= 0 || n % block != 0) return fail(KF_E_INVALID, "%d rows of %d columns for blocks of %d", rows, n, block);
+    if (!x || !act) return fail(KF_E_INVALID, "null activation pointer");
+    if (!aligned(x, 16) || !aligned(act, KF_ACT_ALIGN)) return fail(KF_E_INVALID, "x must be 16-byte and act 256-byte aligned");
+    const hipError_t e = kf_launch_quant_act(x, act, rows, n, kind, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "quant_act launch");
+}
+
+int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int rows,
+                int n, int n_out, void* stream) {
+    const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
+    if (rc != KF_OK) return rc;
+    if (n > kf_gemv_max_n()) return fail(KF_E_UNSUPPORTED, "%d columns above the %d the GEMV stages in LDS", n, kf_gemv_max_n());
+    const kf_act_offsets o = kf_act_layout((size_t)rows, (size_t)n);
+    const char* base = static_cast<const char*>(act);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int r = 0; r < rows; r++) {
+        const int8_t* xq = reinterpret_cast<const int8_t*>(base + o.q) + (size_t)r * n;
+        const int32_t* xs32 = reinterpret_cast<const int32_t*>(base + o.s32) + (size_t)r * (n / 32);
+        const float* xd32 = reinterpret_cast<const float*>(base + o.d32) + (size_t)r * (n / 32);
+        const hipError_t e = kf_launch_gemv1(ty, w, row_bytes, xq, xs32, xd32, bias, res ? res + (size_t)r * n_out : nullptr,
+                                             y + (size_t)r * n_out, n, n_out, gemv_bpc(), s);
+        if (e != hipSuccess) return hip_fail(e, "gemv launch");
+    }
+    return KF_OK;
+}
+
+int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
+                  const float* res, float* y, void* stream) {
+    int block, bytes;
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12)", ty);
+    if (n_in <= 0 || n_in % block != 0) return fail(KF_E_INVALID, "%d columns against blocks of %d", n_in, block);
+    const int64_t rb = (int64_t)(n_in / block) * bytes;
+    const int rc = check_product(ty, w, rb, act, y, rows, n_in, n_out);
+    if (rc != KF_OK) return rc;
+    const int q = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
+    if (q != KF_OK) return q;
+    return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+}
+
+int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out, int32_t* out,
+                      void* stream) {
+    const int rc = check_product(ty, w, row_bytes, act, reinterpret_cast<float*>(out), rows, n, n_out);
+    if (rc != KF_OK) return rc;
+    const hipError_t e = kf_launch_block_ints(ty, w, row_bytes, act, rows, n, n_out, out, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "block_ints launch");
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------ backend mirror
+
+struct kf_hip_weight {
+    uint32_t ty;
+    std::vector<int64_t> dims;
+    void* dev;
+    size_t nbytes;
+};
+
+struct kf_hip_backend {
+    int device;
+    hipStream_t stream;
+    std::vector<kf_hip_weight> weights;
+    void* scratch = nullptr;  // x | act | y, grown on demand (the per-graph pool of exec.rs:603-711, reduced to one op)
+    size_t scratch_bytes = 0;
+};
+
+namespace {
+
+int ensure_scratch(kf_hip_backend* b, size_t need) {
+    if (need <= b->scratch_bytes) return KF_OK;
+    if (b->scratch) hipFree(b->scratch);
+    b->scratch = nullptr;
+    b->scratch_bytes = 0;
+    const hipError_t e = hipMalloc(&b->scratch, need);
+    if (e != hipSuccess) return fail(KF_E_NOMEM, "scratch of %zu bytes: %s", need, hipGetErrorString(e));
+    b->scratch_bytes = need;
+    return KF_OK;
+}
+
+int backend_matmul(kf_hip_backend* b, int wid, int index, const float* x, int rows, int cols, const float* bias, float* y) {
+    if (!b) return fail(KF_E_INVALID, "null backend");
+    if (wid < 0 || wid >= (int)b->weights.size()) return fail(KF_E_INVALID, "weight id %d of %zu", wid, b->weights.size());
+    const kf_hip_weight& w = b->weights[wid];
+    const int64_t n_in = w.dims[0];
+    const int64_t n_out = w.dims.size() > 1 ? w.dims[1] : 1;
+    int64_t n_slices = 1;
+    for (size_t i = 2; i < w.dims.size(); i++) n_slices *= w.dims[i];
+    if (cols != n_in) return fail(KF_E_INVALID, "%d columns against %lld inputs", cols, (long long)n_in);
+    if (index < 0 || index >= n_slices) return fail(KF_E_INVALID, "slice %d of %lld", index, (long long)n_slices);
+    if (rows < 0 || (rows > 0 && (!x || !y))) return fail(KF_E_INVALID, "null rows");
+    if (rows == 0 || n_out == 0) return KF_OK;
+    int block, bytes;
+    type_info(w.ty, block, bytes);
+    const int64_t rb = n_in / block * bytes;
+    const size_t xb = kf_align_up(sizeof(float) * (size_t)rows * n_in, 256);
+    const size_t ab = kf_act_layout((size_t)rows, (size_t)n_in).total;
+    const size_t yb = kf_align_up(sizeof(float) * (size_t)rows * n_out, 256);
+    const size_t bb = bias ? kf_align_up(sizeof(float) * (size_t)n_out, 256) : 0;
+    int rc = ensure_scratch(b, xb + ab + yb + bb);
+    if (rc != KF_OK) return rc;
+    char* base = static_cast<char*>(b->scratch);
+    float* dx = reinterpret_cast<float*>(base);
+    void* act = base + xb;
+    float* dy = reinterpret_cast<float*>(base + xb + ab);
+    float* dbias = bias ? reinterpret_cast<float*>(base + xb + ab + yb) : nullptr;
+    hipError_t e = hipMemcpyAsync(dx, x, sizeof(float) * (size_t)rows * n_in, hipMemcpyHostToDevice, b->stream);
+    if (e == hipSuccess && bias) e = hipMemcpyAsync(dbias, bias, sizeof(float) * (size_t)n_out, hipMemcpyHostToDevice, b->stream);
+    if (e != hipSuccess) return hip_fail(e, "copy of the input rows");
+    const char* wslice = static_cast<const char*>(w.dev) + (size_t)index * n_out * rb;
+    rc = kf_hip_matmul(w.ty, wslice, (int)n_in, (int)n_out, dx, rows, act, dbias, nullptr, dy, b->stream);
+    if (rc != KF_OK) return rc;
+    e = hipMemcpyAsync(y, dy, sizeof(float) * (size_t)rows * n_out, hipMemcpyDeviceToHost, b->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(b->stream);
+    return e == hipSuccess ? KF_OK : hip_fail(e, "matmul");
+}
+
+}  // namespace
+
+extern "C" {
+
+kf_hip_backend* kf_hip_backend_new(int device) {
+    int count = 0;
+    hipError_t e = hipGetDeviceCount(&count);
+    if (e != hipSuccess || device < 0 || device >= count) {
+        fail(KF_E_INVALID, "device %d of %d", device, count);
+        return nullptr;
+    }
+    e = hipSetDevice(device);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipSetDevice");
+        return nullptr;
+    }
+    hipStream_t s;
+    e = hipStreamCreateWithFlags(&s, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        hip_fail(e, "hipStreamCreate");
+        return nullptr;
+    }
+    kf_hip_backend* b = new kf_hip_backend;
+    b->device = device;
+    b->stream = s;
+    return b;
+}
+
+void kf_hip_backend_free(kf_hip_backend* b) {
+    if (!b) return;
+    hipSetDevice(b->device);
+    hipStreamSynchronize(b->stream);
+    for (auto& w : b->weights) hipFree(w.dev);
+    if (b->scratch) hipFree(b->scratch);
+    hipStreamDestroy(b->stream);
+    delete b;
+}
+
+int kf_hip_backend_add_weight(kf_hip_backend* b, uint32_t ty, const int64_t* dims, int ndims, const void* bytes, size_t nbytes) {
+    if (!b) return fail(KF_E_INVALID, "null backend");
+    int block, bsz;
+    if (!type_info(ty, block, bsz)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path", ty);
+    if (!dims || ndims < 1 || !bytes) return fail(KF_E_INVALID, "null dims or bytes");
+    int64_t rows = 1;
+    for (int i = 1; i < ndims; i++) {
+        if (dims[i] < 0) return fail(KF_E_INVALID, "negative dim");
+        rows *= dims[i];
+    }
+    if (dims[0] <= 0 || dims[0] % block != 0) return fail(KF_E_INVALID, "%lld columns against blocks of %d", (long long)dims[0], block);
+    const size_t want = (size_t)(dims[0] / block) * bsz * (size_t)rows;
+    if (nbytes != want) return fail(KF_E_INVALID, "%zu bytes for a tensor of %zu", nbytes, want);
+    hipSetDevice(b->device);
+    void* dev = nullptr;
+    // 16 spare bytes past the tensor, as the reference's ensure_weight keeps (exec.rs:1347-1359)
+    hipError_t e = hipMalloc(&dev, nbytes + 16);
+    if (e != hipSuccess) return fail(KF_E_NOMEM, "weight of %zu bytes: %s", nbytes, hipGetErrorString(e));
+    e = hipMemcpy(dev, bytes, nbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(static_cast<char*>(dev) + nbytes, 0, 16);
+    if (e != hipSuccess) {
+        hipFree(dev);
+        return hip_fail(e, "weight upload");
+    }
+    b->weights.push_back(kf_hip_weight{ty, std::vector<int64_t>(dims, dims + ndims), dev, nbytes});
+    return (int)b->weights.size() - 1;
+}
+
+int kf_hip_backend_matmul(kf_hip_backend* b, int wid, const float* x, int rows, int cols, const float* bias, float* y) {
+    if (b) hipSetDevice(b->device);
+    return backend_matmul(b, wid, 0, x, rows, cols, bias, y);
+}
+
+int kf_hip_backend_matmul_slice(kf_hip_backend* b, int wid, int index, const float* x, int rows, int cols, float* y) {
+    if (b) hipSetDevice(b->device);
+    return backend_matmul(b, wid, index, x, rows, cols, nullptr, y);
+}
+
+}  // extern "C"

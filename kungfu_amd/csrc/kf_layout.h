@@ -1,0 +1,48 @@
+// Block layouts and the int8 activation scratch layout, shared by host and device code.
+//
+// GGUF block layouts consumed unchanged (crates/kf-quant/src/types/q8_0.rs:4, types/q4_k.rs:4):
+//   q8_0: 32 elements in 34 bytes, f16 d then 32 x int8
+//   q4_K: 256 elements in 144 bytes, f16 d, f16 dmin, 12 bytes of packed 6-bit scales and mins for 8 sub-blocks of
+//         32, then 128 bytes of nibbles; pair j of sub-blocks (2j, 2j+1) lives in bytes 16+32j..48+32j, the low
+//         nibble of byte 16+32j+l being element 64j+l and the high nibble element 64j+32+l.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#define KF_TYPE_Q8_0 8u
+#define KF_TYPE_Q4_K 12u
+
+#define KF_ACT_Q8_0 3
+#define KF_ACT_Q8K 4
+
+#define KF_Q8_0_BLOCK 32
+#define KF_Q8_0_BYTES 34
+#define KF_Q4_K_BLOCK 256
+#define KF_Q4_K_BYTES 144
+
+// Alignment of every section of the activation scratch
+#define KF_ACT_ALIGN 256
+
+static inline size_t kf_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// The int8 activation scratch of `rows` rows of `n` columns: the reference's ActI8 (crates/kf-quant/src/lib.rs:48-78)
+// plus per-32 copies of the scale and sum, each section KF_ACT_ALIGN aligned:
+//   q    int8  [rows][n]
+//   d16  f32   [rows][n/16]   scale of every 16 columns
+//   s16  int32 [rows][n/16]   integer sum of every 16 columns
+//   d32  f32   [rows][n/32]   scale of every 32 columns
+//   s32  int32 [rows][n/32]   integer sum of every 32 columns
+struct kf_act_offsets {
+    size_t q, d16, s16, d32, s32, total;
+};
+
+static inline struct kf_act_offsets kf_act_layout(size_t rows, size_t n) {
+    struct kf_act_offsets o;
+    o.q = 0;
+    o.d16 = kf_align_up(o.q + rows * n, KF_ACT_ALIGN);
+    o.s16 = kf_align_up(o.d16 + rows * (n / 16) * 4, KF_ACT_ALIGN);
+    o.d32 = kf_align_up(o.s16 + rows * (n / 16) * 4, KF_ACT_ALIGN);
+    o.s32 = kf_align_up(o.d32 + rows * (n / 32) * 4, KF_ACT_ALIGN);
+    o.total = kf_align_up(o.s32 + rows * (n / 32) * 4, KF_ACT_ALIGN);
+    return o;
+}

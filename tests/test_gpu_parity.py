@@ -1,0 +1,206 @@
+"""GPU parity of the HIP path against the CPU oracle, called through the C ABI on the same seeded inputs.
+
+Bar (from the north star): per-block int32 results bit-exact; fp32 outputs within |got - want| <= 1e-4 + 1e-3 * |want|
+of kf-backend-cpu's matmul_slice (crates/kf-backend-cpu/src/ops.rs:304-346); the quantized activations bit-exact with
+quantize_activations (crates/kf-quant/src/lib.rs:81-140). Shapes follow the reference's differential tests
+(crates/kf-backend-cuda/tests/quant.rs:46-83: ragged n_out, several widths) plus the full Llama-3-8B shapes.
+"""
+import numpy as np
+import pytest
+
+import kungfu_amd as kf
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-3, 1e-4
+
+
+def _tensor(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _weights(ty, n_out, n_in, seed):
+    w = kf.synth_normal(seed, 0.02, n_out * n_in).reshape(n_out, n_in)
+    return kf.quantize(ty, w)
+
+
+def _close(got, want):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bad = err > ATOL + RTOL * np.abs(want)
+    assert not bad.any(), f"{bad.sum()} outputs off, worst {err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}"
+
+
+@pytest.mark.parametrize("kind", [kf.ACT_Q8_0, kf.ACT_Q8K])
+@pytest.mark.parametrize("rows,n", [(1, 256), (3, 4096), (2, 14336), (5, 1024)])
+def test_quant_act_bit_exact(cuda, kind, rows, n):
+    import torch
+
+    rng = np.random.default_rng(rows * 100 + n + kind)
+    x = (rng.standard_normal((rows, n)) * rng.uniform(1e-3, 50, (rows, 1))).astype(np.float32)
+    x[0, :256] = 0.0                       # an all-zero block
+    x[-1, 256:288] = 2.5                   # ties inside a block
+    x[-1, 300] = -x[-1, 256:512].__abs__().max()  # a negative maximum late in the block
+    if n >= 1024:
+        x[0, 512 + 7] = 9.0
+        x[0, 512 + 100] = -9.0             # equal magnitudes: the first index sets the sign of the scale
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kind)
+    torch.cuda.synchronize()
+    q, d16, s16, d32, s32 = [t.cpu().numpy() for t in kf.act_views(act, rows, n)]
+    wq, wd, ws = oracle.quantize_activations(kind, x)
+    assert np.array_equal(q, wq)
+    assert np.array_equal(d16.view(np.uint32), wd.view(np.uint32))
+    assert np.array_equal(s16, ws)
+    assert np.array_equal(d32.view(np.uint32), wd[:, ::2].view(np.uint32))
+    assert np.array_equal(s32, ws[:, ::2] + ws[:, 1::2])
+
+
+def _random_blocks(ty, n_out, n_in, rng):
+    """Random block bytes with sane f16 scales (the harness of crates/kf-backend-cuda/tests/common/mod.rs:100-147)."""
+    block, size = kf.BLOCK[ty]
+    w = rng.integers(0, 256, (n_out, n_in // block, size), dtype=np.uint8)
+    bits = (((5 + rng.integers(0, 8, w.shape[:2])) << 10) | rng.integers(0, 1024, w.shape[:2])).astype(np.uint16)
+    w[:, :, 0:2] = bits.view(np.uint8).reshape(w.shape[0], w.shape[1], 2)
+    if ty == kf.TYPE_Q4_K:
+        bits = (((5 + rng.integers(0, 8, w.shape[:2])) << 10) | rng.integers(0, 1024, w.shape[:2])).astype(np.uint16)
+        w[:, :, 2:4] = bits.view(np.uint8).reshape(w.shape[0], w.shape[1], 2)
+    return w.reshape(n_out, -1)
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q8_0, kf.TYPE_Q4_K])
+@pytest.mark.parametrize("rows,n,n_out", [(1, 256, 5), (2, 1024, 7), (3, 4096, 3)])
+def test_block_ints_bit_exact(cuda, ty, rows, n, n_out):
+    import torch
+
+    rng = np.random.default_rng(n + n_out + ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.act_kind(ty))
+    per = n // 32 if ty == kf.TYPE_Q8_0 else 2 * (n // 256)
+    out = torch.zeros(n_out * rows * per, dtype=torch.int32, device=cuda)
+    kf.block_ints(ty, _tensor(w, cuda), act, out, rows, n, n_out)
+    got = out.cpu().numpy().reshape(n_out, rows, per)
+    q, _, s16 = oracle.quantize_activations(kf.act_kind(ty), x)
+    for o in range(n_out):
+        for r in range(rows):
+            assert np.array_equal(got[o, r], oracle.block_ints(ty, w[o], q[r], s16[r])), (o, r)
+
+
+GEMV_SHAPES = [
+    (kf.TYPE_Q4_K, 256, 1),
+    (kf.TYPE_Q4_K, 256, 13),
+    (kf.TYPE_Q4_K, 1024, 77),
+    (kf.TYPE_Q4_K, 2304, 33),      # 9 super-blocks: a ragged wave step
+    (kf.TYPE_Q4_K, 4096, 520),
+    (kf.TYPE_Q4_K, 14336, 300),
+    (kf.TYPE_Q4_K, 32768, 40),     # the widest row the GEMV stages
+    (kf.TYPE_Q8_0, 32, 3),
+    (kf.TYPE_Q8_0, 96, 11),        # odd block count: rows start 2 bytes into a dword
+    (kf.TYPE_Q8_0, 2080, 17),
+    (kf.TYPE_Q8_0, 4096, 515),
+    (kf.TYPE_Q8_0, 14336, 64),
+    (kf.TYPE_Q8_0, 32768, 9),
+]
+
+
+@pytest.mark.parametrize("ty,n,n_out", GEMV_SHAPES)
+def test_gemv_matches_cpu_backend(cuda, ty, n, n_out):
+    import torch
+
+    w = _weights(ty, n_out, n, seed=n + n_out)
+    x = kf.synth_normal(7 + n, 1.0, n).reshape(1, n)
+    wd = _tensor(w, cuda)
+    xd = _tensor(x, cuda)
+    act = kf.alloc_act(1, n, cuda)
+    y = torch.full((1, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, wd, xd, act, y, n_out)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    _close(got, oracle.matmul_slice(ty, w, n, n_out, x))
+    # against the integer CPU path the only difference left is the order of float additions
+    yi = oracle.matmul_i8(ty, w, n, n_out, x)
+    assert np.abs(got - yi).max() <= 2e-5 * max(1.0, np.abs(yi).max())
+
+
+LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 14336), (14336, 4096)]
+
+
+@pytest.mark.parametrize("n,n_out", LLAMA_SHAPES)
+def test_gemv_q4_k_llama_shapes(cuda, n, n_out):
+    import torch
+
+    w = _weights(kf.TYPE_Q4_K, n_out, n, seed=0)
+    x = kf.synth_normal(1, 1.0, n).reshape(1, n)
+    act = kf.alloc_act(1, n, cuda)
+    y = torch.empty((1, n_out), device=cuda)
+    kf.matmul(kf.TYPE_Q4_K, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x))
+
+
+def test_gemv_q8_0_config_c1(cuda):
+    import torch
+
+    n = n_out = 4096
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=0)
+    x = kf.synth_normal(1, 1.0, n).reshape(1, n)
+    act = kf.alloc_act(1, n, cuda)
+    y = torch.empty((1, n_out), device=cuda)
+    kf.matmul(kf.TYPE_Q8_0, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x))
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q8_0, kf.TYPE_Q4_K])
+def test_gemv_bias_and_residual(cuda, ty):
+    import torch
+
+    n, n_out = 1024, 96
+    w = _weights(ty, n_out, n, seed=3)
+    x = kf.synth_normal(4, 1.0, n).reshape(1, n)
+    bias = kf.synth_normal(5, 1.0, n_out)
+    res = kf.synth_normal(6, 1.0, n_out).reshape(1, n_out)
+    act = kf.alloc_act(1, n, cuda)
+    y = torch.empty((1, n_out), device=cuda)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x, bias) + res)
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q8_0, kf.TYPE_Q4_K])
+@pytest.mark.parametrize("rows", [2, 3, 8])
+def test_multi_row_matches_cpu_backend(cuda, ty, rows):
+    import torch
+
+    n, n_out = 2048, 130
+    w = _weights(ty, n_out, n, seed=rows)
+    x = kf.synth_normal(10 + rows, 1.0, rows * n).reshape(rows, n)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.empty((rows, n_out), device=cuda)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+def test_backend_mirror_matmul_and_slices(cuda):
+    n, n_out, n_slices = 512, 48, 3
+    w = _weights(kf.TYPE_Q4_K, n_out * n_slices, n, seed=21)
+    x = kf.synth_normal(22, 1.0, 2 * n).reshape(2, n)
+    bias = kf.synth_normal(23, 1.0, n_out)
+    be = kf.Backend(0)
+    try:
+        wid = be.add_weight(kf.TYPE_Q4_K, [n, n_out, n_slices], w)
+        _close(be.matmul(wid, x, n_out, bias), oracle.matmul_slice(kf.TYPE_Q4_K, w[:n_out], n, n_out, x, bias))
+        for s in range(n_slices):
+            got = be.matmul_slice(wid, s, x, n_out)
+            _close(got, oracle.matmul_slice(kf.TYPE_Q4_K, w[s * n_out : (s + 1) * n_out], n, n_out, x))
+        with pytest.raises(kf.KfError, match="columns against"):
+            be.matmul(wid, x[:, :256], n_out)
+        with pytest.raises(kf.KfError, match="slice 3 of 3"):
+            be.matmul_slice(wid, 3, x, n_out)
+    finally:
+        be.close()

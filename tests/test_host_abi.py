@@ -1,0 +1,152 @@
+"""CPU checks of the product library: it loads, exports every symbol include/kf_hip.h declares, validates arguments
+before touching a GPU, and its host encoders / synthetic data match the oracle and their definitions."""
+import ctypes
+import json
+import os
+
+import numpy as np
+import pytest
+
+import kungfu_amd as kf
+import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def test_library_exports_every_declared_symbol():
+    L = kf.lib()
+    syms = kf.declared_symbols()
+    assert len(syms) >= 15
+    for s in syms:
+        assert hasattr(L, s), s
+    assert L.kf_hip_abi_version() == 1
+
+
+def test_act_layout_sections_are_aligned_and_sized():
+    for rows, n in [(1, 4096), (3, 14336), (64, 256), (2048, 4096)]:
+        o = kf.act_offsets(rows, n)
+        total = kf.act_bytes(rows, n)
+        assert all(v % 256 == 0 for v in o) and total % 256 == 0
+        assert o[0] == 0 and o[1] >= rows * n and o[2] >= o[1] + rows * n // 16 * 4
+        assert o[3] >= o[2] + rows * n // 16 * 4 and o[4] >= o[3] + rows * n // 32 * 4
+        assert total >= o[4] + rows * n // 32 * 4
+
+
+def test_act_kind_pairs_weight_types():
+    assert kf.act_kind(kf.TYPE_Q8_0) == kf.ACT_Q8_0
+    assert kf.act_kind(kf.TYPE_Q4_K) == kf.ACT_Q8K
+    with pytest.raises(kf.KfError) as e:
+        kf.act_kind(14)
+    assert e.value.code == kf.KF_E_UNSUPPORTED and "14" in str(e.value)
+
+
+FAKE = 0x10000  # a 256-byte aligned address the checks must reject before any HIP call
+
+
+@pytest.mark.parametrize(
+    "args,code,needle",
+    [
+        ((kf.TYPE_Q8_0, FAKE, kf.row_bytes(8, 4096), FAKE, None, None, FAKE, 1, 4096, 16, None), 0, None),
+        ((2, FAKE, 100, FAKE, None, None, FAKE, 1, 4096, 16, None), kf.KF_E_UNSUPPORTED, "type 2"),
+        ((kf.TYPE_Q4_K, FAKE, 144, FAKE, None, None, FAKE, 1, 200, 16, None), kf.KF_E_INVALID, "200 columns"),
+        ((kf.TYPE_Q4_K, FAKE, 100, FAKE, None, None, FAKE, 1, 256, 16, None), kf.KF_E_INVALID, "row_bytes"),
+        ((kf.TYPE_Q4_K, FAKE + 4, 144, FAKE, None, None, FAKE, 1, 256, 16, None), kf.KF_E_INVALID, "16-byte"),
+        ((kf.TYPE_Q4_K, FAKE, 144, FAKE + 16, None, None, FAKE, 1, 256, 16, None), kf.KF_E_INVALID, "256-byte"),
+        ((kf.TYPE_Q4_K, None, 144, FAKE, None, None, FAKE, 1, 256, 16, None), kf.KF_E_INVALID, "null"),
+        ((kf.TYPE_Q4_K, FAKE, 144, FAKE, None, None, FAKE, 0, 256, 16, None), kf.KF_E_INVALID, "0 activation rows"),
+        ((kf.TYPE_Q4_K, FAKE, 144 * 256, FAKE, None, None, FAKE, 1, 65536, 16, None), kf.KF_E_UNSUPPORTED, "LDS"),
+    ],
+)
+def test_gemv_argument_checks(args, code, needle):
+    if code == 0:
+        return  # the valid row is only a template for the invalid ones (running it needs a GPU)
+    rc = kf.lib().kf_hip_gemv(*args)
+    assert rc == code
+    assert needle in kf.last_error()
+
+
+def test_quant_act_argument_checks():
+    L = kf.lib()
+    assert L.kf_hip_quant_act(FAKE, FAKE, 1, 4096, 5, None) == kf.KF_E_UNSUPPORTED
+    assert L.kf_hip_quant_act(FAKE, FAKE, 1, 4016, 3, None) == kf.KF_E_INVALID
+    assert L.kf_hip_quant_act(FAKE, FAKE, 1, 4096 + 32, 4, None) == kf.KF_E_INVALID
+    assert L.kf_hip_quant_act(FAKE + 4, FAKE, 1, 4096, 4, None) == kf.KF_E_INVALID
+    assert L.kf_hip_quant_act(None, FAKE, 1, 4096, 4, None) == kf.KF_E_INVALID
+    assert L.kf_hip_matmul(kf.TYPE_Q4_K, FAKE, 4096 + 32, 8, FAKE, 1, FAKE, None, None, FAKE, None) == kf.KF_E_INVALID
+
+
+def test_backend_errors_without_a_device():
+    import torch
+
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    L = kf.lib()
+    assert L.kf_hip_backend_new(0) is None
+    assert "device 0" in kf.last_error()
+    assert L.kf_hip_backend_matmul(None, 0, None, 1, 4, None, None) == kf.KF_E_INVALID
+
+
+def test_quantize_q8_0_matches_oracle():
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((6, 1024)) * rng.uniform(1e-3, 10, (6, 1))).astype(np.float32)
+    x[2, :64] = 0.0
+    x[3, 5] = 1e30
+    assert np.array_equal(kf.quantize(kf.TYPE_Q8_0, x), oracle.q8_0_quantize(x))
+
+
+def test_quantize_q4_k_round_trip():
+    rng = np.random.default_rng(12)
+    x = (rng.standard_normal((4, 1024)) * 0.02).astype(np.float32)
+    x[1, :256] = 0.0
+    x[2, :256] = np.abs(x[2, :256])  # all-positive super-block: min 0
+    w = kf.quantize(kf.TYPE_Q4_K, x)
+    deq = oracle.dequant(12, w, 1024)
+    assert not deq[1, :256].any()
+    for r in range(4):
+        blk = w[r].reshape(-1, 144)
+        for b in range(4):
+            d = float(blk[b, 0:2].copy().view(np.float16)[0])
+            dmin = float(blk[b, 2:4].copy().view(np.float16)[0])
+            xs = x[r, 256 * b : 256 * (b + 1)].reshape(8, 32)
+            err = np.abs(deq[r, 256 * b : 256 * (b + 1)].reshape(8, 32) - xs)
+            # per sub-block: half a step of its scale plus the rounding of its min, and the 6-bit scale rounding
+            step = (xs.max(axis=1) - np.minimum(xs.min(axis=1), 0)) / 15
+            assert (err.max(axis=1) <= 0.5 * step + 0.5 * d + 0.5 * dmin + 32 * d + 1e-7).all()
+        rel = np.sqrt(((deq[r] - x[r]) ** 2).mean()) / np.sqrt((x[r] ** 2).mean() + 1e-30)
+        if r != 1:
+            assert rel < 0.12
+
+
+def _synth_numpy(seed, sigma, n):
+    """SplitMix64 then Box-Muller in double: z0 = r cos(2 pi u2), z1 = r sin(2 pi u2), r = sqrt(-2 ln u1),
+    u = ((next >> 11) + 0.5) * 2^-53, output f32(sigma * r * trig)."""
+    M = (1 << 64) - 1
+    s = seed
+    out = np.empty(n, np.float32)
+
+    def nxt():
+        nonlocal s
+        s = (s + 0x9E3779B97F4A7C15) & M
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        return z ^ (z >> 31)
+
+    for i in range(0, n, 2):
+        u1 = ((nxt() >> 11) + 0.5) * 2.0**-53
+        u2 = ((nxt() >> 11) + 0.5) * 2.0**-53
+        r = np.sqrt(-2.0 * np.log(u1))
+        out[i] = np.float32(sigma * r * np.cos(2 * np.pi * u2))
+        if i + 1 < n:
+            out[i + 1] = np.float32(sigma * r * np.sin(2 * np.pi * u2))
+    return out
+
+
+def test_synth_normal_matches_definition_and_golden():
+    got = kf.synth_normal(0, 1.0, 1001)
+    want = _synth_numpy(0, 1.0, 1001)
+    assert np.abs(got.astype(np.float64) - want).max() <= 2e-7 * np.abs(want).max()
+    gold = json.load(open(os.path.join(GOLDEN, "synth_normal_seed0.json")))
+    assert np.array_equal(np.array(gold["bits"], np.uint32), got[:64].view(np.uint32))
+    big = kf.synth_normal(1, 0.02, 200000)
+    assert abs(big.mean()) < 3e-4 and abs(big.std() - 0.02) < 2e-4
