@@ -69,21 +69,42 @@ class Shape:
         kf.matmul(self.ty, self.w[i % len(self.w)], self.x, self.act, self.y, self.n_out)
 
 
-def time_launches(fn, iters, warm=3):
-    """Mean µs per call of fn(i) over iters back-to-back calls, bracketed by HIP events on the launch stream."""
+def capture(fn, count):
+    """A HIP graph of count back-to-back calls fn(0..count-1): replays launch the kernels without host overhead."""
     import torch
 
-    for i in range(warm):
-        fn(i)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn(0)
+    torch.cuda.current_stream().wait_stream(side)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(count):
+            fn(i)
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, replays):
+    """Mean ms per replay of graph g, bracketed by HIP events on the stream the replays run on."""
+    import torch
+
+    g.replay()
+    torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
     e0.record(s)
-    for i in range(iters):
-        fn(i)
+    for _ in range(replays):
+        g.replay()
     e1.record(s)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / iters
+    return e0.elapsed_time(e1) / replays
+
+
+def time_launches(fn, iters):
+    """Mean µs per call of fn(i) over iters back-to-back calls captured in one HIP graph."""
+    return time_graph(capture(fn, iters), 3) * 1e3 / iters
 
 
 def cpu_baseline(shapes, budget_s):
@@ -134,17 +155,22 @@ def main():
         for s in shapes:
             s.gemv(i)
 
-    for i in range(args.warmup):
-        step(i)
+    # one graph holds GSTEP steps; the timed region replays it steps/GSTEP times after warmup replays
+    gstep = 10
+    steps = max(gstep, args.steps // gstep * gstep)
+    g = capture(step, gstep)
+    for _ in range(max(1, args.warmup // gstep)):
+        g.replay()
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
-    for i in range(args.steps):
-        step(i)
+    for _ in range(steps // gstep):
+        g.replay()
     e1.record(s)
     torch.cuda.synchronize()
-    ms_step = e0.elapsed_time(e1) / args.steps
+    ms_step = e0.elapsed_time(e1) / steps
+    args.steps = steps
     value = step_bytes / (ms_step * 1e-3) / 1e9
 
     # per-shape µs/call of the GEMV kernel alone and of the whole matmul (quant_act + GEMV)

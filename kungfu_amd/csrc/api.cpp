@@ -17,7 +17,7 @@
 // Launchers in the .hip translation units
 hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s);
 hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
-                           const float* bias, const float* res, float* y, int n, int n_out, int blocks_per_cu, hipStream_t s);
+                           const float* bias, const float* res, float* y, int n, int n_out, int maxit, hipStream_t s);
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
                                 int32_t* out, hipStream_t s);
 int kf_gemv_max_n();
@@ -56,15 +56,12 @@ int kind_of(uint32_t ty) { return ty == KF_TYPE_Q8_0 ? KF_ACT_Q8_0 : KF_ACT_Q8K;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Blocks per CU of the GEMV grid; KF_GEMV_BPC overrides (tuning knob, like the reference's KF_* env knobs)
-int gemv_bpc() {
-    static int v = -1;
-    if (v < 0) {
-        const char* e = getenv("KF_GEMV_BPC");
-        v = e ? atoi(e) : 0;
-        if (v < 0) v = 0;
-    }
-    return v;
+// Row iterations per GEMV block (1, 2 or 4); KF_GEMV_MAXIT overrides the built-in choice (a tuning knob, like the
+// reference's KF_* environment knobs)
+int gemv_maxit() {
+    const char* e = getenv("KF_GEMV_MAXIT");
+    const int v = e ? atoi(e) : 0;
+    return v < 0 ? 0 : v;
 }
 
 int check_product(uint32_t ty, const void* w, int64_t row_bytes, const void* act, float* y, int rows, int n, int n_out) {
@@ -133,7 +130,7 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
         const int32_t* xs32 = reinterpret_cast<const int32_t*>(base + o.s32) + (size_t)r * (n / 32);
         const float* xd32 = reinterpret_cast<const float*>(base + o.d32) + (size_t)r * (n / 32);
         const hipError_t e = kf_launch_gemv1(ty, w, row_bytes, xq, xs32, xd32, bias, res ? res + (size_t)r * n_out : nullptr,
-                                             y + (size_t)r * n_out, n, n_out, gemv_bpc(), s);
+                                             y + (size_t)r * n_out, n, n_out, gemv_maxit(), s);
         if (e != hipSuccess) return hip_fail(e, "gemv launch");
     }
     return KF_OK;

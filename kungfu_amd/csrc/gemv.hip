@@ -14,122 +14,433 @@
 //   * q8_0: one lane owns one 34-byte block read as a 2-byte-skewed dword window and realigned with v_perm_b32; a wave
 //     step covers 64 consecutive blocks = 2176 contiguous bytes.
 //   * Integer dots use v_dot4_i32_i8; the per-block float combine happens per lane; one wave reduction per row.
+#include <type_traits>
+
 #include "kf_blocks.h"
 
 namespace {
 
-constexpr int GV_THREADS = 512;
+#ifndef KF_GV_THREADS
+#define KF_GV_THREADS 512
+#endif
+// ablation builds for roofline evidence (0 = the product). Bits: 1 skips the activation staging, 2 replaces the
+// arithmetic by a XOR of the parked bytes, 4 skips parking the weights in LDS (2 and 4 give wrong results by design)
+#ifndef KF_GV_ABLATE
+#define KF_GV_ABLATE 0
+#endif
+// row iterations a block holds in flight at once (1, 2 or 4)
+#ifndef KF_GV_MAXIT
+#define KF_GV_MAXIT 2
+#endif
+
+constexpr int GV_THREADS = KF_GV_THREADS;
 constexpr int GV_WAVES = GV_THREADS / 64;
 
-// LDS bytes of the staged activation row of n columns for either kind
-__host__ __device__ constexpr size_t gv_smem(int n) { return (size_t)n + (size_t)(n / 32) * 4 + (size_t)(n / 32) * 4; }
+// Shape of one launch, computed on the host: S wave steps per row, WPR waves per row (each taking steps sp, sp+WPR,
+// ...), RPB = GV_WAVES / WPR rows per block iteration, `iters` block iterations. A wave step is 16 q4_K super-blocks
+// (2304 bytes, 4096 columns) or 64 q8_0 blocks (2176 bytes, 2048 columns).
+//
+// Weight bytes travel as contiguous 16-byte pieces (every wave load instruction reads 1 KB of consecutive bytes, the
+// pattern that streams at the chip's read rate), land in the wave's own LDS buffer, and lanes read back the pieces
+// their blocks need.
+//
+// LDS layout:
+//   activations, wave-transposed so a wave's 16-byte reads are contiguous across lanes:
+//     q4_K: step s, piece k (0..3), lane l -> activation bytes 64*l + 16*k of the step, at ((s*4 + k)*64 + l)*16
+//     q8_0: step s, piece k (0..1), lane l -> activation bytes 32*l + 16*k of the step, at ((s*2 + k)*64 + l)*16
+//   int32 sums per 32 (q4_K), f32 scales per 32
+//   one GV_STEP_BYTES buffer per wave for its weight step
+//   `iters * GV_WAVES` f32 partials when WPR > 1
+constexpr int GV_STEP_BYTES = 2304;
+constexpr int GV_PIECES = 3;  // 16-byte pieces per lane per step: 144 (q4_K) or 136 (q8_0) pieces over 64 lanes
 
-// Stages q (n bytes), the per-32 integer sums and the per-32 scales of one activation row into LDS
-__device__ __forceinline__ void gv_stage(uint8_t* smem, const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
-                                         const float* __restrict__ xd32, int n) {
-    uint4* sq = reinterpret_cast<uint4*>(smem);
+struct GvLds {
+    size_t xbytes, sums, scales, wbuf, part, total;
+};
+
+__host__ __device__ inline GvLds gv_lds(uint32_t ty, int n, int iters, int wpr) {
+    GvLds l;
+    const int steps = ty == KF_TYPE_Q4_K ? (n / 256 + 15) / 16 : (n / 32 + 63) / 64;
+    l.xbytes = (size_t)steps * (ty == KF_TYPE_Q4_K ? 4096 : 2048);
+    l.sums = l.xbytes;
+    l.scales = l.sums + (ty == KF_TYPE_Q4_K ? (size_t)(n / 32) * 4 : 0);
+    l.wbuf = l.scales + (size_t)(n / 32) * 4;
+    l.wbuf = (l.wbuf + 15) / 16 * 16;
+    l.part = l.wbuf + (size_t)GV_WAVES * GV_STEP_BYTES;
+    l.total = l.part + (wpr > 1 ? (size_t)iters * GV_WAVES * 4 : 0);
+    return l;
+}
+
+// The activation row of one block in flight: each thread loads at most GV_XC 16-byte pieces of int8 values and
+// GV_SC per-32 sums and scales (n <= 32768 with 512 threads). The loads are issued before the weights are requested
+// so that parking them in LDS waits only on them, not on the weights behind them.
+constexpr int GV_XC = (32768 / 16 + GV_THREADS - 1) / GV_THREADS;
+constexpr int GV_SC = (32768 / 32 + GV_THREADS - 1) / GV_THREADS;
+
+struct GvStage {
+    uint4 x[GV_XC];
+    int32_t sum[GV_SC];
+    float scale[GV_SC];
+};
+
+template <uint32_t TY>
+__device__ __forceinline__ void gv_stage_load(GvStage& st, const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
+                                              const float* __restrict__ xd32, int n) {
+    // unpredicated loads (indices clamped into the row; the extra copies are not stored), so the compiler never
+    // waits on one before issuing the next
     const uint4* gq = reinterpret_cast<const uint4*>(xq);
-    for (int i = threadIdx.x; i < (n >> 4); i += GV_THREADS) sq[i] = gq[i];
-    int32_t* ss = reinterpret_cast<int32_t*>(smem + n);
-    float* sd = reinterpret_cast<float*>(smem + n + (n / 32) * 4);
-    for (int i = threadIdx.x; i < (n >> 5); i += GV_THREADS) {
-        ss[i] = xs32[i];
-        sd[i] = xd32[i];
+#pragma unroll
+    for (int i = 0; i < GV_XC; i++) st.x[i] = gq[min((int)threadIdx.x + i * GV_THREADS, (n >> 4) - 1)];
+#pragma unroll
+    for (int i = 0; i < GV_SC; i++) {
+        const int c = min((int)threadIdx.x + i * GV_THREADS, (n >> 5) - 1);
+        if constexpr (TY == KF_TYPE_Q4_K) st.sum[i] = xs32[c];
+        st.scale[i] = xd32[c];
     }
+}
+
+// Parks the activation row in LDS: int8 values in the wave-transposed order, per-32 sums (q4_K) and per-32 scales.
+// Clamped duplicates write the same bytes to the same place, so no store is predicated either (a predicated store
+// lets the compiler sink its load next to it, behind the weight loads).
+template <uint32_t TY>
+__device__ __forceinline__ void gv_stage_store(uint8_t* smem, const GvLds& L, const GvStage& st, int n) {
+    uint4* sx = reinterpret_cast<uint4*>(smem);
+#pragma unroll
+    for (int i = 0; i < GV_XC; i++) {
+        const int c = min((int)threadIdx.x + i * GV_THREADS, (n >> 4) - 1);
+        int dst;
+        if constexpr (TY == KF_TYPE_Q4_K) {
+            const int sb = c >> 4, j = (c >> 2) & 3, k = c & 3;  // 16 pieces per super-block: pair j, piece k
+            dst = (((sb >> 4) * 4 + k) << 6) + ((sb & 15) << 2) + j;
+        } else {
+            const int b = c >> 1, k = c & 1;  // 2 pieces per 32-block
+            dst = (((b >> 6) * 2 + k) << 6) + (b & 63);
+        }
+        sx[dst] = st.x[i];
+    }
+#pragma unroll
+    for (int i = 0; i < GV_SC; i++) {
+        const int c = min((int)threadIdx.x + i * GV_THREADS, (n >> 5) - 1);
+        if constexpr (TY == KF_TYPE_Q4_K) reinterpret_cast<int32_t*>(smem + L.sums)[c] = st.sum[i];
+        reinterpret_cast<float*>(smem + L.scales)[c] = st.scale[i];
+    }
+}
+
+// Per-lane constants of the weight pieces: lane l moves the 16-byte pieces l, l+64 and l+128 of a step
+struct GvLane {
+    int lane;
+    uint32_t off[GV_PIECES];  // byte offsets of the lane's pieces within a step
+};
+
+// Loads one step's pieces (len bytes of the step starting at `step`, a wave-uniform address). Every lane loads all
+// its pieces: a piece past the step's end is clamped onto the step's last 16 bytes, so no byte past the step is
+// read and no load is predicated (predicated loads make the compiler wait for the ring before refilling it).
+// Clamped pieces carry bytes another lane also holds; parking them writes the same bytes to the same place.
+template <uint32_t TY>
+__device__ __forceinline__ void gv_load_step(uint4* v, const uint8_t* step, int len, const GvLane& ln) {
+#pragma unroll
+    for (int i = 0; i < GV_PIECES; i++) {
+        const uint32_t o = min(ln.off[i], (uint32_t)len - 16u);
+        if constexpr (TY == KF_TYPE_Q4_K)
+            v[i] = kf_load_stream_u4(step + o);
+        else
+            v[i] = kf_load_stream_u4_unaligned(step + o);
+    }
+}
+
+// Parks the pieces in the wave's LDS buffer at the offsets they were loaded from
+template <uint32_t TY>
+__device__ __forceinline__ void gv_park(uint8_t* wb, const uint4* v, int len, const GvLane& ln) {
+#pragma unroll
+    for (int i = 0; i < GV_PIECES; i++) {
+        const uint32_t o = min(ln.off[i], (uint32_t)len - 16u);
+        if constexpr (TY == KF_TYPE_Q4_K)
+            *reinterpret_cast<uint4*>(wb + o) = v[i];
+        else
+            *reinterpret_cast<kf_u32x4_a2*>(wb + o) = kf_u32x4_a2{v[i].x, v[i].y, v[i].z, v[i].w};
+    }
+}
+
+// The lane's share of one q4_K step: super-block (lane >> 2) of the step, sub-block pair j = lane & 3. `sb` is the
+// super-block's index in the row, `xs` the lane's first activation piece of the step in the transposed layout.
+__device__ __forceinline__ float gv_q4k_lane(const uint8_t* wl, const uint4* xs, const int32_t* ss, const float* sd, int sb, int j) {
+    const uint4 hdr = *reinterpret_cast<const uint4*>(wl);
+    const uint4 qa = *reinterpret_cast<const uint4*>(wl + 16 + 32 * j);
+    const uint4 qb = *reinterpret_cast<const uint4*>(wl + 32 + 32 * j);
+    const int2 bs = *reinterpret_cast<const int2*>(ss + sb * 8 + 2 * j);
+    int isum, imin;
+    kf_q4k_lane(hdr, qa, qb, j, xs[0], xs[64], xs[128], xs[192], bs.x, bs.y, isum, imin);
+    const float dx = sd[sb * 8];
+    const float d = kf_h2f(hdr.x & 0xffffu) * dx;
+    const float dm = kf_h2f(hdr.x >> 16) * dx;
+    return fmaf(-dm, (float)imin, d * (float)isum);
+}
+
+// The lane's block of one q8_0 step: the 34 bytes at 34 * lane of the step; b is the block's index in the row
+__device__ __forceinline__ float gv_q8_0_lane(const uint8_t* wl, const uint4* xs, const float* sd, int b) {
+    const kf_u32x4_a2 q0 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 2);
+    const kf_u32x4_a2 q1 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 18);
+    const uint32_t wq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int dt = kf_q8_0_dot(wq, xs[0], xs[64]);
+    return kf_h2f(*reinterpret_cast<const uint16_t*>(wl)) * sd[b] * (float)dt;
+}
+
+// Decode GEMV of one activation row. Block b, iteration it (< iters <= MAXIT), row group rg (= wave / WPR) owns row
+// (it * gridDim.x + b) * RPB + rg; the WPR waves of a row group split its steps and meet in LDS at the end. A wave
+// requests the weights of all its iterations before the activation row is staged, each into registers of its own,
+// so nothing waits on a load before the last one is issued. Everything that depends only on the row or step is
+// wave-uniform and lives in scalar registers.
+template <uint32_t TY, int SPW, int WPR, int MAXIT>
+__global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                          const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
+                                                          const float* __restrict__ bias, const float* __restrict__ res,
+                                                          float* __restrict__ y, int n, int n_out, int iters) {
+    constexpr int RPB = GV_WAVES / WPR;
+    constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
+    constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
+    extern __shared__ __align__(16) uint8_t smem[];
+    const GvLds L = gv_lds(TY, n, iters, WPR);
+    GvLane ln;
+    ln.lane = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < GV_PIECES; i++) ln.off[i] = 16u * (uint32_t)(ln.lane + 64 * i);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = wave / WPR, sp = wave % WPR;
+    const int nblk = TY == KF_TYPE_Q4_K ? n >> 8 : n >> 5;
+    const int B = gridDim.x;
+    uint8_t* wb = smem + L.wbuf + wave * GV_STEP_BYTES;
+    const int j = ln.lane & 3;
+    const uint8_t* wl = TY == KF_TYPE_Q4_K ? wb + (ln.lane >> 2) * KF_Q4_K_BYTES : wb + 34 * ln.lane;
+    const uint4* xl = reinterpret_cast<const uint4*>(smem) + ln.lane;
+    const int32_t* ss = reinterpret_cast<const int32_t*>(smem + L.sums);
+    const float* sd = reinterpret_cast<const float*>(smem + L.scales);
+    const int blk_lane = TY == KF_TYPE_Q4_K ? (ln.lane >> 2) : ln.lane;
+
+    GvStage st;
+    if (!(KF_GV_ABLATE & 1)) gv_stage_load<TY>(st, xq, xs32, xd32, n);
+    // keep the activation loads ahead of the weight loads: loads complete in issue order, so parking the
+    // activations then waits only on them
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 ring[MAXIT][SPW][GV_PIECES];
+    const int64_t last_step = (row_bytes - 1) / STEP;
+#pragma unroll
+    for (int it = 0; it < MAXIT; it++) {
+        // unpredicated: an iteration or step past the end reloads a valid row or step whose result is never used
+        const int o = min((min(it, iters - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
+        const uint8_t* row = w + (int64_t)o * row_bytes;
+#pragma unroll
+        for (int i = 0; i < SPW; i++) {
+            const int64_t at = min((int64_t)(sp + i * WPR), last_step) * STEP;
+            gv_load_step<TY>(ring[it][i], row + at, (int)min((int64_t)STEP, row_bytes - at), ln);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (!(KF_GV_ABLATE & 1)) gv_stage_store<TY>(smem, L, st, n);
     __syncthreads();
-}
-
-template <int STEPS>
-__global__ void __launch_bounds__(GV_THREADS) gemv_q4k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
-                                                              const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
-                                                              const float* __restrict__ xd32, const float* __restrict__ bias,
-                                                              const float* __restrict__ res, float* __restrict__ y, int n,
-                                                              int n_out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    gv_stage(smem, xq, xs32, xd32, n);
-    const int8_t* sx = reinterpret_cast<const int8_t*>(smem);
-    const int32_t* ss = reinterpret_cast<const int32_t*>(smem + n);
-    const float* sd = reinterpret_cast<const float*>(smem + n + (n / 32) * 4);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int sbl = lane >> 2;  // super-block of the lane within a step
-    const int j = lane & 3;     // sub-block pair of the lane
-    const int nsb = n >> 8;
-    for (int o = blockIdx.x * GV_WAVES + wave; o < n_out; o += gridDim.x * GV_WAVES) {
-        const uint8_t* row = w + (int64_t)o * row_bytes;
-        uint4 hdr[STEPS], qa[STEPS], qb[STEPS];
+    float* part = reinterpret_cast<float*>(smem + L.part);
 #pragma unroll
-        for (int s = 0; s < STEPS; s++) {
-            const int sb = s * 16 + sbl;
-            if (sb < nsb) {
-                const uint8_t* blk = row + (int64_t)sb * KF_Q4_K_BYTES;
-                hdr[s] = kf_load_stream_u4(blk);
-                qa[s] = kf_load_stream_u4(blk + 16 + 32 * j);
-                qb[s] = kf_load_stream_u4(blk + 32 + 32 * j);
-            }
-        }
-        float acc = 0.0f;
+    for (int it = 0; it < MAXIT; it++) {
+        const int o = (it * B + (int)blockIdx.x) * RPB + rg;
+        if (it < iters && o < n_out) {
+            float acc = 0.0f;
 #pragma unroll
-        for (int s = 0; s < STEPS; s++) {
-            const int sb = s * 16 + sbl;
-            if (sb < nsb) {
-                const uint4* xs = reinterpret_cast<const uint4*>(sx + sb * 256 + 64 * j);
-                const int2 bs = *reinterpret_cast<const int2*>(ss + sb * 8 + 2 * j);
-                int isum, imin;
-                kf_q4k_lane(hdr[s], qa[s], qb[s], j, xs[0], xs[1], xs[2], xs[3], bs.x, bs.y, isum, imin);
-                const float dx = sd[sb * 8];
-                const float d = kf_h2f(hdr[s].x & 0xffffu) * dx;
-                const float dm = kf_h2f(hdr[s].x >> 16) * dx;
-                acc = fmaf(d, (float)isum, acc);
-                acc = fmaf(-dm, (float)imin, acc);
-            }
-        }
-        acc = kf_wave_sum(acc);
-        if (lane == 0) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
-    }
-}
-
-template <int STEPS>
-__global__ void __launch_bounds__(GV_THREADS) gemv_q8_0_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
-                                                               const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
-                                                               const float* __restrict__ xd32, const float* __restrict__ bias,
-                                                               const float* __restrict__ res, float* __restrict__ y, int n,
-                                                               int n_out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    gv_stage(smem, xq, xs32, xd32, n);
-    const int8_t* sx = reinterpret_cast<const int8_t*>(smem);
-    const float* sd = reinterpret_cast<const float*>(smem + n + (n / 32) * 4);
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int nb = n >> 5;
-    for (int o = blockIdx.x * GV_WAVES + wave; o < n_out; o += gridDim.x * GV_WAVES) {
-        const uint8_t* row = w + (int64_t)o * row_bytes;
-        float acc = 0.0f;
-        // groups of four steps: the loads of a group go out before its arithmetic
-        for (int s0 = 0; s0 < STEPS; s0 += 4) {
-            uint32_t win[4][9];
-            bool sk[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int b = (s0 + u) * 64 + lane;
-                if (s0 + u < STEPS && b < nb) kf_q8_0_window(row + (int64_t)b * KF_Q8_0_BYTES, win[u], sk[u]);
-            }
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int b = (s0 + u) * 64 + lane;
-                if (s0 + u < STEPS && b < nb) {
-                    uint32_t dbits, wq[8];
-                    kf_q8_0_unpack(win[u], sk[u], dbits, wq);
-                    const uint4* xs = reinterpret_cast<const uint4*>(sx + b * 32);
-                    const int dot = kf_q8_0_dot(wq, xs[0], xs[1]);
-                    acc = fmaf(kf_h2f(dbits) * sd[b], (float)dot, acc);
+            for (int i = 0; i < SPW; i++) {
+                const int s = sp + i * WPR;
+                const int64_t at = (int64_t)s * STEP;
+                if (at < row_bytes) {
+                    if (!(KF_GV_ABLATE & 4)) gv_park<TY>(wb, ring[it][i], (int)min((int64_t)STEP, row_bytes - at), ln);
+                    __builtin_amdgcn_wave_barrier();
+                    const int blk = s * PER_STEP + blk_lane;
+                    if (KF_GV_ABLATE & 2) {
+                        const uint4* q = reinterpret_cast<const uint4*>(wl);
+                        acc += (KF_GV_ABLATE & 4) ? (float)(ring[it][i][0].x ^ ring[it][i][1].y ^ ring[it][i][2].z) : (float)(q->x ^ q->w);
+                    } else if (blk < nblk) {
+                        if constexpr (TY == KF_TYPE_Q4_K)
+                            acc += gv_q4k_lane(wl, xl + ((s * 4) << 6), ss, sd, blk, j);
+                        else
+                            acc += gv_q8_0_lane(wl, xl + ((s * 2) << 6), sd, blk);
+                    }
+                    __builtin_amdgcn_wave_barrier();
                 }
             }
+            acc = kf_wave_sum_dpp(acc);
+            if (ln.lane == 0) {
+                if (WPR == 1) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+                else part[it * GV_WAVES + wave] = acc;
+            }
         }
-        acc = kf_wave_sum(acc);
-        if (lane == 0) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+    }
+    if (WPR > 1) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < iters * RPB; t += GV_THREADS) {
+            const int it = t / RPB, g = t % RPB;
+            const int o = (it * B + (int)blockIdx.x) * RPB + g;
+            if (o >= n_out) continue;
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WPR; q++) acc += part[it * GV_WAVES + g * WPR + q];
+            y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+        }
     }
 }
+
+// ------------------------------------------------------------------------------------------------ DMA variant
+// The same product with both the activation row and the weight steps fetched straight into LDS by
+// global_load_lds_dwordx4 (gfx950): lane l of one instruction writes its 16 bytes at the instruction's LDS base
+// + 16 * l. Nothing passes through registers, so the compiler cannot reorder the streams, and a wave's weights for
+// all its row iterations are requested before the block waits on the (small, L2-resident) activation row.
+// Requires 16-byte aligned rows (q4_K always; q8_0 when the row width is a multiple of 128).
+
+typedef __attribute__((address_space(3))) void kf_lds_void;
+typedef const __attribute__((address_space(1))) void kf_gbl_void;
+
+__device__ __forceinline__ void gv_dma16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void gv_dma4(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 4, 0, 0);
+}
+
+struct GdLds {
+    size_t sums, scales, wbuf, part, total;
+};
+
+// LDS of the DMA variant: transposed activations, sums, scales, then MAXIT * SPW step buffers per wave, partials
+__host__ __device__ inline GdLds gd_lds(uint32_t ty, int n, int iters, int wpr, int maxit, int spw) {
+    GdLds l;
+    const int steps = ty == KF_TYPE_Q4_K ? (n / 256 + 15) / 16 : (n / 32 + 63) / 64;
+    const size_t xbytes = (size_t)steps * (ty == KF_TYPE_Q4_K ? 4096 : 2048);
+    const size_t n32 = (size_t)((n / 32 + 63) / 64 * 64);  // whole 64-entry DMA instructions
+    l.sums = xbytes;
+    l.scales = l.sums + (ty == KF_TYPE_Q4_K ? n32 * 4 : 0);
+    l.wbuf = l.scales + n32 * 4;
+    l.part = l.wbuf + (size_t)GV_WAVES * maxit * spw * GV_STEP_BYTES;
+    l.total = l.part + (wpr > 1 ? (size_t)iters * GV_WAVES * 4 : 0);
+    return l;
+}
+
+template <uint32_t TY, int SPW, int WPR, int MAXIT>
+__global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                              const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
+                                                              const float* __restrict__ bias, const float* __restrict__ res,
+                                                              float* __restrict__ y, int n, int n_out, int iters) {
+    constexpr int RPB = GV_WAVES / WPR;
+    constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
+    constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
+    extern __shared__ __align__(16) uint8_t smem[];
+    const GdLds L = gd_lds(TY, n, iters, WPR, MAXIT, SPW);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = wave / WPR, sp = wave % WPR;
+    const int nblk = TY == KF_TYPE_Q4_K ? n >> 8 : n >> 5;
+    const int B = gridDim.x;
+    const int steps = TY == KF_TYPE_Q4_K ? (nblk + 15) / 16 : (nblk + 63) / 64;
+    const int64_t last_step = (row_bytes - 1) / STEP;
+
+    // 1. the activation row, split over the block's waves: instruction q < steps*K4 moves piece k of step s (the 64
+    //    lanes' 16-byte pieces of the transposed layout); then the per-32 sums and scales, 64 entries an instruction
+    {
+        constexpr int K4 = TY == KF_TYPE_Q4_K ? 4 : 2;
+        const int nx = steps * K4;
+        const int n32 = n >> 5, n32i = (n32 + 63) / 64;
+        const int total = nx + (TY == KF_TYPE_Q4_K ? 2 : 1) * n32i;
+        for (int q = wave; q < total; q += GV_WAVES) {
+            if (q < nx) {
+                const int st = q / K4, k = q % K4;
+                // lane l of (step st, piece k) holds activation piece c = 256 st + 4 l + k (q4_K) or 128 st + 2 l + k
+                int c = TY == KF_TYPE_Q4_K ? 256 * st + 4 * lane + k : 128 * st + 2 * lane + k;
+                c = min(c, (n >> 4) - 1);  // lanes past the row's end fetch a valid piece nobody reads
+                gv_dma16(xq + 16 * c, smem + (size_t)((st * K4 + k) << 10));
+            } else {
+                const int r = q - nx;
+                const int which = TY == KF_TYPE_Q4_K ? r / n32i : 1;  // 0: sums, 1: scales
+                const int i = (TY == KF_TYPE_Q4_K ? r % n32i : r) * 64;
+                const int c = min(i + lane, n32 - 1);
+                if (which == 0)
+                    gv_dma4(xs32 + c, smem + L.sums + 4 * i);
+                else
+                    gv_dma4(xd32 + c, smem + L.scales + 4 * i);
+            }
+        }
+    }
+    // 2. the weights of every row iteration of the wave, one buffer per (iteration, step)
+    uint8_t* wb = smem + L.wbuf + (size_t)wave * MAXIT * SPW * GV_STEP_BYTES;
+#pragma unroll
+    for (int it = 0; it < MAXIT; it++) {
+        const int o = min((min(it, iters - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
+        const uint8_t* row = w + (int64_t)o * row_bytes;
+#pragma unroll
+        for (int i = 0; i < SPW; i++) {
+            const int64_t at = min((int64_t)(sp + i * WPR), last_step) * STEP;
+            const int len = (int)min((int64_t)STEP, row_bytes - at);
+            uint8_t* buf = wb + (it * SPW + i) * GV_STEP_BYTES;
+            const uint8_t* src = row + at;
+            gv_dma16(src + min(16 * lane, len - 16), buf);
+            gv_dma16(src + min(16 * lane + 1024, len - 16), buf + 1024);
+            if (lane < (GV_STEP_BYTES - 2048) / 16) gv_dma16(src + min(16 * lane + 2048, len - 16), buf + 2048);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    // 3. the products, from LDS only
+    const int j = lane & 3;
+    const uint4* xl = reinterpret_cast<const uint4*>(smem) + lane;
+    const int32_t* ss = reinterpret_cast<const int32_t*>(smem + L.sums);
+    const float* sd = reinterpret_cast<const float*>(smem + L.scales);
+    const int blk_lane = TY == KF_TYPE_Q4_K ? (lane >> 2) : lane;
+    float* part = reinterpret_cast<float*>(smem + L.part);
+#pragma unroll
+    for (int it = 0; it < MAXIT; it++) {
+        const int o = (it * B + (int)blockIdx.x) * RPB + rg;
+        if (it < iters && o < n_out) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int i = 0; i < SPW; i++) {
+                const int s = sp + i * WPR;
+                const int blk = s * PER_STEP + blk_lane;
+                if (s < steps && blk < nblk) {
+                    const uint8_t* buf = wb + (it * SPW + i) * GV_STEP_BYTES;
+                    if constexpr (TY == KF_TYPE_Q4_K)
+                        acc += gv_q4k_lane(buf + (lane >> 2) * KF_Q4_K_BYTES, xl + ((s * 4) << 6), ss, sd, blk, j);
+                    else
+                        acc += gv_q8_0_lane(buf + 34 * lane, xl + ((s * 2) << 6), sd, blk);
+                }
+            }
+            acc = kf_wave_sum_dpp(acc);
+            if (lane == 0) {
+                if (WPR == 1) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+                else part[it * GV_WAVES + wave] = acc;
+            }
+        }
+    }
+    if (WPR > 1) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < iters * RPB; t += GV_THREADS) {
+            const int it = t / RPB, g = t % RPB;
+            const int o = (it * B + (int)blockIdx.x) * RPB + g;
+            if (o >= n_out) continue;
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WPR; q++) acc += part[it * GV_WAVES + g * WPR + q];
+            y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+        }
+    }
+}
+
+// The unit loads of the per-block integer check: a q8_0 block read as its f16 scale and two unaligned 16-byte loads
+struct Q8Unit {
+    uint32_t dbits;
+    uint4 q0, q1;
+
+    __device__ __forceinline__ void load(const uint8_t* row, int b) {
+        const uint8_t* blk = row + (int64_t)b * KF_Q8_0_BYTES;
+        dbits = *reinterpret_cast<const uint16_t*>(blk);
+        q0 = kf_load_stream_u4_unaligned(blk + 2);
+        q1 = kf_load_stream_u4_unaligned(blk + 18);
+    }
+};
 
 // Per-block integers of weight rows against activation rows, one thread per (weight row, activation row, block):
 // q8_0 one int32 per 32-block, q4_K (sumi, mins) per super-block. The check that pins the GEMV's lane arithmetic.
@@ -144,10 +455,9 @@ __global__ void block_ints_kernel(uint32_t ty, const uint8_t* __restrict__ w, in
     const uint8_t* row = w + (int64_t)o * row_bytes;
     const int8_t* x = xq + (int64_t)r * n;
     if (ty == KF_TYPE_Q8_0) {
-        uint32_t win[9], dbits, wq[8];
-        bool sk;
-        kf_q8_0_window(row + (int64_t)b * KF_Q8_0_BYTES, win, sk);
-        kf_q8_0_unpack(win, sk, dbits, wq);
+        Q8Unit u;
+        u.load(row, b);
+        const uint32_t wq[8] = {u.q0.x, u.q0.y, u.q0.z, u.q0.w, u.q1.x, u.q1.y, u.q1.z, u.q1.w};
         const uint4* xs = reinterpret_cast<const uint4*>(x + b * 32);
         out[t] = kf_q8_0_dot(wq, xs[0], xs[1]);
     } else {
@@ -182,54 +492,74 @@ int cu_count() {
     return g_cu_count;
 }
 
+typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int);
+
+template <uint32_t TY, int SPW, int WPR>
+hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
+                       const float* res, float* y, int n, int n_out, int maxit_env, hipStream_t s) {
+    constexpr int RPB = GV_WAVES / WPR;
+    const int groups = (n_out + RPB - 1) / RPB;
+    // row iterations per block: enough blocks that the chip is full, each block's waves holding the loads of all
+    // their rows at once
+    const int want = maxit_env > 0 ? maxit_env : KF_GV_MAXIT;
+    // the DMA variant needs 16-byte aligned rows and activation pieces
+    const bool dma = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(xq) & 15) == 0 &&
+                     !getenv("KF_GEMV_NO_DMA");
+#define KF_GV_IT(M)                                                                                                      \
+    if (want <= M) {                                                                                                     \
+        const int grid = (groups + M - 1) / M;                                                                           \
+        const int iters = (groups + grid - 1) / grid;                                                                    \
+        if (dma && gd_lds(TY, n, iters, WPR, M, SPW).total <= 65536) {                                                   \
+            const size_t smem = gd_lds(TY, n, iters, WPR, M, SPW).total;                                                 \
+            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters); \
+        } else {                                                                                                         \
+            const size_t smem = gv_lds(TY, n, iters, WPR).total;                                                         \
+            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters); \
+        }                                                                                                                \
+        return hipGetLastError();                                                                                        \
+    }
+    KF_GV_IT(1)
+    KF_GV_IT(2)
+    KF_GV_IT(4)
+#undef KF_GV_IT
+    return hipErrorInvalidValue;
+}
+
+// Waves per row for a row of `steps` wave steps: the smallest power of two covering the steps, at most GV_WAVES
+int gv_wpr(int steps) {
+    int wpr = 1;
+    while (wpr < steps && wpr < GV_WAVES) wpr *= 2;
+    return wpr;
+}
+
 }  // namespace
 
 // Largest row width the single-row GEMV stages in LDS
 int kf_gemv_max_n() { return 32768; }
 
-int kf_gemv_blocks(int n_out, int blocks_per_cu) {
-    const int want = (n_out + GV_WAVES - 1) / GV_WAVES;
-    const int cap = cu_count() * (blocks_per_cu > 0 ? blocks_per_cu : 2);
-    return want < cap ? want : cap;
-}
-
-#define KF_GEMV_CASE(KERN, S)                                                                                               \
-    case S:                                                                                                                 \
-        KERN<S><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out);                       \
-        break;
-
 // Host launcher for one activation row, validated by the caller (api.cpp): n a multiple of the type's block,
 // n <= kf_gemv_max_n(). xq / xs32 / xd32 point at the row's int8 values, per-32 sums and per-32 scales.
 hipError_t kf_launch_gemv1(uint32_t ty, const void* wv, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
-                           const float* bias, const float* res, float* y, int n, int n_out, int blocks_per_cu, hipStream_t s) {
-    const uint8_t* w = static_cast<const uint8_t*>(wv);
-    const size_t smem = gv_smem(n);
-    const int grid = kf_gemv_blocks(n_out, blocks_per_cu);
+                           const float* bias, const float* res, float* y, int n, int n_out, int maxit, hipStream_t s) {
     if (n_out == 0) return hipSuccess;
-    if (ty == KF_TYPE_Q4_K) {
-        const int steps = (n / 256 + 15) / 16;
-        switch (steps) {
-            KF_GEMV_CASE(gemv_q4k_kernel, 1)
-            KF_GEMV_CASE(gemv_q4k_kernel, 2)
-            KF_GEMV_CASE(gemv_q4k_kernel, 3)
-            KF_GEMV_CASE(gemv_q4k_kernel, 4)
-            KF_GEMV_CASE(gemv_q4k_kernel, 5)
-            KF_GEMV_CASE(gemv_q4k_kernel, 6)
-            KF_GEMV_CASE(gemv_q4k_kernel, 7)
-            KF_GEMV_CASE(gemv_q4k_kernel, 8)
-            default: return hipErrorInvalidValue;
-        }
-    } else {
-        const int steps = (n / 32 + 63) / 64;
-        switch ((steps + 3) / 4 * 4) {
-            KF_GEMV_CASE(gemv_q8_0_kernel, 4)
-            KF_GEMV_CASE(gemv_q8_0_kernel, 8)
-            KF_GEMV_CASE(gemv_q8_0_kernel, 12)
-            KF_GEMV_CASE(gemv_q8_0_kernel, 16)
-            default: return hipErrorInvalidValue;
-        }
-    }
-    return hipGetLastError();
+    const uint8_t* w = static_cast<const uint8_t*>(wv);
+    const int steps = ty == KF_TYPE_Q4_K ? (n / 256 + 15) / 16 : (n / 32 + 63) / 64;
+    const int wpr = gv_wpr(steps);
+    const int spw = (steps + wpr - 1) / wpr;
+#define KF_GV(TY, SPW, WPR)                                                                                      \
+    if (ty == TY && spw == SPW && wpr == WPR)                                                                    \
+        return launch_gemv<TY, SPW, WPR>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, maxit, s);
+    KF_GV(KF_TYPE_Q4_K, 1, 1)
+    KF_GV(KF_TYPE_Q4_K, 1, 2)
+    KF_GV(KF_TYPE_Q4_K, 1, 4)
+    KF_GV(KF_TYPE_Q4_K, 1, 8)
+    KF_GV(KF_TYPE_Q8_0, 1, 1)
+    KF_GV(KF_TYPE_Q8_0, 1, 2)
+    KF_GV(KF_TYPE_Q8_0, 1, 4)
+    KF_GV(KF_TYPE_Q8_0, 1, 8)
+    KF_GV(KF_TYPE_Q8_0, 2, 8)
+#undef KF_GV
+    return hipErrorInvalidValue;
 }
 
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,

@@ -6,8 +6,8 @@
 // imin = m_2j * bsum_2j + m_2j+1 * bsum_2j+1. Summing the four lanes of a super-block gives exactly the reference's
 // sumi and mins.
 //
-// q8_0 lane unit: one 34-byte block read through a dword window (the block is only 2-byte aligned), yielding the
-// f16 scale bits and the int32 sum of q_w * q_x (crates/kf-quant/src/types/q8_0.rs:10-29).
+// q8_0 lane unit: one 34-byte block (only 2-byte aligned: its f16 scale, then 32 int8 weights read as two unaligned
+// 16-byte loads), yielding the int32 sum of q_w * q_x (crates/kf-quant/src/types/q8_0.rs:10-29).
 #pragma once
 #include "kf_device.h"
 
@@ -61,19 +61,9 @@ __device__ __forceinline__ void kf_q4k_lane(const uint4 hdr, const uint4 qa, con
     kf_q4k_scales(hdr.y, hdr.z, hdr.w, j, sc2, m2);
     int dlo, dhi;
     kf_q4k_pair_dots(qa, qb, x0, x1, x2, x3, dlo, dhi);
-    isum = (int)(sc2 & 0xffu) * dlo + (int)(sc2 >> 8) * dhi;
-    imin = (int)(m2 & 0xffu) * bs0 + (int)(m2 >> 8) * bs1;
-}
-
-// q8_0 block through a dword window. win[0..8] are the nine dwords from the block address rounded down to 4 bytes;
-// skew2 is set when the block starts 2 bytes into its first dword. Yields the f16 scale bits and the eight int8
-// weight dwords.
-__device__ __forceinline__ void kf_q8_0_unpack(const uint32_t* win, bool skew2, uint32_t& dbits, uint32_t* wq) {
-    dbits = skew2 ? (win[0] >> 16) : (win[0] & 0xffffu);
-    // v_perm_b32 selector: bytes 4-7 name the first operand, 0-3 the second
-    const uint32_t sel = skew2 ? 0x07060504u : 0x05040302u;
-#pragma unroll
-    for (int k = 0; k < 8; k++) wq[k] = __builtin_amdgcn_perm(win[k + 1], win[k], sel);
+    // 24-bit multiplies are exact here: scales and mins are 6-bit, |dot| <= 15*127*32 and |bsum| <= 128*32
+    isum = __mul24((int)(sc2 & 0xffu), dlo) + __mul24((int)(sc2 >> 8), dhi);
+    imin = __mul24((int)(m2 & 0xffu), bs0) + __mul24((int)(m2 >> 8), bs1);
 }
 
 __device__ __forceinline__ int kf_q8_0_dot(const uint32_t* wq, const uint4 x0, const uint4 x1) {
@@ -87,19 +77,4 @@ __device__ __forceinline__ int kf_q8_0_dot(const uint32_t* wq, const uint4 x0, c
     s = kf_dot4(wq[6], x1.z, s);
     s = kf_dot4(wq[7], x1.w, s);
     return s;
-}
-
-// Loads the dword window of the q8_0 block at byte address p (2-byte aligned) without reading past its last byte
-__device__ __forceinline__ void kf_q8_0_window(const uint8_t* p, uint32_t* win, bool& skew2) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    skew2 = (a & 2u) != 0;
-    const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3);
-#pragma unroll
-    for (int k = 0; k < 8; k++) win[k] = __builtin_nontemporal_load(base + k);
-    // the ninth dword holds the block's last 2 bytes (skew 0) or 4 bytes (skew 2)
-    if (skew2) {
-        win[8] = __builtin_nontemporal_load(base + 8);
-    } else {
-        win[8] = (uint32_t)__builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(base + 8));
-    }
 }

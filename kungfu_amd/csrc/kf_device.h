@@ -24,11 +24,31 @@ __device__ __forceinline__ int kf_dot4(uint32_t a, uint32_t b, int c) {
     return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total
+// Sum over the 64 lanes of a wave; every lane receives the total (LDS permutes, for code off the hot path)
 __device__ __forceinline__ float kf_wave_sum(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, KF_WAVE);
     return v;
+}
+
+// DPP lane move of a float (v_mov_b32_dpp), all rows and banks enabled
+template <int CTRL>
+__device__ __forceinline__ float kf_dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over the 64 lanes of a wave through DPP within each row of 16 lanes and four lane reads across the rows; the
+// result is uniform (held in a scalar register). Full-rate VALU work instead of LDS permutes.
+__device__ __forceinline__ float kf_wave_sum_dpp(float v) {
+    v += kf_dpp<0xb1>(v);   // quad_perm [1,0,3,2]
+    v += kf_dpp<0x4e>(v);   // quad_perm [2,3,0,1]
+    v += kf_dpp<0x124>(v);  // row_ror:4
+    v += kf_dpp<0x128>(v);  // row_ror:8
+    const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0));
+    const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 16));
+    const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+    const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 __device__ __forceinline__ int kf_wave_isum(int v) {
@@ -47,5 +67,13 @@ typedef uint32_t kf_u32x4 __attribute__((ext_vector_type(4)));
 // 16-byte load of streamed data read once (non-temporal hint), p 16-byte aligned
 __device__ __forceinline__ uint4 kf_load_stream_u4(const void* p) {
     const kf_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const kf_u32x4*>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16-byte load of streamed data at a 2-byte aligned address. gfx9 HSA targets run in unaligned access mode, so this
+// is one global_load_dwordx4 that the memory pipeline splits across cache lines as needed.
+typedef uint32_t kf_u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+__device__ __forceinline__ uint4 kf_load_stream_u4_unaligned(const void* p) {
+    const kf_u32x4_a2 v = __builtin_nontemporal_load(reinterpret_cast<const kf_u32x4_a2*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
