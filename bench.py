@@ -181,7 +181,7 @@ def main():
         us_mm = time_launches(sh.matmul, 200)
         per[sh.name] = {"n_in": sh.n, "n_out": sh.n_out, "us": round(us, 3), "GBs": round(sh.bytes / us / 1e3, 1),
                         "frac": round(sh.bytes / us / 1e3 / HBM_PEAK_GBS, 4), "us_with_quant": round(us_mm, 3)}
-        if sh.n <= 4096:  # the launches of gemv_q4k_kernel<1>, the kernel with most of the step's time
+        if sh.n <= 4096:  # the launches of the one-wave-per-row q4_K kernel, which take most of the step's time
             k1_bytes += sh.bytes
             k1_us += us
     achieved = k1_bytes / k1_us / 1e3
@@ -207,7 +207,7 @@ def main():
         "config": {"workload": "Q4_K decode GEMV, Llama-3-8B layer shapes, batch 1 (QKV, O, gate, up, down)",
                    "bytes_per_step": step_bytes, "weight_copies": copies,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_q4k_kernel<1> (QKV, O, gate, up launches)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_pipe_kernel<q4_K, 1 wave per row> (QKV, O, gate, up launches)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "shapes": per,

@@ -103,7 +103,7 @@ __device__ __forceinline__ void gv_stage_load(GvStage& st, const int8_t* __restr
 // Clamped duplicates write the same bytes to the same place, so no store is predicated either (a predicated store
 // lets the compiler sink its load next to it, behind the weight loads).
 template <uint32_t TY>
-__device__ __forceinline__ void gv_stage_store(uint8_t* smem, const GvLds& L, const GvStage& st, int n) {
+__device__ __forceinline__ void gv_stage_store(uint8_t* smem, size_t sums_at, size_t scales_at, const GvStage& st, int n) {
     uint4* sx = reinterpret_cast<uint4*>(smem);
 #pragma unroll
     for (int i = 0; i < GV_XC; i++) {
@@ -121,8 +121,8 @@ __device__ __forceinline__ void gv_stage_store(uint8_t* smem, const GvLds& L, co
 #pragma unroll
     for (int i = 0; i < GV_SC; i++) {
         const int c = min((int)threadIdx.x + i * GV_THREADS, (n >> 5) - 1);
-        if constexpr (TY == KF_TYPE_Q4_K) reinterpret_cast<int32_t*>(smem + L.sums)[c] = st.sum[i];
-        reinterpret_cast<float*>(smem + L.scales)[c] = st.scale[i];
+        if constexpr (TY == KF_TYPE_Q4_K) reinterpret_cast<int32_t*>(smem + sums_at)[c] = st.sum[i];
+        reinterpret_cast<float*>(smem + scales_at)[c] = st.scale[i];
     }
 }
 
@@ -223,10 +223,13 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
     __builtin_amdgcn_sched_barrier(0);
     uint4 ring[MAXIT][SPW][GV_PIECES];
     const int64_t last_step = (row_bytes - 1) / STEP;
+    int iw = iters;  // iterations whose row exists for this wave (see the pipelined variant)
+    while (iw > 0 && ((iw - 1) * B + (int)blockIdx.x) * RPB + rg >= n_out) iw--;
+    if (iw == 0) iw = 1;
 #pragma unroll
     for (int it = 0; it < MAXIT; it++) {
         // unpredicated: an iteration or step past the end reloads a valid row or step whose result is never used
-        const int o = min((min(it, iters - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
+        const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
         const uint8_t* row = w + (int64_t)o * row_bytes;
 #pragma unroll
         for (int i = 0; i < SPW; i++) {
@@ -235,7 +238,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (!(KF_GV_ABLATE & 1)) gv_stage_store<TY>(smem, L, st, n);
+    if (!(KF_GV_ABLATE & 1)) gv_stage_store<TY>(smem, L.sums, L.scales, st, n);
     __syncthreads();
     float* part = reinterpret_cast<float*>(smem + L.part);
 #pragma unroll
@@ -291,6 +294,10 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
 // all its row iterations are requested before the block waits on the (small, L2-resident) activation row.
 // Requires 16-byte aligned rows (q4_K always; q8_0 when the row width is a multiple of 128).
 
+// s_waitcnt immediate waiting until at most N vector memory loads are outstanding (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima so they are not waited on)
+#define KF_WAITCNT_VM(N) ((((N) & 15)) | (7 << 4) | (15 << 8) | ((((N) >> 4) & 3) << 14))
+
 typedef __attribute__((address_space(3))) void kf_lds_void;
 typedef const __attribute__((address_space(1))) void kf_gbl_void;
 
@@ -320,6 +327,16 @@ __host__ __device__ inline GdLds gd_lds(uint32_t ty, int n, int iters, int wpr, 
     return l;
 }
 
+#ifdef KF_GV_TRACE
+// timeline of every wave (variant builds only): entry, data in LDS, done, in 100 MHz ticks
+__device__ uint64_t* kf_gv_trace;
+#define KF_GV_STAMP(k)                                                                                                 \
+    if (kf_gv_trace && (threadIdx.x & 63) == 0)                                                                        \
+        kf_gv_trace[((size_t)blockIdx.x * GV_WAVES + (threadIdx.x >> 6)) * 4 + (k)] = __builtin_amdgcn_s_memrealtime();
+#else
+#define KF_GV_STAMP(k)
+#endif
+
 template <uint32_t TY, int SPW, int WPR, int MAXIT>
 __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                               const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
@@ -329,6 +346,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
     extern __shared__ __align__(16) uint8_t smem[];
+    KF_GV_STAMP(0)
     const GdLds L = gd_lds(TY, n, iters, WPR, MAXIT, SPW);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -366,9 +384,12 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
     }
     // 2. the weights of every row iteration of the wave, one buffer per (iteration, step)
     uint8_t* wb = smem + L.wbuf + (size_t)wave * MAXIT * SPW * GV_STEP_BYTES;
+    int iw = iters;  // iterations whose row exists for this wave (see the pipelined variant)
+    while (iw > 0 && ((iw - 1) * B + (int)blockIdx.x) * RPB + rg >= n_out) iw--;
+    if (iw == 0) iw = 1;
 #pragma unroll
     for (int it = 0; it < MAXIT; it++) {
-        const int o = min((min(it, iters - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
+        const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
         const uint8_t* row = w + (int64_t)o * row_bytes;
 #pragma unroll
         for (int i = 0; i < SPW; i++) {
@@ -382,7 +403,9 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
         }
     }
     __builtin_amdgcn_s_waitcnt(0);
+    KF_GV_STAMP(1)
     __syncthreads();
+    KF_GV_STAMP(2)
 
     // 3. the products, from LDS only
     const int j = lane & 3;
@@ -415,6 +438,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
             }
         }
     }
+    KF_GV_STAMP(3)
     if (WPR > 1) {
         __syncthreads();
         for (int t = threadIdx.x; t < iters * RPB; t += GV_THREADS) {
@@ -424,6 +448,150 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
             float acc = 0.0f;
 #pragma unroll
             for (int q = 0; q < WPR; q++) acc += part[it * GV_WAVES + g * WPR + q];
+            y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ pipelined variant
+// Persistent waves walk their rows with two register sets: while row i is parked in the wave's LDS buffer and
+// multiplied, the loads of rows i+1 and i+2 are in flight, so the arithmetic of a wave overlaps its own weight stream
+// (a wave that computes only after all its loads land holds its slot while the memory pipe idles). The activation
+// row reaches LDS by DMA before any weight is requested.
+template <uint32_t TY, int WPR>
+__global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                               const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
+                                                               const float* __restrict__ bias, const float* __restrict__ res,
+                                                               float* __restrict__ y, int n, int n_out, int iters) {
+    constexpr int RPB = GV_WAVES / WPR;
+    constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
+    constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;
+    extern __shared__ __align__(16) uint8_t smem[];
+    KF_GV_STAMP(0)
+    const GdLds L = gd_lds(TY, n, iters, WPR, 1, 1);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = wave / WPR, sp = wave % WPR;
+    const int nblk = TY == KF_TYPE_Q4_K ? n >> 8 : n >> 5;
+    const int B = gridDim.x;
+    const int steps = TY == KF_TYPE_Q4_K ? (nblk + 15) / 16 : (nblk + 63) / 64;
+    const int64_t at = (int64_t)min(sp, steps - 1) * STEP;  // the wave's step of every row
+    const int len = (int)min((int64_t)STEP, row_bytes - at);
+    const bool has_step = sp < steps;
+
+    // the activation row is staged by the first waves only (256 pieces of 16 bytes and 128 sums and scales a wave,
+    // all loads issued before the first wait), which then request their own weights; the other waves request theirs
+    // at once, so most waves start streaming without waiting on the activation row
+    {
+        const int nchunks = n >> 4, n32 = n >> 5;
+        const int nsw = (nchunks + 255) / 256;
+        if (wave < nsw) {
+            const uint4* gq = reinterpret_cast<const uint4*>(xq);
+            uint4 v[4];
+            int32_t sv[2];
+            float dv[2];
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = gq[min(wave * 256 + i * 64 + lane, nchunks - 1)];
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int c = min(wave * 128 + i * 64 + lane, n32 - 1);
+                if constexpr (TY == KF_TYPE_Q4_K) sv[i] = xs32[c];
+                dv[i] = xd32[c];
+            }
+            uint4* sx = reinterpret_cast<uint4*>(smem);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int c = min(wave * 256 + i * 64 + lane, nchunks - 1);
+                int dst;
+                if constexpr (TY == KF_TYPE_Q4_K) {
+                    const int sb = c >> 4, jj = (c >> 2) & 3, k = c & 3;
+                    dst = (((sb >> 4) * 4 + k) << 6) + ((sb & 15) << 2) + jj;
+                } else {
+                    const int bb = c >> 1, k = c & 1;
+                    dst = (((bb >> 6) * 2 + k) << 6) + (bb & 63);
+                }
+                sx[dst] = v[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int c = min(wave * 128 + i * 64 + lane, n32 - 1);
+                if constexpr (TY == KF_TYPE_Q4_K) reinterpret_cast<int32_t*>(smem + L.sums)[c] = sv[i];
+                reinterpret_cast<float*>(smem + L.scales)[c] = dv[i];
+            }
+        }
+    }
+
+    GvLane ln;
+    ln.lane = lane;
+#pragma unroll
+    for (int i = 0; i < GV_PIECES; i++) ln.off[i] = 16u * (uint32_t)(lane + 64 * i);
+    uint8_t* wb = smem + L.wbuf + (size_t)wave * GV_STEP_BYTES;
+    const int j = lane & 3;
+    const uint8_t* wl = TY == KF_TYPE_Q4_K ? wb + (lane >> 2) * KF_Q4_K_BYTES : wb + 34 * lane;
+    const uint4* xl = reinterpret_cast<const uint4*>(smem) + lane + ((sp * (TY == KF_TYPE_Q4_K ? 4 : 2)) << 6);
+    const int32_t* ss = reinterpret_cast<const int32_t*>(smem + L.sums);
+    const float* sd = reinterpret_cast<const float*>(smem + L.scales);
+    const int blk = sp * PER_STEP + (TY == KF_TYPE_Q4_K ? (lane >> 2) : lane);
+    float* part = reinterpret_cast<float*>(smem + L.part);
+    // iterations whose row exists for this wave; loads past them reload the wave's own last row (spread over the
+    // chip, unlike a clamp to the matrix's last row, which would send every such wave to the same cache lines)
+    int iw = iters;
+    while (iw > 0 && ((iw - 1) * B + (int)blockIdx.x) * RPB + rg >= n_out) iw--;
+    if (iw == 0) iw = 1;  // a wave without rows still runs the barrier; it reloads row rg of the block's first group
+    auto row_ptr = [&](int it) {
+        const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
+        return w + (int64_t)o * row_bytes + at;
+    };
+    auto process = [&](const uint4* v, int it) {
+        gv_park<TY>(wb, v, len, ln);
+        __builtin_amdgcn_wave_barrier();
+        float acc = 0.0f;
+        if (has_step && blk < nblk) {
+            if constexpr (TY == KF_TYPE_Q4_K)
+                acc = gv_q4k_lane(wl, xl, ss, sd, blk, j);
+            else
+                acc = gv_q8_0_lane(wl, xl, sd, blk);
+        }
+        __builtin_amdgcn_wave_barrier();
+        acc = kf_wave_sum_dpp(acc);
+        const int o = (it * B + (int)blockIdx.x) * RPB + rg;
+        if (lane == 0 && o < n_out) {
+            if (WPR == 1) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+            else part[it * GV_WAVES + wave] = acc;
+        }
+    };
+
+    // the first two rows' weights go out before the block waits on its activation row; vmcnt counts loads in issue
+    // order, so waiting until only those weight loads are outstanding means the activation DMA has landed
+    uint4 a[GV_PIECES], b[GV_PIECES];
+    gv_load_step<TY>(a, row_ptr(0), len, ln);
+    gv_load_step<TY>(b, row_ptr(1), len, ln);
+    // wave 0's activation stores are LDS writes of this block only: waiting on lgkmcnt and a bare barrier order them
+    // (__syncthreads would add a release fence that waits on the weight loads as well)
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
+    __builtin_amdgcn_s_barrier();
+    KF_GV_STAMP(1)
+    int it = 0;
+    for (; it + 2 < iters; it += 2) {
+        process(a, it);
+        gv_load_step<TY>(a, row_ptr(it + 2), len, ln);
+        process(b, it + 1);
+        gv_load_step<TY>(b, row_ptr(it + 3), len, ln);
+    }
+    process(a, it);
+    KF_GV_STAMP(2)
+    if (it + 1 < iters) process(b, it + 1);
+    KF_GV_STAMP(3)
+
+    if (WPR > 1) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < iters * RPB; t += GV_THREADS) {
+            const int it2 = t / RPB, g = t % RPB;
+            const int o = (it2 * B + (int)blockIdx.x) * RPB + g;
+            if (o >= n_out) continue;
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WPR; q++) acc += part[it2 * GV_WAVES + g * WPR + q];
             y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
         }
     }
@@ -494,6 +662,23 @@ int cu_count() {
 
 typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int);
 
+// Most blocks of one kernel resident per CU at a dynamic LDS size, cached per (kernel, LDS)
+int resident_blocks(GvKernel k, size_t smem) {
+    struct Entry {
+        GvKernel k;
+        size_t smem;
+        int v;
+    };
+    static Entry cache[64];
+    static int used = 0;
+    for (int i = 0; i < used; i++)
+        if (cache[i].k == k && cache[i].smem == smem) return cache[i].v;
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(k), GV_THREADS, smem) != hipSuccess || v < 1) v = 1;
+    if (used < 64) cache[used++] = Entry{k, smem, v};
+    return v;
+}
+
 template <uint32_t TY, int SPW, int WPR>
 hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
                        const float* res, float* y, int n, int n_out, int maxit_env, hipStream_t s) {
@@ -505,6 +690,21 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
     // the DMA variant needs 16-byte aligned rows and activation pieces
     const bool dma = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(xq) & 15) == 0 &&
                      !getenv("KF_GEMV_NO_DMA");
+    // the pipelined persistent variant: a resident grid, every wave walking its rows two in flight
+    if (SPW == 1 && dma && !getenv("KF_GEMV_NO_PIPE")) {
+        GvKernel k = gemv_pipe_kernel<TY, WPR>;
+        const size_t base_lds = gd_lds(TY, n, 0, WPR, 1, 1).total;
+        const char* e = getenv("KF_GEMV_BPC");
+        const int per_cu = e && atoi(e) > 0 ? atoi(e) : resident_blocks(k, base_lds + (WPR > 1 ? 2048 : 0));
+        int grid = cu_count() * per_cu;
+        if (grid > groups) grid = groups;
+        const int iters = (groups + grid - 1) / grid;
+        const size_t smem = gd_lds(TY, n, iters, WPR, 1, 1).total;
+        if (smem <= 65536) {
+            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters);
+            return hipGetLastError();
+        }
+    }
 #define KF_GV_IT(M)                                                                                                      \
     if (want <= M) {                                                                                                     \
         const int grid = (groups + M - 1) / M;                                                                           \
@@ -533,6 +733,10 @@ int gv_wpr(int steps) {
 }
 
 }  // namespace
+
+#ifdef KF_GV_TRACE
+extern "C" int kf_gv_set_trace(void* p) { return hipMemcpyToSymbol(HIP_SYMBOL(kf_gv_trace), &p, sizeof(p)) == hipSuccess ? 0 : -1; }
+#endif
 
 // Largest row width the single-row GEMV stages in LDS
 int kf_gemv_max_n() { return 32768; }
