@@ -85,6 +85,14 @@ int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void*
 int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                 int rows, int n, int n_out, void* stream);
 
+/* Batched / prefill int8 GEMM on q8_0 rows: y [rows][n_out] from `rows` activation rows of Q8_0 kind. One int8 MFMA
+ * per 32-column group gives the exact int32 block dots, rescaled by the group's activation and weight scales.
+ * Replaces kf8_gemm_dense / Store::gemm (crates/kf-backend-cuda/src/kernels/kf8.cu:375-395,
+ * crates/kf-backend-cuda/src/kf8.rs:310-323) without the KF8 unpack: the native q8_0 bytes are read directly.
+ * n must be a multiple of 128. */
+int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
+                   int rows, int n, int n_out, void* stream);
+
 /* The whole Op::MatMul of one weight: quantize x into `act` (device scratch of kf_hip_act_bytes(rows, n_in)) and run
  * the product the row count selects. Replaces matmul_launch (exec.rs:2061-2093). */
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,

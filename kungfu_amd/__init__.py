@@ -69,6 +69,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_gemv": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_matmul": ([U, P, I, I, P, I, P, P, P, P, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
+        "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_backend_new": ([I], P),
         "kf_hip_backend_free": ([P], None),
         "kf_hip_backend_add_weight": ([P, U, P, I, P, S], I),
@@ -169,6 +170,10 @@ def quant_act(x, act, kind: int, stream=None) -> None:
 
 def gemv(ty: int, w, act, y, rows: int, n: int, n_out: int, bias=None, res=None, stream=None) -> None:
     check(lib().kf_hip_gemv(ty, _ptr(w), row_bytes(ty, n), _ptr(act), _ptr(bias), _ptr(res), _ptr(y), rows, n, n_out, _stream(stream)))
+
+
+def gemm_i8(ty: int, w, act, y, rows: int, n: int, n_out: int, bias=None, res=None, stream=None) -> None:
+    check(lib().kf_hip_gemm_i8(ty, _ptr(w), row_bytes(ty, n), _ptr(act), _ptr(bias), _ptr(res), _ptr(y), rows, n, n_out, _stream(stream)))
 
 
 def matmul(ty: int, w, x, act, y, n_out: int, bias=None, res=None, stream=None) -> None:

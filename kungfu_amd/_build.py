@@ -18,11 +18,11 @@ LIB = os.path.join(OUT_DIR, "libkf_hip.so")
 OBJ_DIR = os.path.join(HERE, "build", "obj")
 
 ARCH = "gfx950"
-DEVICE_SOURCES = ["quant_act.hip", "gemv.hip"]
+DEVICE_SOURCES = ["quant_act.hip", "gemv.hip", "gemm.hip"]
 HOST_SOURCES = ["api.cpp", "host_quant.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
-DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-ffp-contract=fast"]
+DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-ffp-contract=fast-honor-pragmas"]
 
 
 def hipcc() -> str:

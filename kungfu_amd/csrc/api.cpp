@@ -21,6 +21,9 @@ hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const 
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
                                 int32_t* out, hipStream_t s);
 int kf_gemv_max_n();
+hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
+                               int N, int K, hipStream_t s);
+int kf_gemm_k_multiple();
 
 namespace {
 
@@ -136,6 +139,16 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
     return KF_OK;
 }
 
+int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
+                   int rows, int n, int n_out, void* stream) {
+    const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
+    if (rc != KF_OK) return rc;
+    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0 weights (type %u given)", ty);
+    if (n % kf_gemm_k_multiple() != 0) return fail(KF_E_INVALID, "%d columns, the GEMM needs a multiple of %d", n, kf_gemm_k_multiple());
+    const hipError_t e = kf_launch_gemm_q8_0(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
+}
+
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream) {
     int block, bytes;
@@ -146,6 +159,10 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
     if (rc != KF_OK) return rc;
     const int q = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
     if (q != KF_OK) return q;
+    // the row count picks the product, as matvec_rows / multi_kind do (exec.rs:1877-1945): one row is the GEMV;
+    // several q8_0 rows are the int8 GEMM, which reads each weight byte once per 128 rows
+    if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
+        return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
 }
 

@@ -10,6 +10,10 @@
 // eight lanes. The integer results are bit-exact with the CPU reference.
 #include "kf_device.h"
 
+// The reference rounds the f32 product v * id: with contraction, roundf's expansion (trunc, then p - trunc(p)) becomes
+// fma(v, id, -trunc(p)), which sees the unrounded product and turns ties such as 58.4999999 -> 58.5 into 58.
+#pragma clang fp contract(off)
+
 namespace {
 
 constexpr int QA_THREADS = 256;

@@ -59,6 +59,21 @@ def test_quant_act_bit_exact(cuda, kind, rows, n):
     assert np.array_equal(s32, ws[:, ::2] + ws[:, 1::2])
 
 
+def test_quant_act_hard_rounding_ties(cuda):
+    """Planted ties where the f32 product is k + 0.5 but the real product is below it (half of all elements)."""
+    import torch
+    from tie_inputs import hard_tie_rows
+
+    x, made = hard_tie_rows(16, 1024, seed=3)
+    assert made > 4000
+    act = kf.alloc_act(16, 1024, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8_0)
+    torch.cuda.synchronize()
+    q = kf.act_views(act, 16, 1024)[0].cpu().numpy()
+    wq, _, _ = oracle.quantize_activations(kf.ACT_Q8_0, x)
+    assert np.array_equal(q, wq), f"{(q != wq).sum()} of {q.size} differ"
+
+
 def _random_blocks(ty, n_out, n_in, rng):
     """Random block bytes with sane f16 scales (the harness of crates/kf-backend-cuda/tests/common/mod.rs:100-147)."""
     block, size = kf.BLOCK[ty]
@@ -225,3 +240,49 @@ def test_gemv_launch_variants(cuda, monkeypatch, dma, maxit, ty, n, n_out):
     kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+GEMM_SHAPES = [(2, 128, 64), (9, 1024, 1000), (130, 512, 200), (256, 4096, 384), (64, 14336, 96)]
+
+
+@pytest.mark.parametrize("rows,n,n_out", GEMM_SHAPES)
+def test_gemm_matches_cpu_backend(cuda, rows, n, n_out):
+    """The int8 MFMA GEMM (q8_0) against matmul_slice; ragged row and column counts exercise the tile edges."""
+    import torch
+
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=40 + rows)
+    x = kf.synth_normal(41 + rows, 1.0, rows * n).reshape(rows, n)
+    bias = kf.synth_normal(42, 1.0, n_out)
+    res = kf.synth_normal(43, 1.0, rows * n_out).reshape(rows, n_out)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8_0)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q8_0, _tensor(w, cuda), act, y, rows, n, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    want = oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res
+    _close(y.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
+def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
+    """Config C4 at full size (M = 2048): every 97th row of the GEMM against the GEMV of that row on the same
+    quantized activations (the GEMV is pinned to the CPU backend above); the CPU oracle is too slow at this size."""
+    import torch
+
+    rows = 2048
+    w = _tensor(_weights(kf.TYPE_Q8_0, n_out, n, seed=0), cuda)
+    x = _tensor(kf.synth_normal(1, 1.0, rows * n).reshape(rows, n), cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(x, act, kf.ACT_Q8_0)
+    y = torch.empty((rows, n_out), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q8_0, w, act, y, rows, n, n_out)
+    q, d16, s16, d32, s32 = kf.act_views(act, rows, n)
+    one = kf.alloc_act(1, n, cuda)
+    oq, od16, os16, od32, os32 = kf.act_views(one, 1, n)
+    yr = torch.empty((1, n_out), device=cuda)
+    for r in range(0, rows, 97):
+        for src, dst in ((q, oq), (d16, od16), (s16, os16), (d32, od32), (s32, os32)):
+            dst.copy_(src[r : r + 1])
+        kf.gemv(kf.TYPE_Q8_0, w, one, yr, 1, n, n_out)
+        torch.cuda.synchronize()
+        _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())

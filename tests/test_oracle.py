@@ -266,6 +266,20 @@ def test_quantize_activations_rounding_ties():
     assert list(q[0, :3]) == [-127, -2, -4] and d16[0, 0] == -1.0
 
 
+def test_quantize_activations_hard_ties_round_the_f32_product():
+    # v * id is exactly k + 0.5 in f32 while the real product is below it: the reference rounds the f32 product
+    from tie_inputs import hard_tie_rows
+
+    x, made = hard_tie_rows(2, 256, seed=1)
+    assert made > 200
+    q, _, _ = oracle.quantize_activations(3, x)
+    b = x.reshape(2, -1, 32)
+    idv = np.float32(1) / (np.abs(b).max(-1, keepdims=True) / np.float32(127)).astype(np.float32)
+    p = (b * idv).astype(np.float32)
+    want = (np.sign(p) * np.floor(np.abs(p) + np.float32(0.5))).astype(np.int8).reshape(2, -1)
+    assert np.array_equal(q, want)
+
+
 def test_quantize_activations_q8k_first_max_wins():
     x = np.zeros((2, 256), np.float32)
     x[0, 3], x[0, 10] = 5.0, -5.0   # +5 first: iscale = -127/5
