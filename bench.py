@@ -107,6 +107,62 @@ def time_launches(fn, iters):
     return time_graph(capture(fn, iters), 3) * 1e3 / iters
 
 
+PREFILL = [("gate_up", 4096, 14336), ("down", 14336, 4096)]
+SMALL_BATCH = [8, 16, 32, 64]
+
+
+def gemm_section(dev, m=2048):
+    """int8 MFMA GEMM of configs[3]: M=2048 Q8_0-kind activation rows against Q8_0 weights, both prefill shapes.
+    TOPS = 2*M*N*K / kernel time (the quant_act launch is timed beside it); two weight copies alternate."""
+    import torch
+
+    import kungfu_amd as kf
+
+    out = {}
+    for name, n, n_out in PREFILL:
+        w = torch.from_numpy(make_weights(kf.TYPE_Q8_0, n, n_out)).to(dev)
+        ws = [w, w.clone()]
+        x = torch.from_numpy(kf.synth_normal(1, 1.0, m * n).reshape(m, n)).to(dev)
+        act = kf.alloc_act(m, n, dev)
+        y = torch.empty((m, n_out), device=dev)
+        kf.quant_act(x, act, kf.ACT_Q8_0)
+        us = time_launches(lambda i: kf.gemm_i8(kf.TYPE_Q8_0, ws[i % 2], act, y, m, n, n_out), 20)
+        us_q = time_launches(lambda i: kf.quant_act(x, act, kf.ACT_Q8_0), 20)
+        tops = 2.0 * m * n * n_out / us / 1e6
+        out[name] = {"M": m, "K": n, "N": n_out, "us": round(us, 2), "TOPS": round(tops, 1),
+                     "frac": round(tops / INT8_PEAK_TOPS, 4), "quant_act_us": round(us_q, 2)}
+        del ws, w, x, act, y
+    return out
+
+
+def small_batch_section(dev):
+    """batch 8..64 of the Llama-3-8B shapes with Q8_0 weights: the product kernel alone on resident
+    quantized activations (µs per call, weight-streaming GB/s, TOPS) and the whole kf_hip_matmul (quant_act + product)."""
+    import torch
+
+    import kungfu_amd as kf
+
+    out = {}
+    for name, n, n_out in LAYER:
+        if name == "up":
+            continue
+        w = torch.from_numpy(make_weights(kf.TYPE_Q8_0, n, n_out)).to(dev)
+        ws = [w] + [w.clone() for _ in range(max(1, -(-2 * MALL_BYTES // w.numel())))]
+        res = {}
+        for m in SMALL_BATCH:
+            x = torch.from_numpy(kf.synth_normal(1, 1.0, m * n).reshape(m, n)).to(dev)
+            act = kf.alloc_act(m, n, dev)
+            y = torch.empty((m, n_out), device=dev)
+            kf.quant_act(x, act, kf.ACT_Q8_0)
+            us = time_launches(lambda i: kf.gemm_i8(kf.TYPE_Q8_0, ws[i % len(ws)], act, y, m, n, n_out), 50)
+            us_mm = time_launches(lambda i: kf.matmul(kf.TYPE_Q8_0, ws[i % len(ws)], x, act, y, n_out), 50)
+            res[str(m)] = {"us": round(us, 2), "GBs": round(gemv_bytes(kf.TYPE_Q8_0, n, n_out, m) / us / 1e3, 1),
+                           "TOPS": round(2.0 * m * n * n_out / us / 1e6, 2), "us_with_quant": round(us_mm, 2)}
+        out[name] = res
+        del ws, w
+    return out
+
+
 def cpu_baseline(shapes, budget_s):
     """The CPU backend's product (oracle restatement of ops::matmul_slice, OpenMP over output rows) on the same
     weights and input: whole layer passes until budget_s of wall time is spent."""
@@ -134,6 +190,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["gemm", "small"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -146,6 +203,9 @@ def main():
 
     dev = torch.device("cuda:0")
     kf.lib()
+    if args.only:
+        print(json.dumps(gemm_section(dev) if args.only == "gemm" else small_batch_section(dev)), flush=True)
+        return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
     copies = max(2, -(-2 * MALL_BYTES // layer_w_bytes) + 1)
     shapes = [Shape(nm, kf.TYPE_Q4_K, n, no, copies, dev) for nm, n, no in LAYER]
@@ -212,8 +272,10 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
         "shapes": per,
         "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1)},
-        "int8_gemm_tops": None,
     }
+    out["int8_gemm"] = gemm_section(dev)
+    out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
+    out["small_batch_q8_0"] = small_batch_section(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
     print(json.dumps(out), flush=True)

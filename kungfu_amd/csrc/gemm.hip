@@ -1,4 +1,4 @@
-// Prefill / batched int8 GEMM on native q8_0 weight bytes: y[m][n] = sum over 32-column groups g of
+// Batched / prefill int8 GEMM on native q8_0 weight bytes: y[m][n] = sum over 32-column groups g of
 // d_x[m][g] * d_w[n][g] * I_g[m][n] (+ bias[n] + res[m][n]), with I_g the exact int32 dot of the group.
 //
 // Replaces the reference's KF8 GEMM (crates/kf-backend-cuda/src/kernels/kf8.cu:116-395, host kf8.rs:258-323), which
@@ -6,17 +6,27 @@
 // already int8 with one f16 scale per 32) and only their 32 weight bytes are moved into LDS tiles.
 //
 // gfx950 design:
-//   * A block computes a 128 x 128 output tile with four waves of 64 x 64 (2 x 2 tiles of 32 x 32).
-//   * K advances 128 columns (four groups) per stage. Global loads of the next stage are in flight in registers
-//     while the current stage is multiplied from LDS; LDS is double-buffered, one barrier per stage.
-//   * LDS holds each 32 x 32 operand tile in MFMA operand order (lane l's 16 bytes at 16 * l), so every operand read
-//     is a contiguous 1 KB and bank-conflict free.
+//   * Four waves per block in a WM x WN grid, each computing TM x TN tiles of 32 x 32, so a block tile is
+//     (32 WM TM) x (32 WN TN): 128 x 128 for prefill, 32 x 128 / 64 x 128 for small batches.
+//   * K advances 128 columns (four groups) per stage. The next stage's global loads are in flight in registers while
+//     the current one is multiplied from LDS; LDS is double-buffered with one barrier per stage.
+//   * An operand tile of 32 rows x 32 bytes sits in LDS as two halves of 32 slots of 16 bytes, in the order the MFMA
+//     consumes (lane l reads slot l % 32 of half l / 32), with the slot XOR-swizzled by the piece's (group, half) so
+//     that both the row-contiguous stores and the operand reads hit 16 distinct bank quads per 16 lanes.
 //   * Per group and 32 x 32 tile: one v_mfma_i32_32x32x32_i8 gives the exact int32 dots I_g; one
 //     v_mfma_f32_32x32x16_f16 with a single non-zero k slot gives the exact outer product d_x (x) d_w of the group's
-//     f16 scales (q8_0 weight scales are f16, Q8_0-kind activation scales are f16-rounded); the VALU then converts
-//     I_g and accumulates with one FMA. The per-element rescale (a convert and an FMA per group) is the VALU work
-//     that bounds this GEMM, not the MFMA.
+//     f16 scales (q8_0 weight scales are f16, Q8_0-kind activation scales are f16-rounded); the VALU converts I_g and
+//     accumulates with one FMA. Those two VALU ops per output per group bound the kernel, not the MFMA: the VALU does
+//     64 lane-ops a clock per CU against the int8 MFMA's ~4096 multiply-adds, i.e. at most 32 outputs x 32 columns
+//     per clock, a quarter of the int8 peak.
+//   * Up to 64 rows (decode batches) the tile GEMM has too few tiles and too little in flight to stream the weights, so
+//     gemm_q8_0_small_kernel takes over: a block owns 32 output columns, its W waves split K among themselves, every
+//     lane loads its MFMA operand pieces straight from memory (no LDS staging) several groups ahead, and the waves'
+//     partial tiles are summed in LDS in a fixed tree order.
 #include "kf_device.h"
+
+#include <algorithm>
+#include <cstdlib>
 
 namespace {
 
@@ -24,153 +34,450 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int GM_BM = 128, GM_BN = 128, GM_BK = 128;  // tile sizes; BK spans four 32-column groups
+constexpr int GM_BK = 128;  // columns per stage: four 32-column groups
+constexpr int GM_G = GM_BK / 32;
 constexpr int GM_THREADS = 256;
-constexpr int GM_G = GM_BK / 32;  // groups per stage
-// LDS of one stage: A and B operand tiles (16 KB each) and f16 scales of A rows and B columns (1 KB each)
-constexpr int GM_A_BYTES = GM_BM * GM_BK, GM_B_BYTES = GM_BN * GM_BK;
-constexpr int GM_SA = GM_A_BYTES + GM_B_BYTES, GM_SB = GM_SA + GM_G * GM_BM * 2;
-constexpr int GM_STAGE = GM_SB + GM_G * GM_BN * 2;
 
-// Byte offset in an operand tile of the 16-byte piece (group g, row r of the 128, half h of the 32 columns):
-// tiles of 32 rows are stored as [half][row % 32] so a wave reads one tile as 64 consecutive 16-byte pieces
-__device__ __forceinline__ int gm_piece(int g, int r, int h) { return (((g * 4 + (r >> 5)) * 2 + h) * 32 + (r & 31)) * 16; }
-
-struct GmPrefetch {
-    uint4 a[4], b[4];
-    uint32_t dw[2];
-    float dx[2];
+template <int WM, int WN, int TM, int TN>
+struct GmCfg {
+    static_assert(WM * WN == 4, "four waves");
+    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+    static constexpr int A_BYTES = BM * GM_BK, B_BYTES = BN * GM_BK;
+    static constexpr int SA = A_BYTES + B_BYTES;          // f16 activation scales [g][BM]
+    static constexpr int SB = SA + GM_G * BM * 2;         // f16 weight scales [g][BN]
+    static constexpr int STAGE = SB + GM_G * BN * 2;
+    static constexpr int PA = BM * 8 / GM_THREADS;        // 16-byte pieces a thread moves per stage
+    static constexpr int PB = BN * 8 / GM_THREADS;
+    static constexpr int QA = (BM * GM_G + GM_THREADS - 1) / GM_THREADS;  // scales a thread moves per stage
+    static constexpr int QB = (BN * GM_G + GM_THREADS - 1) / GM_THREADS;
+    static_assert(PA >= 1 && PB >= 1, "a block tile spans at least 32 rows");
 };
 
+// Byte offset of the 16-byte piece (group g, tile row r, half h) in an operand tile of `tiles` 32-row tiles
+__device__ __forceinline__ int gm_slot(int tiles, int g, int r, int h) {
+    return (((g * tiles + (r >> 5)) * 2 + h) * 32 + ((r & 31) ^ ((g * 2 + h) << 1))) * 16;
+}
+
+// The piece a lane reads for the MFMA operand of tile t, group g: row lane % 32, half lane / 32
+__device__ __forceinline__ int gm_operand(int tiles, int g, int t, int lane) {
+    const int h = lane >> 5;
+    return (((g * tiles + t) * 2 + h) * 32 + ((lane & 31) ^ ((g * 2 + h) << 1))) * 16;
+}
+
+template <class C>
+struct GmStage {
+    uint4 a[C::PA], b[C::PB];
+    float dx[C::QA];
+    uint32_t dw[C::QB];
+
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                         const float* __restrict__ xd32, int m0, int n0, int M, int N, int K, int st, int tid) {
+        const int gb = st * GM_G;
+        const int kg = K >> 5;
+#pragma unroll
+        for (int i = 0; i < C::PA; i++) {
+            const int c = tid + GM_THREADS * i;  // eight consecutive threads read one row's 128 bytes
+            const int m = min(m0 + (c >> 3), M - 1);
+            a[i] = *reinterpret_cast<const uint4*>(xq + (int64_t)m * K + gb * 32 + (c & 7) * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < C::PB; i++) {
+            const int c = tid + GM_THREADS * i;
+            const int n = min(n0 + (c >> 3), N - 1);
+            const int p = c & 7;
+            const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(w + (int64_t)n * row_bytes + (int64_t)(gb + (p >> 1)) * KF_Q8_0_BYTES + 2 +
+                                                                  16 * (p & 1));
+            b[i] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+#pragma unroll
+        for (int i = 0; i < C::QA; i++) {
+            const int c = min(tid + GM_THREADS * i, C::BM * GM_G - 1);  // row c / 4, group c % 4
+            const int m = min(m0 + (c >> 2), M - 1);
+            dx[i] = xd32[(int64_t)m * kg + gb + (c & 3)];
+        }
+#pragma unroll
+        for (int i = 0; i < C::QB; i++) {
+            const int c = min(tid + GM_THREADS * i, C::BN * GM_G - 1);
+            const int n = min(n0 + (c >> 2), N - 1);
+            dw[i] = *reinterpret_cast<const uint16_t*>(w + (int64_t)n * row_bytes + (int64_t)(gb + (c & 3)) * KF_Q8_0_BYTES);
+        }
+    }
+
+    __device__ __forceinline__ void store(uint8_t* buf, int tid) const {
+#pragma unroll
+        for (int i = 0; i < C::PA; i++) {
+            const int c = tid + GM_THREADS * i;
+            const int p = c & 7;
+            *reinterpret_cast<uint4*>(buf + gm_slot(C::BM / 32, p >> 1, c >> 3, p & 1)) = a[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::PB; i++) {
+            const int c = tid + GM_THREADS * i;
+            const int p = c & 7;
+            *reinterpret_cast<uint4*>(buf + C::A_BYTES + gm_slot(C::BN / 32, p >> 1, c >> 3, p & 1)) = b[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::QA; i++) {
+            const int c = tid + GM_THREADS * i;
+            // Q8_0-kind activation scales are f16-rounded values, so this conversion is exact
+            if (c < C::BM * GM_G) reinterpret_cast<_Float16*>(buf + C::SA)[(c & 3) * C::BM + (c >> 2)] = (_Float16)dx[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::QB; i++) {
+            const int c = tid + GM_THREADS * i;
+            if (c < C::BN * GM_G) reinterpret_cast<uint16_t*>(buf + C::SB)[(c & 3) * C::BN + (c >> 2)] = (uint16_t)dw[i];
+        }
+    }
+};
+
+// One block: output tile (blockIdx.y, blockIdx.x) over all of K
+template <int WM, int WN, int TM, int TN>
 __global__ void __launch_bounds__(GM_THREADS, 2) gemm_q8_0_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                   const float* __restrict__ xd32, const float* __restrict__ bias,
                                                                   const float* __restrict__ res, float* __restrict__ y, int M, int N, int K) {
+    using C = GmCfg<WM, WN, TM, TN>;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int m0 = blockIdx.y * GM_BM, n0 = blockIdx.x * GM_BN;
-    const int kg = K >> 5;  // groups per row
-    const int stages = K / GM_BK;
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = blockIdx.y * C::BM, n0 = blockIdx.x * C::BN;
+    const int st0 = 0, st1 = K / GM_BK;
 
-    auto load = [&](GmPrefetch& p, int st) {
-        const int gb = st * GM_G;  // first group of the stage
+    v16f acc[TM][TN];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + GM_THREADS * i;  // 1024 pieces: row c / 8, group (c % 8) / 2, half c % 2
-            const int r = c >> 3, g = (c >> 1) & 3, h = c & 1;
-            const int m = min(m0 + r, M - 1), n = min(n0 + r, N - 1);
-            p.a[i] = *reinterpret_cast<const uint4*>(xq + (int64_t)m * K + (gb + g) * 32 + 16 * h);
-            p.b[i] = kf_load_stream_u4_unaligned(w + (int64_t)n * row_bytes + (int64_t)(gb + g) * KF_Q8_0_BYTES + 2 + 16 * h);
-        }
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = tid + GM_THREADS * i;  // 512 scales: row c / 4, group c % 4
-            const int r = c >> 2, g = c & 3;
-            const int m = min(m0 + r, M - 1), n = min(n0 + r, N - 1);
-            p.dx[i] = xd32[(int64_t)m * kg + gb + g];
-            p.dw[i] = *reinterpret_cast<const uint16_t*>(w + (int64_t)n * row_bytes + (int64_t)(gb + g) * KF_Q8_0_BYTES);
-        }
-    };
-    auto store = [&](const GmPrefetch& p, uint8_t* buf) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int c = tid + GM_THREADS * i;
-            const int r = c >> 3, g = (c >> 1) & 3, h = c & 1;
-            *reinterpret_cast<uint4*>(buf + gm_piece(g, r, h)) = p.a[i];
-            *reinterpret_cast<uint4*>(buf + GM_A_BYTES + gm_piece(g, r, h)) = p.b[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int c = tid + GM_THREADS * i;
-            const int r = c >> 2, g = c & 3;
-            // Q8_0-kind activation scales are f16-rounded values, so this conversion is exact
-            reinterpret_cast<_Float16*>(buf + GM_SA)[g * GM_BM + r] = (_Float16)p.dx[i];
-            reinterpret_cast<uint16_t*>(buf + GM_SB)[g * GM_BN + r] = (uint16_t)p.dw[i];
-        }
-    };
+        for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
 
-    v16f acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int j = 0; j < 2; j++) acc[i][j] = v16f{};
-
-    GmPrefetch pf;
-    load(pf, 0);
-    store(pf, smem);
+    GmStage<C> pf;
+    pf.load(w, row_bytes, xq, xd32, m0, n0, M, N, K, st0, tid);
+    pf.store(smem, tid);
     __syncthreads();
-    for (int st = 0; st < stages; st++) {
-        const uint8_t* buf = smem + (st & 1) * GM_STAGE;
-        if (st + 1 < stages) load(pf, st + 1);
+    for (int st = st0; st < st1; st++) {
+        const uint8_t* buf = smem + ((st - st0) & 1) * C::STAGE;
+        // the last stage reloads itself: an unconditional load keeps the prefetch registers out of any phi
+        pf.load(w, row_bytes, xq, xd32, m0, n0, M, N, K, min(st + 1, st1 - 1), tid);
 #pragma unroll 1
         for (int g = 0; g < GM_G; g++) {
-            v4i a[2], b[2];
-            v8h sa[2], sb[2];
+            v4i a[TM], b[TN];
+            v8h sa[TM], sb[TN];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                a[t] = *reinterpret_cast<const v4i*>(buf + gm_piece(g, (wm * 2 + t) * 32, 0) + 16 * lane);
-                b[t] = *reinterpret_cast<const v4i*>(buf + GM_A_BYTES + gm_piece(g, (wn * 2 + t) * 32, 0) + 16 * lane);
+            for (int t = 0; t < TM; t++) {
+                a[t] = *reinterpret_cast<const v4i*>(buf + gm_operand(C::BM / 32, g, wm * TM + t, lane));
                 sa[t] = v8h{};
-                sb[t] = v8h{};
-                if (lane < 32) {
-                    sa[t][0] = reinterpret_cast<const _Float16*>(buf + GM_SA)[g * GM_BM + (wm * 2 + t) * 32 + lane];
-                    sb[t][0] = reinterpret_cast<const _Float16*>(buf + GM_SB)[g * GM_BN + (wn * 2 + t) * 32 + lane];
-                }
+                if (lane < 32) sa[t][0] = reinterpret_cast<const _Float16*>(buf + C::SA)[g * C::BM + (wm * TM + t) * 32 + lane];
             }
 #pragma unroll
-            for (int i = 0; i < 2; i++) {
-                v16i c[2];
-                v16f s[2];
+            for (int t = 0; t < TN; t++) {
+                b[t] = *reinterpret_cast<const v4i*>(buf + C::A_BYTES + gm_operand(C::BN / 32, g, wn * TN + t, lane));
+                sb[t] = v8h{};
+                if (lane < 32) sb[t][0] = reinterpret_cast<const _Float16*>(buf + C::SB)[g * C::BN + (wn * TN + t) * 32 + lane];
+            }
 #pragma unroll
-                for (int j = 0; j < 2; j++) {
+            for (int i = 0; i < TM; i++) {
+                v16i c[TN];
+                v16f s[TN];
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
                     c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
                     s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa[i], sb[j], v16f{}, 0, 0, 0);
                 }
 #pragma unroll
-                for (int j = 0; j < 2; j++)
+                for (int j = 0; j < TN; j++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)c[j][r], s[j][r], acc[i][j][r]);
             }
         }
-        if (st + 1 < stages) store(pf, smem + ((st + 1) & 1) * GM_STAGE);
+        if (st + 1 < st1) pf.store(smem + ((st + 1 - st0) & 1) * C::STAGE, tid);
         __syncthreads();
     }
 
     // 32 x 32 accumulator layout: lane l holds column l % 32; register r holds row (r % 4) + 8 * (r / 4) + 4 * (l / 32)
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int n = n0 + (wn * 2 + j) * 32 + (lane & 31);
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + (wn * TN + j) * 32 + (lane & 31);
             if (n >= N) continue;
             const float bn = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + (wm * 2 + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
-                if (m < M) y[(int64_t)m * N + n] = acc[i][j][r] + bn + (res ? res[(int64_t)m * N + n] : 0.0f);
+                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
             }
         }
 }
 
+// Decode-batch product (up to MR activation rows). Block x owns 32 output columns [32 x, +32); its W waves take the
+// 8-group chunks of K round-robin. A chunk is 272 bytes of each of the 32 weight rows (17 aligned 16-byte pieces, so a
+// wave's loads cover about four rows each); the next chunk is in flight in registers while the current one is
+// multiplied out of the wave's own LDS region (row stride 304 bytes, 76 dwords: consecutive rows start on distinct
+// bank quads). Per group, 16 x 16 tile pair and activation tile, one v_mfma_i32_16x16x32_i8 gives the int32 dots (the
+// weight operand read from LDS at its 2-byte aligned address, the activation operand loaded from memory in MFMA order:
+// lane l holds row l % 16, bytes [8 (l / 16), +8) of the group, reused for both weight tiles) and one
+// v_mfma_f32_16x16x16_f16 the outer product of the f16 scales. The waves' partial tiles are summed by a fixed-order
+// tree in LDS.
+typedef long v1l;
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef int v4i_ __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+
+// Ablation switch for measurement builds only (0 in the product): bit 1 drops the MFMA/VALU arithmetic, bit 2 the
+// LDS staging and operand reads, bit 4 the activation loads
+#ifndef KF_SK_ABLATE
+#define KF_SK_ABLATE 0
+#endif
+constexpr int SK_G = 8;                        // groups per chunk
+constexpr int SK_WB = SK_G * KF_Q8_0_BYTES;    // 272 weight bytes per row per chunk
+constexpr int SK_WP = SK_WB / 16;              // 17 pieces
+constexpr int SK_STRIDE = 304;                 // LDS row stride
+constexpr int SK_TN = 2;                       // 16-column weight tiles of a wave
+constexpr int SK_ROWS = 16 * SK_TN;            // weight rows of a wave
+constexpr int SK_WI = (SK_ROWS * SK_WP + 63) / 64;  // 9 load instructions for the weights
+constexpr int SK_WAVE_LDS = SK_ROWS * SK_STRIDE;    // 9728 bytes: also holds one partial tile (TM x TN x 1 KB)
+
+// The activation operands and scales of one chunk, loaded together when the chunk starts (they are small and stay
+// in L2, shared by every block)
+template <int MR>
+struct SkAct {
+    static constexpr int TM = MR / 16;  // 16-row activation tiles
+    uint32_t aq[TM][SK_G][2];           // this lane's 8 activation bytes of each tile and group
+    v4f dx[TM][2];                      // the scales of this lane's activation row (lanes < 16 use them)
+
+    __device__ __forceinline__ void load(const int8_t* __restrict__ xq, const float* __restrict__ xd32, const uint32_t (&aoff)[TM],
+                                         const uint32_t (&doff)[TM], int ch) {
+        typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+        const uint32_t ab = (uint32_t)ch * SK_G * 32;
+#pragma unroll
+        for (int t = 0; t < TM; t++) {
+#pragma unroll
+            for (int g = 0; g < SK_G; g++) {
+                const v2u v = *reinterpret_cast<const v2u*>(xq + (aoff[t] + ab + 32 * g));
+                aq[t][g][0] = v.x;
+                aq[t][g][1] = v.y;
+            }
+            dx[t][0] = *reinterpret_cast<const v4f*>(xd32 + doff[t] + ch * SK_G);
+            dx[t][1] = *reinterpret_cast<const v4f*>(xd32 + doff[t] + ch * SK_G + 4);
+        }
+    }
+};
+
+template <int MR>
+__global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
+                                                                               const int8_t* __restrict__ xq, const float* __restrict__ xd32,
+                                                                               const float* __restrict__ bias, const float* __restrict__ res,
+                                                                               float* __restrict__ y, int M, int N, int K) {
+    constexpr int TM = SkAct<MR>::TM;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int W = blockDim.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint8_t* lw = smem + wave * SK_WAVE_LDS;
+    const int n0 = blockIdx.x * SK_ROWS, m0 = blockIdx.y * MR;
+    const int q = lane >> 4, c = lane & 15;  // operand k-quarter and row/column
+    const int kg = K >> 5;
+    const int chunks = kg / SK_G;  // K % 256 == 0: whole chunks
+
+    // weight piece p = 64 i + lane is row p / 17, piece p % 17 (clamped: duplicates of the last piece). Byte offsets
+    // fit in 32 bits (the launcher checks the weight and activation sizes).
+    uint32_t woff[SK_WI];
+#pragma unroll
+    for (int i = 0; i < SK_WI; i++) {
+        const int p = min(64 * i + lane, SK_ROWS * SK_WP - 1);
+        woff[i] = (uint32_t)min(n0 + p / SK_WP, N - 1) * (uint32_t)row_bytes + 16 * (p % SK_WP);
+    }
+    uint32_t aoff[TM], doff[TM];
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+        const int m = min(m0 + 16 * t + c, M - 1);
+        aoff[t] = (uint32_t)m * (uint32_t)K + 8 * q;
+        doff[t] = (uint32_t)m * (uint32_t)kg;
+    }
+
+    v4f acc[TM][SK_TN];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int j = 0; j < SK_TN; j++) acc[t][j] = v4f{};
+    // software pipeline over this wave's chunks. Loads complete in issue order (one vmcnt counter), so each
+    // iteration issues chunk j+1's activations before its weights: multiplying chunk j then needs nothing in flight,
+    // and the next iteration's single wait (for chunk j+1's weights) covers both. LDS operations of one wave complete
+    // in order, so no barrier separates the staging from the reads, nor the reads of chunk j from the staging of j+1.
+    v4u wq[SK_WI];
+    auto load_w = [&](int chk) {
+        const uint32_t wb = (uint32_t)chk * SK_WB;
+#pragma unroll
+        for (int i = 0; i < SK_WI; i++) wq[i] = *reinterpret_cast<const v4u*>(w + (woff[i] + wb));
+    };
+    int ch = wave;
+    SkAct<MR> nact;
+    nact.load(xq, xd32, aoff, doff, min(ch, chunks - 1));
+    load_w(min(ch, chunks - 1));
+    for (; ch < chunks; ch += W) {
+        if (!(KF_SK_ABLATE & 2)) {
+#pragma unroll
+            for (int i = 0; i < SK_WI; i++) {
+                const int p = min(64 * i + lane, SK_ROWS * SK_WP - 1);
+                *reinterpret_cast<v4u*>(lw + (p / SK_WP) * SK_STRIDE + 16 * (p % SK_WP)) = wq[i];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < SK_WI; i++) acc[0][0][0] += __builtin_bit_cast(float, wq[i].x ^ wq[i].w);
+        }
+        const SkAct<MR> act = nact;
+        if (ch + W < chunks) {  // uniform
+            if (!(KF_SK_ABLATE & 4)) nact.load(xq, xd32, aoff, doff, ch + W);
+            load_w(ch + W);
+        }
+
+#pragma unroll
+        for (int g = 0; g < SK_G; g++) {
+            if (KF_SK_ABLATE & 3) {
+                if (!(KF_SK_ABLATE & 2)) acc[0][0][0] += __builtin_bit_cast(float, *reinterpret_cast<const uint32_t*>(lw + c * SK_STRIDE + 34 * g));
+                acc[0][0][1] += __builtin_bit_cast(float, act.aq[0][g][0]);
+                continue;
+            }
+            long b[SK_TN];
+            v4h sb[SK_TN];
+#pragma unroll
+            for (int j = 0; j < SK_TN; j++) {
+                const uint8_t* wp = lw + (16 * j + c) * SK_STRIDE + g * KF_Q8_0_BYTES;
+                const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
+                b[j] = (long)bv.x | ((long)bv.y << 32);
+                sb[j] = v4h{};
+                sb[j][0] = q == 0 ? *reinterpret_cast<const _Float16*>(wp) : (_Float16)0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                const long a = (long)act.aq[t][g][0] | ((long)act.aq[t][g][1] << 32);
+                const float d = act.dx[t][g >> 2][g & 3];
+                v4h sa = v4h{};
+                sa[0] = q == 0 ? (_Float16)d : (_Float16)0.0f;  // f16-rounded scales: exact
+#pragma unroll
+                for (int j = 0; j < SK_TN; j++) {
+                    const v4i_ ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b[j], v4i_{}, 0, 0, 0);
+                    const v4f sc = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, sb[j], v4f{}, 0, 0, 0);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[t][j][k] = fmaf((float)ci[k], sc[k], acc[t][j][k]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the groups apart: bounded registers
+        }
+    }
+
+    // fixed-order tree over the waves (W a power of two): the upper half stores its tile, the lower half adds
+    __syncthreads();
+    for (int half = W / 2; half >= 1; half >>= 1) {
+        if (wave >= half && wave < 2 * half) {
+            float* p = reinterpret_cast<float*>(smem + (wave - half) * SK_WAVE_LDS) + lane;
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+#pragma unroll
+                for (int j = 0; j < SK_TN; j++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) p[((t * SK_TN + j) * 4 + k) * 64] = acc[t][j][k];
+        }
+        __syncthreads();
+        if (wave < half) {
+            const float* p = reinterpret_cast<const float*>(smem + wave * SK_WAVE_LDS) + lane;
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+#pragma unroll
+                for (int j = 0; j < SK_TN; j++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[t][j][k] += p[((t * SK_TN + j) * 4 + k) * 64];
+        }
+        __syncthreads();
+    }
+    if (wave != 0) return;
+    // 16 x 16 accumulator layout: lane l holds column l % 16, register k holds row 4 (l / 16) + k
+#pragma unroll
+    for (int j = 0; j < SK_TN; j++) {
+        const int n = n0 + 16 * j + c;
+        if (n >= N) continue;
+        const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int m = m0 + 16 * t + 4 * q + k;
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[t][j][k] + bn + (res ? res[o] : 0.0f);
+            }
+    }
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res, float* y,
+                       int M, int N, int K, hipStream_t s) {
+    using C = GmCfg<WM, WN, TM, TN>;
+    auto* fn = gemm_q8_0_kernel<WM, WN, TM, TN>;
+    static bool lds_set = false;  // the double-buffered stage needs more than the default 64 KB of LDS
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, 2 * C::STAGE);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    dim3 grid((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
+    fn<<<grid, GM_THREADS, 2 * C::STAGE, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
+}
+
+template <int MR>
+hipError_t gemm_small_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
+                             float* y, int M, int N, int K, int W, hipStream_t s) {
+    static_assert(SK_WAVE_LDS >= SkAct<MR>::TM * SK_TN * 4 * 64 * 4, "a wave region holds a partial tile");
+    auto* fn = gemm_q8_0_small_kernel<MR>;
+    static bool lds_set = false;
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, 8 * SK_WAVE_LDS);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    fn<<<dim3((N + SK_ROWS - 1) / SK_ROWS, (M + MR - 1) / MR), 64 * W, W * SK_WAVE_LDS, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
+}
+
+// Waves per block of the small-batch kernel: enough blocks x waves to fill the GPU (about 4096 waves), at least two
+// chunks a wave, a power of two; KF_GEMM_SMALL_W overrides it (a tuning knob)
+int small_waves(int M, int N, int K) {
+    static const int forced = [] {
+        const char* e = getenv("KF_GEMM_SMALL_W");
+        return e ? atoi(e) : 0;
+    }();
+    const int cap = 8;
+    const int rblocks = (M + 15) / 16;
+    if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
+    const int tiles = (N + SK_ROWS - 1) / SK_ROWS, chunks = K / 256;
+    int w = 1;
+    while (w < cap && tiles * rblocks * w < 4096 && chunks / (2 * w) >= 2) w *= 2;
+    return w;
+}
+
 }  // namespace
+
+int kf_gemm_k_multiple() { return GM_BK; }
 
 // Host launcher, validated by the caller (api.cpp): K a multiple of 128, Q8_0-kind activations in `act`
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s) {
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
     const char* base = static_cast<const char*>(act);
-    dim3 grid((N + GM_BN - 1) / GM_BN, (M + GM_BM - 1) / GM_BM);
-    static bool lds_set = false;  // the double-buffered stage needs 68 KB of LDS per block
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_q8_0_kernel), hipFuncAttributeMaxDynamicSharedMemorySize, 2 * GM_STAGE);
-        if (e != hipSuccess) return e;
-        lds_set = true;
+    const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
+    const auto* xd = reinterpret_cast<const float*>(base + o.d32);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    // the small-batch kernel reads whole 16-byte pieces of rows, which needs 16-byte aligned rows (K % 256 == 0)
+    if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31)) {
+        const int wv = small_waves(M, N, K);
+        if (M <= 16) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);
+        if (M <= 64) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);  // M / 16 row blocks
     }
-    gemm_q8_0_kernel<<<grid, GM_THREADS, 2 * GM_STAGE, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
-                                                           reinterpret_cast<const float*>(base + o.d32), bias, res, y, M, N, K);
-    return hipGetLastError();
+    return gemm_launch<2, 2, 2, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
 }
-
-int kf_gemm_k_multiple() { return GM_BK; }

@@ -242,7 +242,9 @@ def test_gemv_launch_variants(cuda, monkeypatch, dma, maxit, ty, n, n_out):
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
 
 
-GEMM_SHAPES = [(2, 128, 64), (9, 1024, 1000), (130, 512, 200), (256, 4096, 384), (64, 14336, 96)]
+GEMM_SHAPES = [(2, 128, 64), (9, 1024, 1000), (130, 512, 200), (256, 4096, 384), (64, 14336, 96), (8, 14336, 520),
+               (33, 4096, 300), (48, 2048, 136), (16, 4096, 4096), (64, 4096, 4160),
+               (1, 512, 40), (65, 1024, 130)]
 
 
 @pytest.mark.parametrize("rows,n,n_out", GEMM_SHAPES)
