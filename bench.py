@@ -163,6 +163,40 @@ def small_batch_section(dev):
     return out
 
 
+def moe_section(dev, seed=0):
+    """the routed expert layer (kf_hip_moe_ffn) for 8 Q4_K experts of gate/up 4096->14336 and down
+    14336->4096, 16 tokens, top-2 uniform without replacement. GB/s over the weight bytes of the touched experts (each
+    read once per call) plus the fp32 activations in and out; two copies of the expert set alternate (1.6 GB)."""
+    import numpy as np
+    import torch
+
+    import kungfu_amd as kf
+
+    ty, n_exp, n_embd, n_ff, rows, n_used = kf.TYPE_Q4_K, 8, 4096, 14336, 16, 2
+    mats = []
+    for i, (n_out, n_in) in enumerate([(n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff)]):
+        w = torch.from_numpy(make_weights(ty, n_in, n_exp * n_out, seed=10 + i)).to(dev)
+        mats.append([w, w.clone()])
+    rng = np.random.default_rng(seed)
+    sel = np.stack([rng.choice(n_exp, n_used, replace=False) for _ in range(rows)]).astype(np.int32)
+    wts = rng.uniform(0.1, 1.0, sel.shape).astype(np.float32)
+    x = torch.from_numpy(kf.synth_normal(1, 1.0, rows * n_embd).reshape(rows, n_embd)).to(dev)
+    s_, w_ = torch.from_numpy(sel).to(dev), torch.from_numpy(wts).to(dev)
+    scratch = torch.empty(kf.moe_scratch_bytes(rows, n_used, n_embd, n_ff, n_exp), dtype=torch.uint8, device=dev)
+    out = torch.empty((rows, n_embd), device=dev)
+
+    def call(i):
+        kf.moe_ffn(ty, mats[0][i % 2], mats[1][i % 2], mats[2][i % 2], n_exp, n_embd, n_ff, x, s_, w_, out, scratch)
+
+    us = time_launches(call, 20)
+    touched = len(np.unique(sel))
+    wbytes = touched * (2 * n_ff * kf.row_bytes(ty, n_embd) + n_embd * kf.row_bytes(ty, n_ff))
+    nbytes = wbytes + 4 * rows * n_embd * 2
+    del mats
+    return {"us": round(us, 2), "GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "touched_experts": touched, "weight_bytes": wbytes, "tokens": rows, "top_k": n_used}
+
+
 def cpu_baseline(shapes, budget_s):
     """The CPU backend's product (oracle restatement of ops::matmul_slice, OpenMP over output rows) on the same
     weights and input: whole layer passes until budget_s of wall time is spent."""
@@ -190,7 +224,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "small"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "small", "moe"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -204,7 +238,8 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        print(json.dumps(gemm_section(dev) if args.only == "gemm" else small_batch_section(dev)), flush=True)
+        sec = {"gemm": gemm_section, "small": small_batch_section, "moe": moe_section}[args.only]
+        print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
     copies = max(2, -(-2 * MALL_BYTES // layer_w_bytes) + 1)
@@ -276,6 +311,7 @@ def main():
     out["int8_gemm"] = gemm_section(dev)
     out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
     out["small_batch_q8_0"] = small_batch_section(dev)
+    out["moe_q4_k"] = moe_section(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
     print(json.dumps(out), flush=True)

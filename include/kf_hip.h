@@ -79,9 +79,10 @@ int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void*
  * bias [n_out] and res [rows][n_out] are nullable device pointers. The weight base must be 16-byte aligned and
  * row_bytes must equal the type's row size for n (rows are packed). */
 
-/* Decode and small-batch product of `rows` activation rows. Replaces matvec_i8_launch (exec.rs:1996-2039) with the
- * kernels matvec_i8 / matvec_i8_1 / matvec_i8_1s / mm_i8_{8,16,32} / mm_frag_{8,16,24,32}
- * (crates/kf-backend-cuda/src/kernels/quant.cuh:604-627, mm_frag.cuh:294-300). */
+/* Decode and small-batch product of `rows` activation rows: one row is the streaming GEMV, several rows the
+ * multi-row product that reads each weight row once per eight activation rows. Replaces matvec_i8_launch
+ * (exec.rs:1996-2039) with the kernels matvec_i8 / matvec_i8_1 / matvec_i8_1s / mm_i8_{8,16,32} /
+ * mm_frag_{8,16,24,32} (crates/kf-backend-cuda/src/kernels/quant.cuh:604-627, mm_frag.cuh:294-300). */
 int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                 int rows, int n, int n_out, void* stream);
 
@@ -97,6 +98,41 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
  * the product the row count selects. Replaces matmul_launch (exec.rs:2061-2093). */
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream);
+
+/* ---------------------------------------------------------------------------------------------------------------
+ * MoE grouped experts (Op::MoeFfn with routed pairs: rows x n_used pairs rj = r * n_used + j, slot sel[rj] < 0 =
+ * unused). Expert matrices are stacked: expert e's rows start at base + e * expert_bytes.
+ * The CPU meaning is moe::exec / expert_forward (crates/kf-backend-cpu/src/moe.rs:66-107,110-257). */
+
+/* Pairs grouped by slot: offsets[s] .. offsets[s + 1] index `order`, which lists the pair indices of slot s in
+ * increasing order (deterministic; the reference's atomic placement leaves it unspecified). offsets has n_slots + 1
+ * entries; slots outside [0, n_slots) are skipped. Replaces moe_group (crates/kf-backend-cuda/src/kernels/moe.cu:118-141). */
+int kf_hip_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, void* stream);
+
+/* Grouped expert product: for each slot s and each pair p of its group, y[p][o] = W_s[o] . x, x the activation row p
+ * (per_slot != 0) or p / n_used of `act` (act_rows rows of n columns, quantized with the weight type's kind). Each
+ * expert row is read once per group (eight pairs at a time). With w_up non-null the gate (w) and up (w_up) experts
+ * are multiplied together and y[p][o] = silu(gate . x) * (up . x). Replaces moe_matvec_i8 / moe_gate_up_i8
+ * (crates/kf-backend-cuda/src/kernels/quant.cuh:519-581, launches exec.rs:2208-2237), which read each expert once
+ * per pair. n at most 16384 (q4_K) or 8192 (q8_0). */
+int kf_hip_moe_gemv(uint32_t ty, const void* w, const void* w_up, int64_t expert_bytes, int64_t row_bytes, const void* act, int act_rows, int n,
+                    int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int n_used, int per_slot, float* y, void* stream);
+
+/* out[r][o] = sum over j of wts[rj] * scale * part[rj][o] for the row's pairs with slots[rj] >= 0, in j order, plus
+ * host[r][o] (nullable). Replaces moe_combine (moe.cu:153-164). */
+int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used, int n_embd,
+                       float scale, void* stream);
+
+/* Device scratch of one kf_hip_moe_ffn call. No reference counterpart (the reference sizes its per-node scratch in
+ * the plan). */
+size_t kf_hip_moe_scratch_bytes(int rows, int n_used, int n_embd, int n_ff, int n_slots);
+
+/* The routed expert layer with silu gating: quantize x, group the pairs, fused gate/up product, quantize the hidden
+ * rows, down product, weighted combine. gate and up are [n_slots][n_ff][row of n_embd], down [n_slots][n_embd][row
+ * of n_ff], all of type ty. out [rows][n_embd]. Replaces expert_launches (crates/kf-backend-cuda/src/exec.rs:2378-2386)
+ * for int8-capable experts resident on the device. */
+int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* down, int n_slots, int n_embd, int n_ff, const float* x, int rows,
+                   const int32_t* sel, const float* wts, int n_used, float scale, void* scratch, size_t scratch_bytes, float* out, void* stream);
 
 /* Per-block int32 results of n_out weight rows against the `rows` activation rows of `act`: q8_0 one int32 per 32-block
  * (out [n_out][rows][n/32]); q4_K (sumi, mins) per super-block (out [n_out][rows][n/256][2]). The integers of

@@ -70,6 +70,11 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_matmul": ([U, P, I, I, P, I, P, P, P, P, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
         "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
+        "kf_hip_moe_group": ([P, I, I, P, P, P], I),
+        "kf_hip_moe_gemv": ([U, P, P, L64, L64, P, I, I, I, P, P, I, I, I, P, P], I),
+        "kf_hip_moe_combine": ([P, P, P, P, P, I, I, I, ctypes.c_float, P], I),
+        "kf_hip_moe_scratch_bytes": ([I, I, I, I, I], S),
+        "kf_hip_moe_ffn": ([U, P, P, P, I, I, I, P, I, P, P, I, ctypes.c_float, P, S, P, P], I),
         "kf_hip_backend_new": ([I], P),
         "kf_hip_backend_free": ([P], None),
         "kf_hip_backend_add_weight": ([P, U, P, I, P, S], I),
@@ -183,6 +188,32 @@ def matmul(ty: int, w, x, act, y, n_out: int, bias=None, res=None, stream=None) 
 
 def block_ints(ty: int, w, act, out, rows: int, n: int, n_out: int, stream=None) -> None:
     check(lib().kf_hip_block_ints(ty, _ptr(w), row_bytes(ty, n), _ptr(act), rows, n, n_out, _ptr(out), _stream(stream)))
+
+
+def moe_group(slots, total: int, n_slots: int, order, offsets, stream=None) -> None:
+    check(lib().kf_hip_moe_group(_ptr(slots), total, n_slots, _ptr(order), _ptr(offsets), _stream(stream)))
+
+
+def moe_gemv(ty: int, w, act, act_rows: int, n: int, n_out: int, order, offsets, n_slots: int, n_used: int, per_slot: bool, y,
+             w_up=None, expert_bytes: int | None = None, stream=None) -> None:
+    eb = row_bytes(ty, n) * n_out if expert_bytes is None else expert_bytes
+    check(lib().kf_hip_moe_gemv(ty, _ptr(w), _ptr(w_up), eb, row_bytes(ty, n), _ptr(act), act_rows, n, n_out, _ptr(order), _ptr(offsets),
+                                n_slots, n_used, int(per_slot), _ptr(y), _stream(stream)))
+
+
+def moe_combine(part, wts, slots, out, rows: int, n_used: int, n_embd: int, scale: float = 1.0, host=None, stream=None) -> None:
+    check(lib().kf_hip_moe_combine(_ptr(part), _ptr(wts), _ptr(slots), _ptr(host), _ptr(out), rows, n_used, n_embd, scale, _stream(stream)))
+
+
+def moe_scratch_bytes(rows: int, n_used: int, n_embd: int, n_ff: int, n_slots: int) -> int:
+    return lib().kf_hip_moe_scratch_bytes(rows, n_used, n_embd, n_ff, n_slots)
+
+
+def moe_ffn(ty: int, gate, up, down, n_slots: int, n_embd: int, n_ff: int, x, sel, wts, out, scratch, scale: float = 1.0, stream=None) -> None:
+    """The routed expert layer (kf_hip_moe_ffn): x [rows][n_embd] f32, sel/wts [rows][n_used] int32/f32, out [rows][n_embd]."""
+    rows, n_used = sel.shape
+    check(lib().kf_hip_moe_ffn(ty, _ptr(gate), _ptr(up), _ptr(down), n_slots, n_embd, n_ff, _ptr(x), rows, _ptr(sel), _ptr(wts), n_used, scale,
+                               _ptr(scratch), scratch.numel() * scratch.element_size(), _ptr(out), _stream(stream)))
 
 
 def alloc_act(rows: int, n: int, device="cuda"):

@@ -24,6 +24,13 @@ int kf_gemv_max_n();
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s);
 int kf_gemm_k_multiple();
+int kf_rows_max_n(uint32_t ty);
+hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, const void* act, int act_rows,
+                          int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used, int per_slot,
+                          const float* bias, const float* res, float* y, hipStream_t s);
+hipError_t kf_launch_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, hipStream_t s);
+hipError_t kf_launch_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used,
+                                 int n_embd, float scale, hipStream_t s);
 
 namespace {
 
@@ -128,6 +135,11 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
     const kf_act_offsets o = kf_act_layout((size_t)rows, (size_t)n);
     const char* base = static_cast<const char*>(act);
     hipStream_t s = static_cast<hipStream_t>(stream);
+    // several rows: each weight row streamed once against up to eight staged activation rows
+    if (rows > 1 && n <= kf_rows_max_n(ty)) {
+        const hipError_t e = kf_launch_rows(ty, w, nullptr, 0, row_bytes, act, rows, n, n_out, nullptr, nullptr, 1, rows, 1, 1, bias, res, y, s);
+        return e == hipSuccess ? KF_OK : hip_fail(e, "rows launch");
+    }
     for (int r = 0; r < rows; r++) {
         const int8_t* xq = reinterpret_cast<const int8_t*>(base + o.q) + (size_t)r * n;
         const int32_t* xs32 = reinterpret_cast<const int32_t*>(base + o.s32) + (size_t)r * (n / 32);
@@ -164,6 +176,99 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
     if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
         return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+}
+
+int kf_hip_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, void* stream) {
+    if (total < 0 || n_slots < 1) return fail(KF_E_INVALID, "%d pairs over %d slots", total, n_slots);
+    if (n_slots > 16384) return fail(KF_E_UNSUPPORTED, "%d slots (at most 16384)", n_slots);
+    if ((total > 0 && (!slots || !order)) || !offsets) return fail(KF_E_INVALID, "null slot, order or offset pointer");
+    const hipError_t e = kf_launch_moe_group(slots, total, n_slots, order, offsets, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "moe_group launch");
+}
+
+int kf_hip_moe_gemv(uint32_t ty, const void* w, const void* w_up, int64_t expert_bytes, int64_t row_bytes, const void* act, int act_rows, int n,
+                    int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int n_used, int per_slot, float* y, void* stream) {
+    const int rc = check_product(ty, w, row_bytes, act, y, act_rows, n, n_out);
+    if (rc != KF_OK) return rc;
+    if (w_up && !aligned(w_up, 16)) return fail(KF_E_INVALID, "up weight base must be 16-byte aligned");
+    if (!order || !offsets || n_slots < 1 || n_used < 1) return fail(KF_E_INVALID, "null order/offsets or %d slots, %d used", n_slots, n_used);
+    if (expert_bytes < (int64_t)n_out * row_bytes || expert_bytes % 16 != 0)
+        return fail(KF_E_INVALID, "expert stride %lld for %d rows of %lld bytes (16-byte multiple)", (long long)expert_bytes, n_out, (long long)row_bytes);
+    if (n > kf_rows_max_n(ty)) return fail(KF_E_UNSUPPORTED, "%d columns above the %d of the grouped product", n, kf_rows_max_n(ty));
+    const hipError_t e = kf_launch_rows(ty, w, w_up, expert_bytes, row_bytes, act, act_rows, n, n_out, order, offsets, n_slots, 0, n_used,
+                                        per_slot ? 1 : 0, nullptr, nullptr, y, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "moe product launch");
+}
+
+int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used, int n_embd,
+                       float scale, void* stream) {
+    if (rows < 0 || n_used < 1 || n_embd < 0) return fail(KF_E_INVALID, "%d rows, %d used, %d columns", rows, n_used, n_embd);
+    if (rows > 0 && n_embd > 0 && (!part || !wts || !slots || !out)) return fail(KF_E_INVALID, "null combine pointer");
+    const hipError_t e = kf_launch_moe_combine(part, wts, slots, host, out, rows, n_used, n_embd, scale, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "moe_combine launch");
+}
+
+namespace {
+// Scratch of one MoE layer: x activations | order | offsets | hidden f32 | hidden activations | pair outputs
+struct MoeScratch {
+    size_t xact, order, offsets, hidden, hact, part, total;
+};
+MoeScratch moe_scratch(int rows, int n_used, int n_embd, int n_ff, int n_slots) {
+    MoeScratch m{};
+    const size_t pairs = (size_t)rows * n_used;
+    size_t at = 0;
+    m.xact = at;
+    at += kf_align_up(kf_act_layout((size_t)rows, (size_t)n_embd).total, 256);
+    m.order = at;
+    at += kf_align_up(pairs * 4, 256);
+    m.offsets = at;
+    at += kf_align_up(((size_t)n_slots + 1) * 4, 256);
+    m.hidden = at;
+    at += kf_align_up(pairs * n_ff * 4, 256);
+    m.hact = at;
+    at += kf_align_up(kf_act_layout(pairs, (size_t)n_ff).total, 256);
+    m.part = at;
+    at += kf_align_up(pairs * n_embd * 4, 256);
+    m.total = at;
+    return m;
+}
+}  // namespace
+
+size_t kf_hip_moe_scratch_bytes(int rows, int n_used, int n_embd, int n_ff, int n_slots) {
+    if (rows < 0 || n_used < 1 || n_embd < 0 || n_ff < 0 || n_slots < 1) return 0;
+    return moe_scratch(rows, n_used, n_embd, n_ff, n_slots).total;
+}
+
+int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* down, int n_slots, int n_embd, int n_ff, const float* x, int rows,
+                   const int32_t* sel, const float* wts, int n_used, float scale, void* scratch, size_t scratch_bytes, float* out, void* stream) {
+    int block, bytes;
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12)", ty);
+    if (rows < 1 || n_used < 1 || n_slots < 1) return fail(KF_E_INVALID, "%d rows, %d used of %d slots", rows, n_used, n_slots);
+    if (n_embd <= 0 || n_ff <= 0 || n_embd % block != 0 || n_ff % block != 0) return fail(KF_E_INVALID, "%d / %d columns against blocks of %d", n_embd, n_ff, block);
+    if (!gate || !up || !down || !x || !sel || !wts || !scratch || !out) return fail(KF_E_INVALID, "null MoE pointer");
+    const MoeScratch m = moe_scratch(rows, n_used, n_embd, n_ff, n_slots);
+    if (scratch_bytes < m.total) return fail(KF_E_INVALID, "scratch of %zu bytes, the layer needs %zu", scratch_bytes, m.total);
+    if (!aligned(scratch, 256)) return fail(KF_E_INVALID, "scratch must be 256-byte aligned");
+    const int64_t rb_in = (int64_t)(n_embd / block) * bytes, rb_ff = (int64_t)(n_ff / block) * bytes;
+    const int64_t eb_gu = kf_align_up((size_t)(n_ff * rb_in), 16), eb_dn = kf_align_up((size_t)(n_embd * rb_ff), 16);
+    if (eb_gu != (int64_t)n_ff * rb_in || eb_dn != (int64_t)n_embd * rb_ff)
+        return fail(KF_E_UNSUPPORTED, "expert matrices must be whole multiples of 16 bytes");
+    char* base = static_cast<char*>(scratch);
+    void* xact = base + m.xact;
+    auto* order = reinterpret_cast<int32_t*>(base + m.order);
+    auto* offsets = reinterpret_cast<int32_t*>(base + m.offsets);
+    auto* hidden = reinterpret_cast<float*>(base + m.hidden);
+    void* hact = base + m.hact;
+    auto* part = reinterpret_cast<float*>(base + m.part);
+    const int pairs = rows * n_used;
+    int rc = kf_hip_quant_act(x, xact, rows, n_embd, kind_of(ty), stream);
+    if (rc == KF_OK) rc = kf_hip_moe_group(sel, pairs, n_slots, order, offsets, stream);
+    if (rc == KF_OK)
+        rc = kf_hip_moe_gemv(ty, gate, up, eb_gu, rb_in, xact, rows, n_embd, n_ff, order, offsets, n_slots, n_used, 0, hidden, stream);
+    if (rc == KF_OK) rc = kf_hip_quant_act(hidden, hact, pairs, n_ff, kind_of(ty), stream);
+    if (rc == KF_OK) rc = kf_hip_moe_gemv(ty, down, nullptr, eb_dn, rb_ff, hact, pairs, n_ff, n_embd, order, offsets, n_slots, n_used, 1, part, stream);
+    if (rc == KF_OK) rc = kf_hip_moe_combine(part, wts, sel, nullptr, out, rows, n_used, n_embd, scale, stream);
+    return rc;
 }
 
 int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out, int32_t* out,

@@ -66,6 +66,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.kfo_matmul_slice.argtypes = [U, P, I, I, P, I, P, P, I]
     L.kfo_matmul_i8.argtypes = [U, P, I, I, P, I, P, P, I]
     L.kfo_moe_ffn.argtypes = [U, P, P, P, I, I, I, P, I, P, P, I, P, I]
+    L.kfo_moe_ffn_i8.argtypes = [U, P, P, P, I, I, I, P, I, P, P, I, P, I]
     L.kfo_silu.argtypes = [ctypes.c_float]
     L.kfo_silu.restype = ctypes.c_float
 
@@ -201,6 +202,20 @@ def moe_ffn(ty, gate, up, down, n_exp, n_embd, n_ff, x, sel, wts, threads: int =
     out = np.zeros((rows, n_embd), np.float32)
     rc = lib().kfo_moe_ffn(ty, _p(_c(gate, np.uint8)), _p(_c(up, np.uint8)), _p(_c(down, np.uint8)), n_exp, n_embd, n_ff,
                            _p(x), rows, _p(sel), _p(wts), n_used, _p(out), threads)
+    assert rc == 0, rc
+    return out
+
+
+def moe_ffn_i8(ty, gate, up, down, n_exp, n_embd, n_ff, x, sel, wts, threads: int = 0) -> np.ndarray:
+    """experts::hidden_rows + down_cols: the int8 expert path (the GPU's arithmetic)."""
+    x = _c(np.atleast_2d(x), np.float32)
+    rows = x.shape[0]
+    sel = _c(sel, np.int32)
+    wts = _c(wts, np.float32)
+    n_used = sel.shape[1]
+    out = np.zeros((rows, n_embd), np.float32)
+    rc = lib().kfo_moe_ffn_i8(ty, _p(_c(gate, np.uint8)), _p(_c(up, np.uint8)), _p(_c(down, np.uint8)), n_exp, n_embd, n_ff,
+                              _p(x), rows, _p(sel), _p(wts), n_used, _p(out), threads)
     assert rc == 0, rc
     return out
 

@@ -583,3 +583,41 @@ int kfo_moe_ffn(uint32_t ty, const uint8_t* gate, const uint8_t* up, const uint8
     free(g); free(u); free(h); free(ye); free(xq);
     return rc;
 }
+
+/* The int8 expert path of the CPU backend, hidden_rows then down_cols (crates/kf-backend-cpu/src/experts.rs:93-124):
+ * gate and up by dot_i8 on the quantized input row, hidden = silu(g) * u (ops::gated with Act::Silu, ops.rs:46-60),
+ * the hidden row quantized again (Rows::new, experts.rs:48-53) and the down product by dot_i8; out[r] accumulates
+ * wts * y in selection order. */
+int kfo_moe_ffn_i8(uint32_t ty, const uint8_t* gate, const uint8_t* up, const uint8_t* down, int n_exp, int n_embd, int n_ff,
+                   const float* x, int rows, const int32_t* sel, const float* wts, int n_used, float* out, int threads) {
+    int block, size;
+    if (kfo_type_info(ty, &block, &size) != 0 || n_embd % block != 0 || n_ff % block != 0) return -1;
+    size_t rb_in = (size_t)(n_embd / block) * size, rb_ff = (size_t)(n_ff / block) * size;
+    float* g = (float*)malloc(sizeof(float) * n_ff);
+    float* u = (float*)malloc(sizeof(float) * n_ff);
+    float* h = (float*)malloc(sizeof(float) * n_ff);
+    float* ye = (float*)malloc(sizeof(float) * n_embd);
+    if (!g || !u || !h || !ye) return -2;
+    int rc = 0;
+    for (int r = 0; r < rows && rc == 0; r++) {
+        float* acc = out + (size_t)r * n_embd;
+        for (int o = 0; o < n_embd; o++) acc[o] = 0.0f;
+        const float* xr = x + (size_t)r * n_embd;
+        for (int k = 0; k < n_used && rc == 0; k++) {
+            int e = sel[r * n_used + k];
+            if (e < 0) continue;
+            if (e >= n_exp) {
+                rc = -1;
+                break;
+            }
+            rc |= kfo_matmul_i8(ty, gate + (size_t)e * n_ff * rb_in, n_embd, n_ff, xr, 1, NULL, g, threads);
+            rc |= kfo_matmul_i8(ty, up + (size_t)e * n_ff * rb_in, n_embd, n_ff, xr, 1, NULL, u, threads);
+            for (int o = 0; o < n_ff; o++) h[o] = kfo_silu(g[o]) * u[o];
+            rc |= kfo_matmul_i8(ty, down + (size_t)e * n_embd * rb_ff, n_ff, n_embd, h, 1, NULL, ye, threads);
+            float wv = wts[r * n_used + k];
+            for (int o = 0; o < n_embd; o++) acc[o] += wv * ye[o];
+        }
+    }
+    free(g); free(u); free(h); free(ye);
+    return rc;
+}

@@ -79,6 +79,10 @@ int kfo_matmul_i8(uint32_t ty, const uint8_t* w, int n_in, int n_out, const floa
 int kfo_moe_ffn(uint32_t ty, const uint8_t* gate, const uint8_t* up, const uint8_t* down, int n_exp, int n_embd, int n_ff,
                 const float* x, int rows, const int32_t* sel, const float* wts, int n_used, float* out, int threads);
 
+/* The CPU backend's int8 expert path, experts::hidden_rows then down_cols, silu gating, out = sum of wts * y in
+ * selection order. */
+int kfo_moe_ffn_i8(uint32_t ty, const uint8_t* gate, const uint8_t* up, const uint8_t* down, int n_exp, int n_embd, int n_ff,
+                   const float* x, int rows, const int32_t* sel, const float* wts, int n_used, float* out, int threads);
 /* ops::silu */
 float kfo_silu(float x);
 

@@ -374,3 +374,34 @@ def test_moe_ffn_composition():
         scale = np.abs(want).max() + 1e-3
         assert np.abs(out[r] - want).max() <= 2e-3 * scale, r
     assert not out[3].any()
+
+
+def test_moe_ffn_i8_is_the_int8_composition_and_near_the_float_path():
+    """experts::hidden_rows + down_cols: per pair, gate/up by matmul_i8, silu(g) * u, down by matmul_i8 on the hidden
+    row, weighted in selection order; and within the reference's own int8-vs-float bound of the float path
+    (crates/kf-backend-cpu/src/experts.rs:181-217: 2e-2 of the mean magnitude)."""
+    rng = np.random.default_rng(8)
+    n_exp, n_embd, n_ff, rows, used = 3, 256, 512, 4, 2
+    gate = _random_q4k(rng, n_exp * n_ff, n_embd)
+    up = _random_q4k(rng, n_exp * n_ff, n_embd)
+    down = _random_q4k(rng, n_exp * n_embd, n_ff)
+    x = rng.standard_normal((rows, n_embd)).astype(np.float32)
+    sel = np.array([[0, 2], [1, -1], [2, 1], [-1, -1]], np.int32)
+    wts = rng.uniform(0.1, 1, (rows, used)).astype(np.float32)
+    out = oracle.moe_ffn_i8(12, gate, up, down, n_exp, n_embd, n_ff, x, sel, wts)
+    for r in range(rows):
+        want = np.zeros(n_embd, np.float32)
+        for k in range(used):
+            e = sel[r, k]
+            if e < 0:
+                continue
+            g = oracle.matmul_i8(12, gate[e * n_ff : (e + 1) * n_ff], n_embd, n_ff, x[r])[0]
+            u = oracle.matmul_i8(12, up[e * n_ff : (e + 1) * n_ff], n_embd, n_ff, x[r])[0]
+            h = np.array([oracle.silu(float(v)) for v in g], np.float32) * u
+            y = oracle.matmul_i8(12, down[e * n_embd : (e + 1) * n_embd], n_ff, n_embd, h)[0]
+            want = want + wts[r, k] * y
+        assert np.array_equal(out[r], want), r
+    flt = oracle.moe_ffn(12, gate, up, down, n_exp, n_embd, n_ff, x, sel, wts)
+    live = np.abs(flt[:3]).mean()
+    assert np.abs(out - flt).max() <= 2e-2 * live
+    assert not out[3].any()
