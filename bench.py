@@ -197,6 +197,40 @@ def moe_section(dev, seed=0):
             "touched_experts": touched, "weight_bytes": wbytes, "tokens": rows, "top_k": n_used}
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.md")
+
+
+def traffic_section(dev):
+    """The dispatches the traffic counters are read on: a device copy of exactly 256 MiB (the calibration: it must
+    fetch and write 256 MiB) and three gate GEMV launches (Q4_K 4096 -> 14336, distinct weight copies), no graph."""
+    import torch
+
+    import kungfu_amd as kf
+
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    src.fill_(1)
+    dst = torch.empty_like(src)
+    sh = Shape("gate", kf.TYPE_Q4_K, 4096, 14336, 4, dev)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        dst.copy_(src)
+    for i in range(3):
+        sh.gemv(i + 1)
+    torch.cuda.synchronize()
+    return {"copy_bytes": src.numel(), "gemv_algorithmic_bytes": sh.bytes}
+
+
+def read_traffic():
+    """HBM bytes per gate GEMV launch from the committed counter summary (null when it is absent)."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(shapes, budget_s):
     """The CPU backend's product (oracle restatement of ops::matmul_slice, OpenMP over output rows) on the same
     weights and input: whole layer passes until budget_s of wall time is spent."""
@@ -224,7 +258,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "small", "moe"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "small", "moe", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -238,7 +272,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "small": small_batch_section, "moe": moe_section}[args.only]
+        sec = {"gemm": gemm_section, "small": small_batch_section, "moe": moe_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -276,7 +310,7 @@ def main():
         us_mm = time_launches(sh.matmul, 200)
         per[sh.name] = {"n_in": sh.n, "n_out": sh.n_out, "us": round(us, 3), "GBs": round(sh.bytes / us / 1e3, 1),
                         "frac": round(sh.bytes / us / 1e3 / HBM_PEAK_GBS, 4), "us_with_quant": round(us_mm, 3)}
-        if sh.n <= 4096:  # the launches of the one-wave-per-row q4_K kernel, which take most of the step's time
+        if sh.n_out == 14336:  # gate and up: gemv_pipe_kernel<q4_K, one wave a row>, the largest share of the step
             k1_bytes += sh.bytes
             k1_us += us
     achieved = k1_bytes / k1_us / 1e3
@@ -302,9 +336,10 @@ def main():
         "config": {"workload": "Q4_K decode GEMV, Llama-3-8B layer shapes, batch 1 (QKV, O, gate, up, down)",
                    "bytes_per_step": step_bytes, "weight_copies": copies,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_pipe_kernel<q4_K, 1 wave per row> (QKV, O, gate, up launches)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_pipe_kernel<q4_K, one wave a row> (gate and up launches)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "algorithmic_bytes": gemv_bytes(kf.TYPE_Q4_K, 4096, 14336)},
         "shapes": per,
         "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1)},
     }

@@ -124,12 +124,14 @@ struct GmStage {
         for (int i = 0; i < C::QA; i++) {
             const int c = tid + GM_THREADS * i;
             // Q8_0-kind activation scales are f16-rounded values, so this conversion is exact
-            if (c < C::BM * GM_G) reinterpret_cast<_Float16*>(buf + C::SA)[(c & 3) * C::BM + (c >> 2)] = (_Float16)dx[i];
+            if (C::QA * GM_THREADS == C::BM * GM_G || c < C::BM * GM_G)
+                reinterpret_cast<_Float16*>(buf + C::SA)[(c & 3) * C::BM + (c >> 2)] = (_Float16)dx[i];
         }
 #pragma unroll
         for (int i = 0; i < C::QB; i++) {
             const int c = tid + GM_THREADS * i;
-            if (c < C::BN * GM_G) reinterpret_cast<uint16_t*>(buf + C::SB)[(c & 3) * C::BN + (c >> 2)] = (uint16_t)dw[i];
+            if (C::QB * GM_THREADS == C::BN * GM_G || c < C::BN * GM_G)
+                reinterpret_cast<uint16_t*>(buf + C::SB)[(c & 3) * C::BN + (c >> 2)] = (uint16_t)dw[i];
         }
     }
 };
@@ -161,36 +163,48 @@ __global__ void __launch_bounds__(GM_THREADS, 2) gemm_q8_0_kernel(const uint8_t*
         const uint8_t* buf = smem + ((st - st0) & 1) * C::STAGE;
         // the last stage reloads itself: an unconditional load keeps the prefetch registers out of any phi
         pf.load(w, row_bytes, xq, xd32, m0, n0, M, N, K, min(st + 1, st1 - 1), tid);
-#pragma unroll 1
-        for (int g = 0; g < GM_G; g++) {
+        // the operands of group g + 1 are read from LDS while group g is multiplied and rescaled; the scale operands
+        // of the outer-product MFMA carry one f16 in k slot 0 (lanes < 32; lanes >= 32 hold k slots 8..15) and
+        // zeros elsewhere, and only their first dword changes from group to group
+        struct Ops {
             v4i a[TM], b[TN];
-            v8h sa[TM], sb[TN];
+            uint32_t sa[TM], sb[TN];
+        };
+        auto read_ops = [&](Ops& o, int g) {
 #pragma unroll
             for (int t = 0; t < TM; t++) {
-                a[t] = *reinterpret_cast<const v4i*>(buf + gm_operand(C::BM / 32, g, wm * TM + t, lane));
-                sa[t] = v8h{};
-                if (lane < 32) sa[t][0] = reinterpret_cast<const _Float16*>(buf + C::SA)[g * C::BM + (wm * TM + t) * 32 + lane];
+                o.a[t] = *reinterpret_cast<const v4i*>(buf + gm_operand(C::BM / 32, g, wm * TM + t, lane));
+                const uint16_t v = reinterpret_cast<const uint16_t*>(buf + C::SA)[g * C::BM + (wm * TM + t) * 32 + (lane & 31)];
+                o.sa[t] = lane < 32 ? v : 0u;
             }
 #pragma unroll
             for (int t = 0; t < TN; t++) {
-                b[t] = *reinterpret_cast<const v4i*>(buf + C::A_BYTES + gm_operand(C::BN / 32, g, wn * TN + t, lane));
-                sb[t] = v8h{};
-                if (lane < 32) sb[t][0] = reinterpret_cast<const _Float16*>(buf + C::SB)[g * C::BN + (wn * TN + t) * 32 + lane];
+                o.b[t] = *reinterpret_cast<const v4i*>(buf + C::A_BYTES + gm_operand(C::BN / 32, g, wn * TN + t, lane));
+                o.sb[t] = reinterpret_cast<const uint16_t*>(buf + C::SB)[g * C::BN + (wn * TN + t) * 32 + (lane & 31)];
             }
+        };
+        Ops cur;
+        read_ops(cur, 0);
+#pragma unroll 1
+        for (int g = 0; g < GM_G; g++) {
+            Ops nxt;
+            read_ops(nxt, min(g + 1, GM_G - 1));
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 v16i c[TN];
                 v16f s[TN];
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
-                    c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
-                    s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(sa[i], sb[j], v16f{}, 0, 0, 0);
+                    c[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[i], cur.b[j], v16i{}, 0, 0, 0);
+                    const v4u sa = {cur.sa[i], 0u, 0u, 0u}, sb = {cur.sb[j], 0u, 0u, 0u};
+                    s[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, sa), __builtin_bit_cast(v8h, sb), v16f{}, 0, 0, 0);
                 }
 #pragma unroll
                 for (int j = 0; j < TN; j++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)c[j][r], s[j][r], acc[i][j][r]);
             }
+            cur = nxt;
         }
         if (st + 1 < st1) pf.store(smem + ((st + 1 - st0) & 1) * C::STAGE, tid);
         __syncthreads();

@@ -18,6 +18,8 @@
 
 #include "kf_blocks.h"
 
+#include <algorithm>
+
 namespace {
 
 #ifndef KF_GV_THREADS
@@ -27,6 +29,10 @@ namespace {
 // arithmetic by a XOR of the parked bytes, 4 skips parking the weights in LDS (2 and 4 give wrong results by design)
 #ifndef KF_GV_ABLATE
 #define KF_GV_ABLATE 0
+#endif
+// rows a wave of the pipelined variant holds in flight (2, 3 or 4); KF_GEMV_DEPTH overrides it (a tuning knob)
+#ifndef KF_GV_DEPTH
+#define KF_GV_DEPTH 2
 #endif
 // row iterations a block holds in flight at once (1, 2 or 4)
 #ifndef KF_GV_MAXIT
@@ -458,7 +464,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
 // multiplied, the loads of rows i+1 and i+2 are in flight, so the arithmetic of a wave overlaps its own weight stream
 // (a wave that computes only after all its loads land holds its slot while the memory pipe idles). The activation
 // row reaches LDS by DMA before any weight is requested.
-template <uint32_t TY, int WPR>
+template <uint32_t TY, int WPR, int D>
 __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                                const float* __restrict__ bias, const float* __restrict__ res,
@@ -485,7 +491,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     {
         const int nchunks = n >> 4, n32 = n >> 5;
         const int nsw = (nchunks + 255) / 256;
-        if (wave < nsw) {
+        if (!(KF_GV_ABLATE & 1) && wave < nsw) {
             const uint4* gq = reinterpret_cast<const uint4*>(xq);
             uint4 v[4];
             int32_t sv[2];
@@ -543,10 +549,12 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         return w + (int64_t)o * row_bytes + at;
     };
     auto process = [&](const uint4* v, int it) {
-        gv_park<TY>(wb, v, len, ln);
+        if (!(KF_GV_ABLATE & 4)) gv_park<TY>(wb, v, len, ln);
         __builtin_amdgcn_wave_barrier();
         float acc = 0.0f;
-        if (has_step && blk < nblk) {
+        if (KF_GV_ABLATE & 2) {
+            acc = (KF_GV_ABLATE & 4) ? (float)(v[0].x ^ v[1].y ^ v[2].z) : (float)(*reinterpret_cast<const uint32_t*>(wl) ^ xl[0].x);
+        } else if (has_step && blk < nblk) {
             if constexpr (TY == KF_TYPE_Q4_K)
                 acc = gv_q4k_lane(wl, xl, ss, sd, blk, j);
             else
@@ -561,26 +569,30 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         }
     };
 
-    // the first two rows' weights go out before the block waits on its activation row; vmcnt counts loads in issue
-    // order, so waiting until only those weight loads are outstanding means the activation DMA has landed
-    uint4 a[GV_PIECES], b[GV_PIECES];
-    gv_load_step<TY>(a, row_ptr(0), len, ln);
-    gv_load_step<TY>(b, row_ptr(1), len, ln);
-    // wave 0's activation stores are LDS writes of this block only: waiting on lgkmcnt and a bare barrier order them
+    // the first D rows' weights go out before the block waits on its activation row; vmcnt counts loads in issue
+    // order, so waiting until only those weight loads are outstanding means the activation loads have landed
+    uint4 ring[D][GV_PIECES];
+#pragma unroll
+    for (int k = 0; k < D; k++) gv_load_step<TY>(ring[k], row_ptr(k), len, ln);
+    // the activation stores are LDS writes of this block only: waiting on lgkmcnt and a bare barrier order them
     // (__syncthreads would add a release fence that waits on the weight loads as well)
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
     __builtin_amdgcn_s_barrier();
     KF_GV_STAMP(1)
+    // a ring of D rows in flight: row it is multiplied while rows it+1 .. it+D-1 stream, then its registers take row
+    // it+D
     int it = 0;
-    for (; it + 2 < iters; it += 2) {
-        process(a, it);
-        gv_load_step<TY>(a, row_ptr(it + 2), len, ln);
-        process(b, it + 1);
-        gv_load_step<TY>(b, row_ptr(it + 3), len, ln);
+    for (; it + D < iters; it += D) {
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            process(ring[k], it + k);
+            gv_load_step<TY>(ring[k], row_ptr(it + k + D), len, ln);
+        }
     }
-    process(a, it);
     KF_GV_STAMP(2)
-    if (it + 1 < iters) process(b, it + 1);
+#pragma unroll
+    for (int k = 0; k < D; k++)
+        if (it + k < iters) process(ring[k], it + k);
     KF_GV_STAMP(3)
 
     if (WPR > 1) {
@@ -690,12 +702,29 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
     // the DMA variant needs 16-byte aligned rows and activation pieces
     const bool dma = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(xq) & 15) == 0 &&
                      !getenv("KF_GEMV_NO_DMA");
+    // one row a wave (WPR == 1) and every block resident at once: one-shot waves, each fetching its row straight into
+    // LDS (nothing to pipeline: the whole matrix is requested at launch)
+    if (SPW == 1 && WPR == 1 && dma && maxit_env == 0 && !getenv("KF_GEMV_NO_ONESHOT")) {
+        const size_t smem = gd_lds(TY, n, 1, WPR, 1, 1).total;
+        GvKernel k = gemv_dma_kernel<TY, 1, WPR, 1>;
+        if (groups <= cu_count() * resident_blocks(k, smem) && smem <= 65536) {
+            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1);
+            return hipGetLastError();
+        }
+    }
     // the pipelined persistent variant: a resident grid, every wave walking its rows two in flight
     if (SPW == 1 && dma && !getenv("KF_GEMV_NO_PIPE")) {
-        GvKernel k = gemv_pipe_kernel<TY, WPR>;
+        static const int depth = [] {
+            const char* e = getenv("KF_GEMV_DEPTH");
+            const int v = e ? atoi(e) : 0;
+            return v >= 2 && v <= 4 ? v : KF_GV_DEPTH;
+        }();
+        GvKernel k = depth == 4 ? gemv_pipe_kernel<TY, WPR, 4> : depth == 3 ? gemv_pipe_kernel<TY, WPR, 3> : gemv_pipe_kernel<TY, WPR, 2>;
         const size_t base_lds = gd_lds(TY, n, 0, WPR, 1, 1).total;
+        // two blocks (16 waves) per CU measured best on MI355X (3.9-4.1 TB/s at 33 MB against 3.2-3.5 with every
+        // resident slot filled, where waves contend for the memory pipe); KF_GEMV_BPC overrides it
         const char* e = getenv("KF_GEMV_BPC");
-        const int per_cu = e && atoi(e) > 0 ? atoi(e) : resident_blocks(k, base_lds + (WPR > 1 ? 2048 : 0));
+        const int per_cu = e && atoi(e) > 0 ? atoi(e) : std::min(2, resident_blocks(k, base_lds + (WPR > 1 ? 2048 : 0)));
         int grid = cu_count() * per_cu;
         if (grid > groups) grid = groups;
         const int iters = (groups + grid - 1) / grid;
