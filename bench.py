@@ -1,7 +1,9 @@
 """Benchmark of the MI355X-native quantized linear-layer hot path (one JSON line on stdout).
 
 Workload: the Q4_K decode GEMV at the Llama-3-8B layer shapes, batch 1 — one step is one
-decoder layer's linear products: QKV 4096->6144, O 4096->4096, gate 4096->14336, up 4096->14336, down 14336->4096.
+decoder layer's linear products: QKV 4096->6144, O 4096->4096, gate and up 4096->14336 each, down 14336->4096. Gate
+and up share their input, so their weights are stored as one [2 * 14336][row] tensor and run as one launch (the same
+bytes and outputs as two launches; the layout a loader chooses when it reads the two GGUF tensors).
 Weights are N(0, 0.02) from SplitMix64/Box-Muller (seed 0) quantized to Q4_K super-blocks; x is N(0, 1) (seed 1).
 Inputs are resident in HBM; the activations are quantized once before the timed region (the quant_act launch is timed
 separately and reported beside). Weight copies rotate over more than 2x the 256 MB Infinity Cache so every call
@@ -23,7 +25,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 MALL_BYTES = 256 << 20
-LAYER = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096)]
+LAYER = [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate_up", 4096, 2 * 14336), ("down", 14336, 4096)]
 METRIC = "Q4_K GEMV GB/s (% of HBM peak) + int8 GEMM TOPS, 1×MI355X"
 
 
@@ -143,9 +145,7 @@ def small_batch_section(dev):
     import kungfu_amd as kf
 
     out = {}
-    for name, n, n_out in LAYER:
-        if name == "up":
-            continue
+    for name, n, n_out in [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate", 4096, 14336), ("down", 14336, 4096)]:
         w = torch.from_numpy(make_weights(kf.TYPE_Q8_0, n, n_out)).to(dev)
         ws = [w] + [w.clone() for _ in range(max(1, -(-2 * MALL_BYTES // w.numel())))]
         res = {}
@@ -197,12 +197,12 @@ def moe_section(dev, seed=0):
             "touched_experts": touched, "weight_bytes": wbytes, "tokens": rows, "top_k": n_used}
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.md")
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_up_traffic.md")
 
 
 def traffic_section(dev):
     """The dispatches the traffic counters are read on: a device copy of exactly 256 MiB (the calibration: it must
-    fetch and write 256 MiB) and three gate GEMV launches (Q4_K 4096 -> 14336, distinct weight copies), no graph."""
+    fetch and write 256 MiB) and three gate+up GEMV launches (Q4_K 4096 -> 28672, distinct weight copies), no graph."""
     import torch
 
     import kungfu_amd as kf
@@ -210,7 +210,7 @@ def traffic_section(dev):
     src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     src.fill_(1)
     dst = torch.empty_like(src)
-    sh = Shape("gate", kf.TYPE_Q4_K, 4096, 14336, 4, dev)
+    sh = Shape("gate_up", kf.TYPE_Q4_K, 4096, 2 * 14336, 4, dev)
     torch.cuda.synchronize()
     for _ in range(3):
         dst.copy_(src)
@@ -221,7 +221,7 @@ def traffic_section(dev):
 
 
 def read_traffic():
-    """HBM bytes per gate GEMV launch from the committed counter summary (null when it is absent)."""
+    """HBM bytes per gate+up GEMV launch from the committed counter summary (null when it is absent)."""
     try:
         for line in open(TRAFFIC_PROFILE):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -310,7 +310,7 @@ def main():
         us_mm = time_launches(sh.matmul, 200)
         per[sh.name] = {"n_in": sh.n, "n_out": sh.n_out, "us": round(us, 3), "GBs": round(sh.bytes / us / 1e3, 1),
                         "frac": round(sh.bytes / us / 1e3 / HBM_PEAK_GBS, 4), "us_with_quant": round(us_mm, 3)}
-        if sh.n_out == 14336:  # gate and up: gemv_pipe_kernel<q4_K, one wave a row>, the largest share of the step
+        if sh.name == "gate_up":  # gemv_pipe_kernel<q4_K, one wave a row>, the largest share of the step
             k1_bytes += sh.bytes
             k1_us += us
     achieved = k1_bytes / k1_us / 1e3
@@ -333,13 +333,13 @@ def main():
         "vs_baseline": None,
         "dtype": "int8 x q4_K (int32 dot, f32 scale)",
         "data": "synthetic: SplitMix64/Box-Muller N(0,0.02) weights quantized to Q4_K, N(0,1) activations",
-        "config": {"workload": "Q4_K decode GEMV, Llama-3-8B layer shapes, batch 1 (QKV, O, gate, up, down)",
+        "config": {"workload": "Q4_K decode GEMV, Llama-3-8B layer shapes, batch 1 (QKV, O, gate+up as one [28672] tensor, down)",
                    "bytes_per_step": step_bytes, "weight_copies": copies,
                    "hbm_frac": round(value / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "gemv_pipe_kernel<q4_K, one wave a row> (gate and up launches)",
+        "roofline": {"bound": "hbm", "kernel": "gemv_pipe_kernel<q4_K, one wave a row> (the gate+up launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "algorithmic_bytes": gemv_bytes(kf.TYPE_Q4_K, 4096, 14336)},
+                     "algorithmic_bytes": gemv_bytes(kf.TYPE_Q4_K, 4096, 2 * 14336)},
         "shapes": per,
         "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1)},
     }

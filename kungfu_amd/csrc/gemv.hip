@@ -586,7 +586,8 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
 #pragma unroll
         for (int k = 0; k < D; k++) {
             process(ring[k], it + k);
-            gv_load_step<TY>(ring[k], row_ptr(it + k + D), len, ln);
+            // only rows this wave owns: a reload past them would fetch its last row again (a uniform branch)
+            if (it + k + D < iw) gv_load_step<TY>(ring[k], row_ptr(it + k + D), len, ln);
         }
     }
     KF_GV_STAMP(2)

@@ -142,7 +142,7 @@ def test_gemv_matches_cpu_backend(cuda, ty, n, n_out):
     assert np.abs(got - yi).max() <= 2e-5 * max(1.0, np.abs(yi).max())
 
 
-LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 14336), (14336, 4096)]
+LLAMA_SHAPES = [(4096, 6144), (4096, 4096), (4096, 14336), (4096, 28672), (14336, 4096)]
 
 
 @pytest.mark.parametrize("n,n_out", LLAMA_SHAPES)
