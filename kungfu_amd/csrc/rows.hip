@@ -23,8 +23,6 @@
 
 namespace {
 
-constexpr int RW_THREADS = 256;
-constexpr int RW_WAVES = RW_THREADS / 64;
 
 template <uint32_t TY>
 struct RwType {
@@ -67,9 +65,47 @@ __device__ __forceinline__ void rw_load(RwLaneW& v, const uint8_t* row, int s, i
     }
 }
 
-// The lane's float contribution of one step against one staged activation row at xr (LDS)
+// The weight side of one lane's step, decoded once and reused against every staged activation row: q4_K nibbles
+// split into low and high halves, the sub-block pair's 6-bit scales and mins, the super-block's f16 scales; q8_0 the
+// int8 quants and the f16 scale.
+struct RwPrep {
+    uint32_t q[16];
+    int sc0, sc1, m0, m1;
+    float d, dm;
+};
+
 template <uint32_t TY>
-__device__ __forceinline__ float rw_dot(const RwLaneW& v, const uint8_t* xr, int n, int s, int lane) {
+__device__ __forceinline__ void rw_prep(RwPrep& u, const RwLaneW& v, int lane) {
+    if constexpr (TY == KF_TYPE_Q4_K) {
+        const uint32_t m4 = 0x0f0f0f0fu;
+        const uint32_t qa[4] = {v.b.x, v.b.y, v.b.z, v.b.w}, qb[4] = {v.c.x, v.c.y, v.c.z, v.c.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            u.q[i] = qa[i] & m4;
+            u.q[4 + i] = qb[i] & m4;
+            u.q[8 + i] = (qa[i] >> 4) & m4;
+            u.q[12 + i] = (qb[i] >> 4) & m4;
+        }
+        uint32_t sc2, m2;
+        kf_q4k_scales(v.a.y, v.a.z, v.a.w, lane & 3, sc2, m2);
+        u.sc0 = (int)(sc2 & 0xffu);
+        u.sc1 = (int)(sc2 >> 8);
+        u.m0 = (int)(m2 & 0xffu);
+        u.m1 = (int)(m2 >> 8);
+        u.d = kf_h2f(v.a.x & 0xffffu);
+        u.dm = kf_h2f(v.a.x >> 16);
+    } else {
+        const uint32_t w[8] = {v.a.x, v.a.y, v.a.z, v.a.w, v.b.x, v.b.y, v.b.z, v.b.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) u.q[i] = w[i];
+        u.d = kf_h2f(v.c.x);
+    }
+}
+
+// The lane's float contribution of one step against one staged activation row at xr (LDS). The integers are those of
+// kf_q4k_lane / kf_q8_0_dot (the reference's dot_i8 integers), the float combine that of the GEMV.
+template <uint32_t TY>
+__device__ __forceinline__ float rw_dot(const RwPrep& u, const uint8_t* xr, int n, int s, int lane) {
     using T = RwType<TY>;
     const uint4* xs = reinterpret_cast<const uint4*>(xr) + (s * T::STEP_PIECES) + lane;
     const int32_t* ss = reinterpret_cast<const int32_t*>(xr + (n / T::BLOCK + T::PER_STEP - 1) / T::PER_STEP * T::STEP_PIECES * 16);
@@ -77,18 +113,27 @@ __device__ __forceinline__ float rw_dot(const RwLaneW& v, const uint8_t* xr, int
         const float* sd = reinterpret_cast<const float*>(ss + n / 32);
         const int sb = s * 16 + (lane >> 2), j = lane & 3;
         const int2 bs = *reinterpret_cast<const int2*>(ss + sb * 8 + 2 * j);
-        int isum, imin;
-        kf_q4k_lane(v.a, v.b, v.c, j, xs[0], xs[64], xs[128], xs[192], bs.x, bs.y, isum, imin);
+        const uint4 x0 = xs[0], x1 = xs[64], x2 = xs[128], x3 = xs[192];
+        const uint32_t xv[16] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w, x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+        int lo = 0, hi = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) lo = kf_dot4(u.q[i], xv[i], lo);
+#pragma unroll
+        for (int i = 8; i < 16; i++) hi = kf_dot4(u.q[i], xv[i], hi);
+        // 24-bit multiplies are exact: scales and mins are 6-bit, |dot| <= 15*127*32 and |bsum| <= 128*32
+        const int isum = __mul24(u.sc0, lo) + __mul24(u.sc1, hi);
+        const int imin = __mul24(u.m0, bs.x) + __mul24(u.m1, bs.y);
         const float dx = sd[sb * 8];
-        const float d = kf_h2f(v.a.x & 0xffffu) * dx;
-        const float dm = kf_h2f(v.a.x >> 16) * dx;
-        return fmaf(-dm, (float)imin, d * (float)isum);
+        return fmaf(-(u.dm * dx), (float)imin, (u.d * dx) * (float)isum);
     } else {
         const float* sd = reinterpret_cast<const float*>(ss);
-        const uint32_t wq[8] = {v.a.x, v.a.y, v.a.z, v.a.w, v.b.x, v.b.y, v.b.z, v.b.w};
+        const uint4 x0 = xs[0], x1 = xs[64];
+        const uint32_t xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        int dt = 0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) dt = kf_dot4(u.q[i], xv[i], dt);
         const int b = s * 64 + lane;
-        const int dt = kf_q8_0_dot(wq, xs[0], xs[64]);
-        return kf_h2f(v.c.x) * sd[b] * (float)dt;
+        return u.d * sd[b] * (float)dt;
     }
 }
 
@@ -99,14 +144,20 @@ __device__ __forceinline__ float rw_silu(float x) { return x / (1.0f + expf(-x))
 // pairs [offsets[slot], offsets[slot + 1]) of `order` (identity without order; one slot [0, pairs) without offsets),
 // RMAX at a time. The activation row of pair p is p (per_slot) or p / n_used. Outputs y[p][o]: GLU ? silu(gate .
 // x) * (up . x) : w . x + bias[o] + res[p][o].
-template <uint32_t TY, int RMAX, bool GLU>
-__global__ void __launch_bounds__(RW_THREADS) rows_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int64_t expert_bytes,
+// Threads of a block: wide rows (four register steps) stage large activation rows, so eight waves share them (four
+// for the fused gate + up form, whose two rows of registers leave room for no more)
+template <int STEPS, bool GLU>
+constexpr int rw_threads() { return STEPS > 1 && !GLU ? 512 : 256; }
+
+template <uint32_t TY, int RMAX, bool GLU, int STEPS>
+__global__ void __launch_bounds__((rw_threads<STEPS, GLU>())) rows_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int64_t expert_bytes,
                                                          int64_t row_bytes, const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
                                                          const float* __restrict__ xd32, int n, int n_out, const int32_t* __restrict__ order,
                                                          const int32_t* __restrict__ offsets, int pairs, int n_used, int per_slot,
                                                          const float* __restrict__ bias, const float* __restrict__ res, float* __restrict__ y,
                                                          int rpb) {
     using T = RwType<TY>;
+    constexpr int THREADS = rw_threads<STEPS, GLU>(), WAVES = THREADS / 64;
     extern __shared__ __align__(16) uint8_t smem[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -123,78 +174,106 @@ __global__ void __launch_bounds__(RW_THREADS) rows_kernel(const uint8_t* __restr
     const uint8_t* ubase = GLU ? w2 + (int64_t)slot * expert_bytes : nullptr;
     const int nsum = n / 32, npc = n / 16;
 
+    // staging registers: every thread moves at most KMAX 16-byte pieces and one sum/scale of each staged row
+    constexpr int KMAX = (STEPS * T::STEP_PIECES + THREADS - 1) / THREADS;
     for (int c0 = p0; c0 < p1; c0 += RMAX) {
         const int R = min(RMAX, p1 - c0);
-        // stage the chunk's activation rows: transposed int8 pieces, then sums and scales
-        for (int r = 0; r < R; r++) {
-            const int p = order ? order[c0 + r] : c0 + r;
-            const int xrow = per_slot ? p : p / n_used;
-            uint8_t* xr = smem + r * row_lds;
-            const uint4* gq = reinterpret_cast<const uint4*>(xq + (int64_t)xrow * n);
-            for (int c = threadIdx.x; c < npc; c += RW_THREADS) {
-                int dst;
-                if constexpr (TY == KF_TYPE_Q4_K) {
-                    const int sb = c >> 4, jj = (c >> 2) & 3, k = c & 3;
-                    dst = (((sb >> 4) * 4 + k) << 6) + ((sb & 15) << 2) + jj;
-                } else {
-                    const int bb = c >> 1, k = c & 1;
-                    dst = (((bb >> 6) * 2 + k) << 6) + (bb & 63);
-                }
-                reinterpret_cast<uint4*>(xr)[dst] = gq[c];
+        RwLaneW ring[GLU ? 2 : 1][STEPS];
+        auto load_row = [&](RwLaneW (&v)[GLU ? 2 : 1][STEPS], int orow) {  // every step of a row
+            const uint8_t* gr = wbase + (int64_t)min(orow, n_out - 1) * row_bytes;
+#pragma unroll
+            for (int s2 = 0; s2 < STEPS; s2++)
+                if (s2 < steps) rw_load<TY>(v[0][s2], gr, s2, nblk, lane);
+            if constexpr (GLU) {
+                const uint8_t* ur = ubase + (int64_t)min(orow, n_out - 1) * row_bytes;
+#pragma unroll
+                for (int s2 = 0; s2 < STEPS; s2++)
+                    if (s2 < steps) rw_load<TY>(v[1][s2], ur, s2, nblk, lane);
             }
-            int32_t* ss = reinterpret_cast<int32_t*>(xr + steps * T::STEP_PIECES * 16);
-            float* sd = reinterpret_cast<float*>(ss + (TY == KF_TYPE_Q4_K ? nsum : 0));
-            for (int c = threadIdx.x; c < nsum; c += RW_THREADS) {
-                if constexpr (TY == KF_TYPE_Q4_K) ss[c] = xs32[(int64_t)xrow * nsum + c];
-                sd[c] = xd32[(int64_t)xrow * nsum + c];
+        };
+        // the wave's first row of weights goes out before the activations are staged (it does not depend on them)
+        int o = o0 + wave;
+        if (o < o1) load_row(ring, o);
+        // stage the chunk's activation rows: all loads first, then the stores (transposed int8 pieces, sums, scales)
+        {
+            typedef uint32_t v4u_ __attribute__((ext_vector_type(4)));
+            v4u_ pv[RMAX][KMAX];
+            int32_t sv[RMAX];
+            float dv[RMAX];
+#pragma unroll
+            for (int r = 0; r < RMAX; r++) {
+                if (r >= R) break;
+                const int p = order ? order[c0 + r] : c0 + r;
+                const int xrow = per_slot ? p : p / n_used;
+                const v4u_* gq = reinterpret_cast<const v4u_*>(xq + (int64_t)xrow * n);
+#pragma unroll
+                for (int k = 0; k < KMAX; k++) pv[r][k] = gq[min((int)threadIdx.x + k * THREADS, npc - 1)];
+                const int c = min((int)threadIdx.x, nsum - 1);
+                if constexpr (TY == KF_TYPE_Q4_K) sv[r] = xs32[(int64_t)xrow * nsum + c];
+                dv[r] = xd32[(int64_t)xrow * nsum + c];
+            }
+#pragma unroll
+            for (int r = 0; r < RMAX; r++) {
+                if (r >= R) break;
+                uint8_t* xr = smem + r * row_lds;
+#pragma unroll
+                for (int k = 0; k < KMAX; k++) {
+                    const int c = threadIdx.x + k * THREADS;
+                    if (c >= npc) break;
+                    int dst;
+                    if constexpr (TY == KF_TYPE_Q4_K) {
+                        const int sb = c >> 4, jj = (c >> 2) & 3, kk = c & 3;
+                        dst = (((sb >> 4) * 4 + kk) << 6) + ((sb & 15) << 2) + jj;
+                    } else {
+                        const int bb = c >> 1, kk = c & 1;
+                        dst = (((bb >> 6) * 2 + kk) << 6) + (bb & 63);
+                    }
+                    reinterpret_cast<v4u_*>(xr)[dst] = pv[r][k];
+                }
+                int32_t* ss = reinterpret_cast<int32_t*>(xr + steps * T::STEP_PIECES * 16);
+                float* sd = reinterpret_cast<float*>(ss + (TY == KF_TYPE_Q4_K ? nsum : 0));
+                if ((int)threadIdx.x < nsum) {
+                    if constexpr (TY == KF_TYPE_Q4_K) ss[threadIdx.x] = sv[r];
+                    sd[threadIdx.x] = dv[r];
+                }
             }
         }
         __syncthreads();
 
-        // each wave walks rows o0 + wave, + RW_WAVES, ...; the next row's weights are requested before this row's
-        // arithmetic
-        int o = o0 + wave;
-        RwLaneW cw[4], cu[4];  // one register set per step of the row (n <= 16384 for q4_K, 8192 for q8_0)
-        auto load_row = [&](int orow) {
-            const uint8_t* gr = wbase + (int64_t)min(orow, n_out - 1) * row_bytes;
-#pragma unroll
-            for (int s = 0; s < 4; s++)
-                if (s < steps) rw_load<TY>(cw[s], gr, s, nblk, lane);
-            if constexpr (GLU) {
-                const uint8_t* ur = ubase + (int64_t)min(orow, n_out - 1) * row_bytes;
-#pragma unroll
-                for (int s = 0; s < 4; s++)
-                    if (s < steps) rw_load<TY>(cu[s], ur, s, nblk, lane);
-            }
-        };
-        if (o < o1) load_row(o);
-        for (; o < o1; o += RW_WAVES) {
-            RwLaneW vw[4], vu[4];
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                vw[s] = cw[s];
-                if constexpr (GLU) vu[s] = cu[s];
-            }
-            if (o + RW_WAVES < o1) load_row(o + RW_WAVES);
+        // each wave walks rows o0 + wave, + WAVES, ...; the next row's weights are requested before this row's
+        // arithmetic (two register sets, STEPS steps of the row each)
+        // a rolling ring: as soon as a step's weights are decoded, its registers take the same step of the wave's
+        // next row, so that row's loads stream while this row's dots run
+        auto compute_row = [&](RwLaneW (&v)[GLU ? 2 : 1][STEPS], int orow, int next) {
             float ag[RMAX], au[RMAX];
 #pragma unroll
             for (int r = 0; r < RMAX; r++) {
                 ag[r] = 0.0f;
                 au[r] = 0.0f;
             }
+            const uint8_t* gn = wbase + (int64_t)min(next, n_out - 1) * row_bytes;
+            const uint8_t* un = GLU ? ubase + (int64_t)min(next, n_out - 1) * row_bytes : nullptr;
 #pragma unroll
-            for (int s = 0; s < 4; s++) {
-                if (s >= steps) break;
-                const bool valid = s * T::PER_STEP + (TY == KF_TYPE_Q4_K ? (lane >> 2) : lane) < nblk;
+            for (int s2 = 0; s2 < STEPS; s2++) {
+                if (s2 >= steps) break;
+                const bool valid = s2 * T::PER_STEP + (TY == KF_TYPE_Q4_K ? (lane >> 2) : lane) < nblk;
+                RwPrep pg, pu;
+                rw_prep<TY>(pg, v[0][s2], lane);
+                if constexpr (GLU) rw_prep<TY>(pu, v[1][s2], lane);
+                if (next < o1) {  // uniform
+                    rw_load<TY>(v[0][s2], gn, s2, nblk, lane);
+                    if constexpr (GLU) rw_load<TY>(v[1][s2], un, s2, nblk, lane);
+                }
 #pragma unroll
                 for (int r = 0; r < RMAX; r++) {
                     if (r >= R) break;
                     const uint8_t* xr = smem + r * row_lds;
                     if (valid) {
-                        ag[r] += rw_dot<TY>(vw[s], xr, n, s, lane);
-                        if constexpr (GLU) au[r] += rw_dot<TY>(vu[s], xr, n, s, lane);
+                        ag[r] += rw_dot<TY>(pg, xr, n, s2, lane);
+                        if constexpr (GLU) au[r] += rw_dot<TY>(pu, xr, n, s2, lane);
                     }
                 }
+                if (STEPS > 1) __builtin_amdgcn_sched_barrier(0);  // one step's decoded weights live at a time
             }
 #pragma unroll
             for (int r = 0; r < RMAX; r++) {
@@ -204,14 +283,15 @@ __global__ void __launch_bounds__(RW_THREADS) rows_kernel(const uint8_t* __restr
                 if constexpr (GLU) u = kf_wave_sum_dpp(au[r]);
                 if (lane == 0) {
                     const int p = order ? order[c0 + r] : c0 + r;
-                    float* yo = y + (int64_t)p * n_out + o;
+                    float* yo = y + (int64_t)p * n_out + orow;
                     if constexpr (GLU)
                         *yo = rw_silu(g) * u;
                     else
-                        *yo = g + (bias ? bias[o] : 0.0f) + (res ? res[(int64_t)p * n_out + o] : 0.0f);
+                        *yo = g + (bias ? bias[orow] : 0.0f) + (res ? res[(int64_t)p * n_out + orow] : 0.0f);
                 }
             }
-        }
+        };
+        for (; o < o1; o += WAVES) compute_row(ring, o, o + WAVES);
         __syncthreads();  // before the next chunk restages
     }
 }
@@ -279,11 +359,11 @@ __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restric
     }
 }
 
-template <uint32_t TY, int RMAX, bool GLU>
+template <uint32_t TY, int RMAX, bool GLU, int STEPS>
 hipError_t rows_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
                        const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
                        int per_slot, const float* bias, const float* res, float* y, hipStream_t s) {
-    auto* fn = rows_kernel<TY, RMAX, GLU>;
+    auto* fn = rows_kernel<TY, RMAX, GLU, STEPS>;
     const int lds = RMAX * rw_row_lds<TY>(n);
     static int lds_set = 0;
     if (lds > 65536 && lds_set < lds) {
@@ -291,30 +371,46 @@ hipError_t rows_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    const int rpb = 16 * RW_WAVES;  // rows per block: 16 a wave
+    constexpr int threads = rw_threads<STEPS, GLU>();
+    const int rpb = 16 * (threads / 64);  // rows per block: 16 a wave
     dim3 grid((n_out + rpb - 1) / rpb, offsets ? n_slots : 1);
-    fn<<<grid, RW_THREADS, lds, s>>>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, pairs, n_used, per_slot, bias, res,
+    fn<<<grid, threads, lds, s>>>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, pairs, n_used, per_slot, bias, res,
                                      y, rpb);
     return hipGetLastError();
 }
 
-// Pairs staged per chunk: as many as fit 96 KB of LDS, at most 8
+// Pairs staged per chunk, at most 8: every chunk past the first streams the slot's weights again, so wide rows (one
+// block of eight waves a CU) may take all of the CU's 160 KB of LDS; rows of one step keep within 96 KB so that
+// several blocks share a CU
 template <uint32_t TY>
 int rows_rmax(int n) {
     const int per = rw_row_lds<TY>(n);
-    return 8 * per <= 98304 ? 8 : 4 * per <= 98304 ? 4 : 2 * per <= 98304 ? 2 : 1;
+    const int steps = (n / RwType<TY>::BLOCK + RwType<TY>::PER_STEP - 1) / RwType<TY>::PER_STEP;
+    const int budget = steps > 1 ? 160 * 1024 : 96 * 1024;
+    return 8 * per <= budget ? 8 : 4 * per <= budget ? 4 : 2 * per <= budget ? 2 : 1;
 }
 
+template <uint32_t TY, bool GLU, int STEPS>
+hipError_t rows_dispatch_steps(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
+                               const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
+                               int per_slot, const float* bias, const float* res, float* y, hipStream_t s) {
+    switch (rows_rmax<TY>(n)) {
+        case 8: return rows_launch<TY, 8, GLU, STEPS>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
+        case 4: return rows_launch<TY, 4, GLU, STEPS>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
+        case 2: return rows_launch<TY, 2, GLU, STEPS>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
+        default: return rows_launch<TY, 1, GLU, STEPS>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
+    }
+}
+
+// Register steps a row needs: one step when it covers the row (q4_K n <= 4096, q8_0 n <= 2048), else four
 template <uint32_t TY, bool GLU>
 hipError_t rows_dispatch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
                          const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
                          int per_slot, const float* bias, const float* res, float* y, hipStream_t s) {
-    switch (rows_rmax<TY>(n)) {
-        case 8: return rows_launch<TY, 8, GLU>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
-        case 4: return rows_launch<TY, 4, GLU>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
-        case 2: return rows_launch<TY, 2, GLU>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
-        default: return rows_launch<TY, 1, GLU>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
-    }
+    const int steps = (n / RwType<TY>::BLOCK + RwType<TY>::PER_STEP - 1) / RwType<TY>::PER_STEP;
+    if (steps <= 1)
+        return rows_dispatch_steps<TY, GLU, 1>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
+    return rows_dispatch_steps<TY, GLU, 4>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
 }
 
 }  // namespace
