@@ -68,6 +68,11 @@ __device__ __forceinline__ void rw_load(RwLaneW& v, const uint8_t* row, int s, i
 // The weight side of one lane's step, decoded once and reused against every staged activation row: q4_K nibbles
 // split into low and high halves, the sub-block pair's 6-bit scales and mins, the super-block's f16 scales; q8_0 the
 // int8 quants and the f16 scale.
+// Scheduling barrier between staged pairs (bounds the registers a row's dots hold; 0 lets the compiler interleave)
+#ifndef KF_RW_PAIR_BARRIER
+#define KF_RW_PAIR_BARRIER 1
+#endif
+
 struct RwPrep {
     uint32_t q[16];
     int sc0, sc1, m0, m1;
@@ -272,6 +277,7 @@ __global__ void __launch_bounds__((rw_threads<STEPS, GLU>())) rows_kernel(const 
                         ag[r] += rw_dot<TY>(pg, xr, n, s2, lane);
                         if constexpr (GLU) au[r] += rw_dot<TY>(pu, xr, n, s2, lane);
                     }
+                    if (KF_RW_PAIR_BARRIER) __builtin_amdgcn_sched_barrier(0);  // one pair's activations live at a time
                 }
                 if (STEPS > 1) __builtin_amdgcn_sched_barrier(0);  // one step's decoded weights live at a time
             }
@@ -372,8 +378,13 @@ hipError_t rows_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes
         lds_set = lds;
     }
     constexpr int threads = rw_threads<STEPS, GLU>();
-    const int rpb = 16 * (threads / 64);  // rows per block: 16 a wave
-    dim3 grid((n_out + rpb - 1) / rpb, offsets ? n_slots : 1);
+    constexpr int waves = threads / 64;
+    // rows per block: enough blocks to fill the GPU (about 1024 over all slots), each wave walking at most 16 rows
+    // (a block stages its activation rows once for all of them)
+    const int slots = offsets ? n_slots : 1;
+    int per_wave = (int)std::min<int64_t>(16, std::max<int64_t>(1, ((int64_t)n_out * slots / 1024 + waves - 1) / waves));
+    const int rpb = per_wave * waves;
+    dim3 grid((n_out + rpb - 1) / rpb, slots);
     fn<<<grid, threads, lds, s>>>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, pairs, n_used, per_slot, bias, res,
                                      y, rpb);
     return hipGetLastError();
