@@ -113,28 +113,37 @@ PREFILL = [("gate_up", 4096, 14336), ("down", 14336, 4096)]
 SMALL_BATCH = [8, 16, 32, 64]
 
 
-def gemm_section(dev, m=2048):
-    """int8 MFMA GEMM of configs[3]: M=2048 Q8_0-kind activation rows against Q8_0 weights, both prefill shapes.
-    TOPS = 2*M*N*K / kernel time (the quant_act launch is timed beside it); two weight copies alternate."""
+def gemm_section(dev, m=2048, ty=None):
+    """int8 MFMA GEMM of configs[3]: M=2048 Q8_0-kind activation rows against Q8_0 weights, both prefill shapes
+    (with ty = q4_K: the same shapes with Q4_K weights and Q8K-kind activations, the tile GEMM kf_hip_matmul takes for
+    Q4_K prefill). TOPS = 2*M*N*K / kernel time (the quant_act launch is timed beside it); two weight copies alternate."""
     import torch
 
     import kungfu_amd as kf
 
+    ty = kf.TYPE_Q8_0 if ty is None else ty
+    kind = kf.act_kind(ty)
     out = {}
     for name, n, n_out in PREFILL:
-        w = torch.from_numpy(make_weights(kf.TYPE_Q8_0, n, n_out)).to(dev)
+        w = torch.from_numpy(make_weights(ty, n, n_out)).to(dev)
         ws = [w, w.clone()]
         x = torch.from_numpy(kf.synth_normal(1, 1.0, m * n).reshape(m, n)).to(dev)
         act = kf.alloc_act(m, n, dev)
         y = torch.empty((m, n_out), device=dev)
-        kf.quant_act(x, act, kf.ACT_Q8_0)
-        us = time_launches(lambda i: kf.gemm_i8(kf.TYPE_Q8_0, ws[i % 2], act, y, m, n, n_out), 20)
-        us_q = time_launches(lambda i: kf.quant_act(x, act, kf.ACT_Q8_0), 20)
+        kf.quant_act(x, act, kind)
+        us = time_launches(lambda i: kf.gemm_i8(ty, ws[i % 2], act, y, m, n, n_out), 20)
+        us_q = time_launches(lambda i: kf.quant_act(x, act, kind), 20)
         tops = 2.0 * m * n * n_out / us / 1e6
         out[name] = {"M": m, "K": n, "N": n_out, "us": round(us, 2), "TOPS": round(tops, 1),
                      "frac": round(tops / INT8_PEAK_TOPS, 4), "quant_act_us": round(us_q, 2)}
         del ws, w, x, act, y
     return out
+
+
+def gemm_q4_k_section(dev):
+    import kungfu_amd as kf
+
+    return gemm_section(dev, ty=kf.TYPE_Q4_K)
 
 
 def small_batch_section(dev):
@@ -258,7 +267,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "small", "moe", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -272,7 +281,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "small": small_batch_section, "moe": moe_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -345,6 +354,7 @@ def main():
     }
     out["int8_gemm"] = gemm_section(dev)
     out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
+    out["int8_gemm_q4_k"] = gemm_q4_k_section(dev)
     out["small_batch_q8_0"] = small_batch_section(dev)
     out["moe_q4_k"] = moe_section(dev)
     if not args.no_cpu:

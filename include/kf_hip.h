@@ -86,11 +86,14 @@ int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void*
 int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                 int rows, int n, int n_out, void* stream);
 
-/* Batched / prefill int8 GEMM on q8_0 rows: y [rows][n_out] from `rows` activation rows of Q8_0 kind. One int8 MFMA
- * per 32-column group gives the exact int32 block dots, rescaled by the group's activation and weight scales.
- * Replaces kf8_gemm_dense / Store::gemm (crates/kf-backend-cuda/src/kernels/kf8.cu:375-395,
- * crates/kf-backend-cuda/src/kf8.rs:310-323) without the KF8 unpack: the native q8_0 bytes are read directly.
- * n must be a multiple of 128. */
+/* Batched / prefill int8 GEMM on native rows: y [rows][n_out] from `rows` activation rows of the weight type's kind.
+ * q8_0 (Q8_0-kind activations, n a multiple of 128): one int8 MFMA per 32-column group gives the exact int32 block
+ * dots, rescaled by the group's activation and weight scales. q4_K (Q8K-kind activations): one int8 MFMA per 32-column
+ * group on the unpacked nibbles, the 6-bit scale folded in with an integer multiply-add, the mins term by an exact f16
+ * MFMA per super-block, and the float rescale once per 256 columns.
+ * Replaces kf8_gemm_dense / Store::gemm (crates/kf-backend-cuda/src/kernels/kf8.cu:375-395, HAS_M for q4_K;
+ * crates/kf-backend-cuda/src/kf8.rs:310-323) without the KF8 unpack pass (kf_unpack_i8, quant.cuh:585-601): the
+ * native q8_0 / q4_K bytes are read directly. */
 int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                    int rows, int n, int n_out, void* stream);
 

@@ -24,6 +24,9 @@ int kf_gemv_max_n();
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s);
 int kf_gemm_k_multiple();
+
+hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
+                              int N, int K, hipStream_t s);
 int kf_rows_max_n(uint32_t ty);
 hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, const void* act, int act_rows,
                           int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used, int per_slot,
@@ -155,7 +158,11 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
                    int rows, int n, int n_out, void* stream) {
     const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
     if (rc != KF_OK) return rc;
-    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0 weights (type %u given)", ty);
+    if (ty == KF_TYPE_Q4_K) {
+        const hipError_t e = kf_launch_gemm_q4k(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
+        return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
+    }
+    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0 and q4_K weights (type %u given)", ty);
     if (n % kf_gemm_k_multiple() != 0) return fail(KF_E_INVALID, "%d columns, the GEMM needs a multiple of %d", n, kf_gemm_k_multiple());
     const hipError_t e = kf_launch_gemm_q8_0(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
@@ -175,6 +182,13 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
     // several q8_0 rows are the int8 GEMM, which reads each weight byte once per 128 rows
     if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
         return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+    // q4_K: the multi-row product streams each weight row once per eight activation rows, the tile GEMM once per 128
+    // rows but with one block per 128 x 128 output tile; the GEMM is taken from 128 rows, or from 32 when it has at
+    // least 96 blocks to spread over the GPU (measured crossovers at the Llama shapes)
+    if (ty == KF_TYPE_Q4_K && n_out > 0) {
+        const int64_t blocks = (int64_t)((n_out + 127) / 128) * ((rows + 127) / 128);
+        if (rows >= 128 || (rows >= 32 && blocks >= 96)) return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+    }
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
 }
 

@@ -23,6 +23,7 @@
 //     gemm_q8_0_small_kernel takes over: a block owns 32 output columns, its W waves split K among themselves, every
 //     lane loads its MFMA operand pieces straight from memory (no LDS staging) several groups ahead, and the waves'
 //     partial tiles are summed in LDS in a fixed tree order.
+#include "kf_blocks.h"
 #include "kf_device.h"
 
 #include <algorithm>
@@ -41,6 +42,9 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int GM_BK = 128;  // columns per stage: four 32-column groups
 constexpr int GM_G = GM_BK / 32;
 constexpr int GM_THREADS = 256;
+#ifndef KF_GK_ABLATE
+#define KF_GK_ABLATE 0  // measurement builds only: 1 = no global loads after the first stage
+#endif
 
 template <int WM, int WN, int TM, int TN>
 struct GmCfg {
@@ -428,6 +432,242 @@ __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __r
     }
 }
 
+// ------------------------------------------------------------------------------------------- q4_K prefill GEMM
+// y[m][n] = sum over super-blocks b of dx[m][b] * (d[n][b] * S_b[m][n] - dmin[n][b] * mins_b[m][n]) (+ bias + res),
+// with S_b = sum_j sc_j[n] * I_j[m][n] and mins_b = sum_j m_j[n] * bsum_j[m] the reference's per-super-block integers
+// (crates/kf-quant/src/types/q4_k.rs:10-58). Per 32-column group j one v_mfma_i32_32x32x32_i8 gives I_j (the weight
+// operand is the group's nibbles, 0..15, unpacked to bytes when staged) and one 24-bit integer multiply-add per output
+// folds in the 6-bit scale, so S_b is exact. mins_b is one v_mfma_f32_32x32x16_f16 per super-block: bsum_j = 64 hi + lo
+// (hi in [-64, 63], lo in [0, 63]) fills eight k slots with hi against 64 m_j and eight with lo against m_j; every
+// product and partial sum is an integer below 2^24, so the f32 result is exact. The float rescale runs once per 256
+// columns per output (convert, multiply, two FMAs), an eighth of the q8_0 form's per-group work.
+//
+// LDS: two stage buffers (128 columns each: activation bytes and unpacked weight nibbles in the gm_slot layout) and two
+// super-block records, by super-block parity: sc [8][BN] u8, (d, dmin) [BN] float2, dx [BM] f32 in accumulator row
+// order, the mins operands xo [BM][16] f16 (hi_0..7, lo_0..7) and mo [BN][16] f16 (64 m_0..7, m_0..7). A record is
+// written with the first stage of its super-block and read through the second, and the next write to the same record
+// comes two barriers later.
+template <int WM, int WN, int TM, int TN>
+struct GkCfg {
+    static_assert(WM * WN == 4, "four waves");
+    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+    static constexpr int A_BYTES = BM * GM_BK, B_BYTES = BN * GM_BK;
+    static constexpr int STAGE = A_BYTES + B_BYTES;
+    static constexpr int SC = 0, DD = SC + 8 * BN, DX = DD + 8 * BN, XO = DX + 4 * BM, MO = XO + 32 * BM;
+    static constexpr int REC = MO + 32 * BN;
+    static constexpr int TOTAL = 2 * STAGE + 2 * REC;
+    static constexpr int PA = BM * 8 / GM_THREADS;  // 16-byte activation pieces a thread moves per stage
+    static constexpr int PB = BN * 4 / GM_THREADS;  // 16-byte nibble pieces (64 bytes of a row per stage)
+    static constexpr int XS = BM * 8 / GM_THREADS;  // activation group sums a thread moves per super-block
+    static_assert(PA >= 1 && PB >= 1 && XS >= 1 && BN <= GM_THREADS && BM <= GM_THREADS, "tile sizes");
+};
+
+template <class C>
+struct GkStage {
+    uint4 a[C::PA], b[C::PB];
+    uint4 hdr;  // the q4_K header (d, dmin, 12 scale bytes) of row tid, first stage of a super-block only
+    float dx;   // the activation super-block scale of row tid
+    int xs[C::XS];
+
+    __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                         const int32_t* __restrict__ xs32, const float* __restrict__ xd32, int m0, int n0, int M, int N,
+                                         int K, int st, int tid) {
+        const int sb = st >> 1, h = st & 1;
+        const int kg = K >> 5;
+#pragma unroll
+        for (int i = 0; i < C::PA; i++) {
+            const int c = tid + GM_THREADS * i;
+            const int m = min(m0 + (c >> 3), M - 1);
+            a[i] = *reinterpret_cast<const uint4*>(xq + (int64_t)m * K + st * GM_BK + (c & 7) * 16);
+        }
+#pragma unroll
+        for (int i = 0; i < C::PB; i++) {
+            const int c = tid + GM_THREADS * i;  // four consecutive threads read one row's 64 nibble bytes
+            const int n = min(n0 + (c >> 2), N - 1);
+            b[i] = *reinterpret_cast<const uint4*>(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES + 16 + 64 * h + 16 * (c & 3));
+        }
+        if (h == 0) {
+            const int n = min(n0 + min(tid, C::BN - 1), N - 1);
+            hdr = *reinterpret_cast<const uint4*>(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES);
+            const int m = min(m0 + min(tid, C::BM - 1), M - 1);
+            dx = xd32[(int64_t)m * kg + sb * 8];
+#pragma unroll
+            for (int i = 0; i < C::XS; i++) {
+                const int c = tid + GM_THREADS * i;  // row c / 8, group c % 8
+                const int mm = min(m0 + (c >> 3), M - 1);
+                xs[i] = xs32[(int64_t)mm * kg + sb * 8 + (c & 7)];
+            }
+        }
+    }
+
+    __device__ __forceinline__ void store(uint8_t* buf, uint8_t* rec, int st, int tid) const {
+#pragma unroll
+        for (int i = 0; i < C::PA; i++) {
+            const int c = tid + GM_THREADS * i;
+            const int p = c & 7;
+            *reinterpret_cast<uint4*>(buf + gm_slot(C::BM / 32, p >> 1, c >> 3, p & 1)) = a[i];
+        }
+#pragma unroll
+        for (int i = 0; i < C::PB; i++) {
+            // piece p holds nibble bytes 16p..16p+15 of the stage: the low nibbles are elements 16(p&1).. of local group
+            // 2(p>>1), the high nibbles the same elements of group 2(p>>1)+1
+            const int c = tid + GM_THREADS * i;
+            const int p = c & 3, r = c >> 2;
+            const uint32_t m4 = 0x0f0f0f0fu;
+            const uint4 v = b[i];
+            *reinterpret_cast<uint4*>(buf + C::A_BYTES + gm_slot(C::BN / 32, (p >> 1) * 2, r, p & 1)) =
+                make_uint4(v.x & m4, v.y & m4, v.z & m4, v.w & m4);
+            *reinterpret_cast<uint4*>(buf + C::A_BYTES + gm_slot(C::BN / 32, (p >> 1) * 2 + 1, r, p & 1)) =
+                make_uint4((v.x >> 4) & m4, (v.y >> 4) & m4, (v.z >> 4) & m4, (v.w >> 4) & m4);
+        }
+        if ((st & 1) == 0) {
+            if (tid < C::BN) {
+                uint8_t* sc = rec + C::SC;
+                _Float16* mo = reinterpret_cast<_Float16*>(rec + C::MO) + tid * 16;
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    uint32_t sc2, m2;
+                    kf_q4k_scales(hdr.y, hdr.z, hdr.w, j, sc2, m2);
+                    sc[(2 * j) * C::BN + tid] = (uint8_t)(sc2 & 0xffu);
+                    sc[(2 * j + 1) * C::BN + tid] = (uint8_t)(sc2 >> 8);
+                    mo[2 * j] = (_Float16)(float)(64u * (m2 & 0xffu));
+                    mo[2 * j + 1] = (_Float16)(float)(64u * (m2 >> 8));
+                    mo[8 + 2 * j] = (_Float16)(float)(m2 & 0xffu);
+                    mo[8 + 2 * j + 1] = (_Float16)(float)(m2 >> 8);
+                }
+                reinterpret_cast<float2*>(rec + C::DD)[tid] = make_float2(kf_h2f(hdr.x & 0xffffu), kf_h2f(hdr.x >> 16));
+            }
+            if (tid < C::BM) {
+                // accumulator row order: tile t, half h = (row / 4) % 2, register (row % 4) + 4 (row / 8)
+                const int t = tid >> 5, rr = tid & 31;
+                reinterpret_cast<float*>(rec + C::DX)[t * 32 + ((rr >> 2) & 1) * 16 + (rr & 3) + 4 * (rr >> 3)] = dx;
+            }
+#pragma unroll
+            for (int i = 0; i < C::XS; i++) {
+                const int c = tid + GM_THREADS * i;
+                const int v = xs[i];
+                _Float16* xo = reinterpret_cast<_Float16*>(rec + C::XO) + (c >> 3) * 16;
+                xo[c & 7] = (_Float16)(float)(v >> 6);     // |hi| <= 64: exact
+                xo[8 + (c & 7)] = (_Float16)(float)(v & 63);
+            }
+        }
+    }
+};
+
+template <int WM, int WN, int TM, int TN>
+__global__ void __launch_bounds__(GM_THREADS, 2) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                                 const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
+                                                                 const float* __restrict__ bias, const float* __restrict__ res,
+                                                                 float* __restrict__ y, int M, int N, int K) {
+    using C = GkCfg<WM, WN, TM, TN>;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    const int m0 = blockIdx.y * C::BM, n0 = blockIdx.x * C::BN;
+    const int st1 = K / GM_BK;
+
+    v16f acc[TM][TN];
+    v16i S[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            acc[i][j] = v16f{};
+            S[i][j] = v16i{};
+        }
+
+    GkStage<C> pf;
+    pf.load(w, row_bytes, xq, xs32, xd32, m0, n0, M, N, K, 0, tid);
+    pf.store(smem, smem + 2 * C::STAGE, 0, tid);
+    __syncthreads();
+    for (int st = 0; st < st1; st++) {
+        const uint8_t* buf = smem + (st & 1) * C::STAGE;
+        const uint8_t* rec = smem + 2 * C::STAGE + ((st >> 1) & 1) * C::REC;
+        const int gb = (st & 1) * GM_G;  // the stage's first group within its super-block
+#if !(KF_GK_ABLATE & 1)
+        pf.load(w, row_bytes, xq, xs32, xd32, m0, n0, M, N, K, min(st + 1, st1 - 1), tid);
+#endif
+        struct Ops {
+            v4i a[TM], b[TN];
+            int sc[TN];
+        };
+        auto read_ops = [&](Ops& o, int g) {
+#pragma unroll
+            for (int t = 0; t < TM; t++) o.a[t] = *reinterpret_cast<const v4i*>(buf + gm_operand(C::BM / 32, g, wm * TM + t, lane));
+#pragma unroll
+            for (int t = 0; t < TN; t++) {
+                o.b[t] = *reinterpret_cast<const v4i*>(buf + C::A_BYTES + gm_operand(C::BN / 32, g, wn * TN + t, lane));
+                o.sc[t] = rec[C::SC + (gb + g) * C::BN + (wn * TN + t) * 32 + (lane & 31)];
+            }
+        };
+        Ops cur;
+        read_ops(cur, 0);
+#pragma unroll 1
+        for (int g = 0; g < GM_G; g++) {
+            Ops nxt;
+            read_ops(nxt, min(g + 1, GM_G - 1));
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[i], cur.b[j], v16i{}, 0, 0, 0);
+                    // |I_j| <= 15 * 128 * 32 and sc_j < 64: 24-bit multiplies are exact
+#pragma unroll
+                    for (int r = 0; r < 16; r++) S[i][j][r] += __mul24(c[r], cur.sc[j]);
+                }
+            cur = nxt;
+        }
+        if (st & 1) {
+            // end of a super-block: mins by MFMA, then the float rescale of S and mins, and S restarts
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                const int tr = wm * TM + i;
+                const v8h xo = *reinterpret_cast<const v8h*>(rec + C::XO + (tr * 32 + (lane & 31)) * 32 + (lane >> 5) * 16);
+                const float* dxp = reinterpret_cast<const float*>(rec + C::DX) + tr * 32 + (lane >> 5) * 16;
+                v16f dxv;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const v4f t4 = *reinterpret_cast<const v4f*>(dxp + 4 * q);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) dxv[4 * q + e] = t4[e];
+                }
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const int col = (wn * TN + j) * 32 + (lane & 31);
+                    const v8h mo = *reinterpret_cast<const v8h*>(rec + C::MO + col * 32 + (lane >> 5) * 16);
+                    const float2 dd = reinterpret_cast<const float2*>(rec + C::DD)[col];
+                    const v16f mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo, v16f{}, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const float t = fmaf(-dd.y, mins[r], dd.x * (float)S[i][j][r]);
+                        acc[i][j][r] = fmaf(t, dxv[r], acc[i][j][r]);
+                    }
+                    S[i][j] = v16i{};
+                }
+            }
+        }
+        if (st + 1 < st1) pf.store(smem + ((st + 1) & 1) * C::STAGE, smem + 2 * C::STAGE + (((st + 1) >> 1) & 1) * C::REC, st + 1, tid);
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + (wn * TN + j) * 32 + (lane & 31);
+            if (n >= N) continue;
+            const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
+            }
+        }
+}
+
 template <int WM, int WN, int TM, int TN>
 hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res, float* y,
                        int M, int N, int K, hipStream_t s) {
@@ -441,6 +681,22 @@ hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
     }
     dim3 grid((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
     fn<<<grid, GM_THREADS, 2 * C::STAGE, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t gemm_q4k_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
+                           const float* res, float* y, int M, int N, int K, hipStream_t s) {
+    using C = GkCfg<WM, WN, TM, TN>;
+    auto* fn = gemm_q4k_kernel<WM, WN, TM, TN>;
+    static bool lds_set = false;
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::TOTAL);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    dim3 grid((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
+    fn<<<grid, GM_THREADS, C::TOTAL, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, M, N, K);
     return hipGetLastError();
 }
 
@@ -494,4 +750,14 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
         if (M <= 64) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);  // M / 16 row blocks
     }
     return gemm_launch<2, 2, 2, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+}
+
+// Host launcher of the q4_K GEMM, validated by the caller (api.cpp): K a multiple of 256, Q8K-kind activations in `act`
+hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
+                              int N, int K, hipStream_t s) {
+    const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
+    const char* base = static_cast<const char*>(act);
+    return gemm_q4k_launch<2, 2, 2, 2>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
+                                       reinterpret_cast<const int32_t*>(base + o.s32), reinterpret_cast<const float*>(base + o.d32), bias,
+                                       res, y, M, N, K, s);
 }

@@ -265,6 +265,94 @@ def test_gemm_matches_cpu_backend(cuda, rows, n, n_out):
     _close(y.cpu().numpy(), want)
 
 
+Q4K_GEMM_SHAPES = [(9, 256, 64), (2, 256, 40), (17, 1024, 1000), (130, 512, 200), (256, 4096, 384), (33, 14336, 96),
+                   (129, 2304, 130)]
+
+
+@pytest.mark.parametrize("rows,n,n_out", Q4K_GEMM_SHAPES)
+def test_gemm_q4_k_matches_cpu_backend(cuda, rows, n, n_out):
+    """The q4_K int8 MFMA GEMM against matmul_slice, with bias and residual; ragged tiles and nine-super-block rows."""
+    import torch
+
+    w = _weights(kf.TYPE_Q4_K, n_out, n, seed=50 + rows)
+    x = kf.synth_normal(51 + rows, 1.0, rows * n).reshape(rows, n)
+    bias = kf.synth_normal(52, 1.0, n_out)
+    res = kf.synth_normal(53, 1.0, rows * n_out).reshape(rows, n_out)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q4_K, _tensor(w, cuda), act, y, rows, n, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x, bias) + res)
+
+
+def test_gemm_q4_k_random_blocks_and_extreme_sums(cuda):
+    """Random header bytes (6-bit scales and mins up to 63) and activation blocks at full scale, so the group sums
+    reach +-4064 and the exact mins product (64 hi + lo split) is exercised at its limits."""
+    import torch
+
+    rng = np.random.default_rng(7)
+    rows, n, n_out = 70, 1024, 136
+    w = _random_blocks(kf.TYPE_Q4_K, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    # Q8K rounds the super-block's first max-|v| value to -127 and clamps the opposite sign at +127, so a group at the
+    # maximum and one at minus the maximum give sums of -4064 and +4064
+    x[3, :32] = 4.0
+    x[3, 32:64] = -4.0
+    x[5, 256:288] = -4.0
+    x[5, 288:320] = 4.0
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    _, _, _, _, s32 = kf.act_views(act, rows, n)
+    sums = s32.cpu().numpy()
+    assert sums.max() == 4064 and sums.min() == -4064
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q4_K, _tensor(w, cuda), act, y, rows, n, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x))
+
+
+@pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
+def test_gemm_q4_k_prefill_shapes_match_gemv(cuda, n, n_out):
+    """Q4_K at the Llama-3-8B shapes and M = 2048: every 97th row of the GEMM against the GEMV of that row on the same
+    quantized activations (the GEMV is pinned to the CPU backend above)."""
+    import torch
+
+    rows = 2048
+    w = _tensor(_weights(kf.TYPE_Q4_K, n_out, n, seed=3), cuda)
+    x = _tensor(kf.synth_normal(4, 1.0, rows * n).reshape(rows, n), cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(x, act, kf.ACT_Q8K)
+    y = torch.empty((rows, n_out), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q4_K, w, act, y, rows, n, n_out)
+    views = kf.act_views(act, rows, n)
+    one = kf.alloc_act(1, n, cuda)
+    oviews = kf.act_views(one, 1, n)
+    yr = torch.empty((1, n_out), device=cuda)
+    for r in range(0, rows, 97):
+        for src, dst in zip(views, oviews):
+            dst.copy_(src[r : r + 1])
+        kf.gemv(kf.TYPE_Q4_K, w, one, yr, 1, n, n_out)
+        torch.cuda.synchronize()
+        _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())
+
+
+@pytest.mark.parametrize("rows,n_out", [(9, 96), (40, 96), (40, 12300), (200, 96)])
+def test_matmul_q4_k_many_rows(cuda, rows, n_out):
+    """kf_hip_matmul with many q4_K rows (the multi-row product below the GEMM crossover, the tile GEMM above it:
+    200 rows, or 40 rows over 97 column tiles); results as the CPU backend's."""
+    import torch
+
+    n = 512
+    w = _weights(kf.TYPE_Q4_K, n_out, n, seed=60 + rows)
+    x = kf.synth_normal(61 + rows, 1.0, rows * n).reshape(rows, n)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.matmul(kf.TYPE_Q4_K, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x))
+
+
 @pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
 def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
     """Config C4 at full size (M = 2048): every 97th row of the GEMM against the GEMV of that row on the same
