@@ -42,9 +42,6 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 constexpr int GM_BK = 128;  // columns per stage: four 32-column groups
 constexpr int GM_G = GM_BK / 32;
 constexpr int GM_THREADS = 256;
-#ifndef KF_GK_ABLATE
-#define KF_GK_ABLATE 0  // measurement builds only: 1 = no global loads after the first stage
-#endif
 
 template <int WM, int WN, int TM, int TN>
 struct GmCfg {
@@ -435,219 +432,236 @@ __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __r
 // ------------------------------------------------------------------------------------------- q4_K prefill GEMM
 // y[m][n] = sum over super-blocks b of dx[m][b] * (d[n][b] * S_b[m][n] - dmin[n][b] * mins_b[m][n]) (+ bias + res),
 // with S_b = sum_j sc_j[n] * I_j[m][n] and mins_b = sum_j m_j[n] * bsum_j[m] the reference's per-super-block integers
-// (crates/kf-quant/src/types/q4_k.rs:10-58). Per 32-column group j one v_mfma_i32_32x32x32_i8 gives I_j (the weight
-// operand is the group's nibbles, 0..15, unpacked to bytes when staged) and one 24-bit integer multiply-add per output
-// folds in the 6-bit scale, so S_b is exact. mins_b is one v_mfma_f32_32x32x16_f16 per super-block: bsum_j = 64 hi + lo
-// (hi in [-64, 63], lo in [0, 63]) fills eight k slots with hi against 64 m_j and eight with lo against m_j; every
-// product and partial sum is an integer below 2^24, so the f32 result is exact. The float rescale runs once per 256
-// columns per output (convert, multiply, two FMAs), an eighth of the q8_0 form's per-group work.
+// (crates/kf-quant/src/types/q4_k.rs:10-58); the reference GPU path first unpacks q4_K into int8 + per-32 float scale
+// and min and runs a float-rescaled GEMM (crates/kf-backend-cuda/src/kernels/quant.cuh:585-601, kf8.cu:253-310).
 //
-// LDS: two stage buffers (128 columns each: activation bytes and unpacked weight nibbles in the gm_slot layout) and two
-// super-block records, by super-block parity: sc [8][BN] u8, (d, dmin) [BN] float2, dx [BM] f32 in accumulator row
-// order, the mins operands xo [BM][16] f16 (hi_0..7, lo_0..7) and mo [BN][16] f16 (64 m_0..7, m_0..7). A record is
-// written with the first stage of its super-block and read through the second, and the next write to the same record
-// comes two barriers later.
+// Here the native bytes feed the matrix core and S_b stays an exact integer formed by it:
+//   * the 6-bit scale is split as sc_j = 8 sh_j + sl_j (sh_j, sl_j in [0, 7]), so the nibble products q * sl_j and
+//     q * sh_j (at most 105) are int8 operands; two int32 MFMA chains per 32 x 32 tile run through the super-block,
+//     S_lo = sum_j X_j . (q_j sl_j) and S_hi = sum_j X_j . (q_j sh_j), and S_b = 8 S_hi + S_lo;
+//   * mins_b is one v_mfma_f32_32x32x16_f16 per super-block and tile: bsum_j = 64 hi + lo (hi in [-64, 63], lo in
+//     [0, 63]) fills eight k slots with hi against 64 m_j and eight with lo against m_j; every product and partial sum
+//     is an integer below 2^24, so the f32 result is exact;
+//   * the float rescale runs once per super-block and output (shift-add, convert, three float operations).
+// Staging is all DMA (global_load_lds_dwordx4), no register round trip:
+//   * an A stage (128 activation columns) sits in LDS as [group][32-row tile] 1 KB blocks in MFMA order (lane l reads
+//     bytes 16 l..: row l % 32, columns 16 (l / 32).. of the group), one DMA instruction per block;
+//   * the weights' raw nibble bytes sit as [pair][32-row tile] 1 KB blocks (lane l: row l % 32, bytes 16 (l / 32)..
+//     of the sub-block pair), in which each lane holds the bytes of its MFMA operand for both groups of the pair
+//     (low nibbles: group 2p, high nibbles: group 2p + 1); the consuming wave expands them into the two planes in
+//     registers (a mask, a shift and a packed 16-bit multiply per plane and dword);
+//   * once per super-block the rows' 16-byte headers, the activation scales dx and the activation group sums are
+//     fetched the same way into a record, double-buffered by super-block parity.
+// Measured on gfx950, the alternatives were slower: staging through registers let the compiler sink the prefetch
+// loads to their LDS stores (the full memory latency every stage), one LDS array made it wait for every outstanding
+// DMA before each LDS read (so the buffers are distinct static arrays), and wave tiles above two 32 x 32 tiles push the
+// two chains and the float accumulator (48 registers a tile) into AGPRs, which the compiler then copies every stage.
+// Eight waves (two per SIMD), each a 64 x 32 tile; blocks in XCD order (gm_tile).
+
+// Packed 16-bit multiply of the bytes of x by a small s: exact per byte while every byte product stays below 256
+__device__ __forceinline__ uint32_t gs_pmul(uint32_t x, uint32_t s) {
+    typedef unsigned short v2us __attribute__((ext_vector_type(2)));
+    const v2us r = __builtin_bit_cast(v2us, x) * v2us{(unsigned short)s, (unsigned short)s};
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// XCD-aware tile order. Workgroups go to the eight XCDs round-robin by linear block id, and each XCD has its own L2.
+// Block b runs tile t = (b % 8) * (T / 8) + b / 8, so XCD x works through the contiguous tile range
+// [x T / 8, (x + 1) T / 8). Tiles are numbered M-fastest, so an XCD's range is a few weight tiles against every
+// activation panel: the blocks in flight on an XCD share their weight tiles, every weight byte crosses HBM once, and
+// only the (smaller, MALL-resident) activations are streamed per XCD. Numbered N-fastest, each XCD would stream the
+// whole weight matrix once per activation panel pair (measured: about 1 GB per 62 MB GEMM and no faster kernel).
+// Identity when T is not a multiple of eight.
+__device__ __forceinline__ void gm_tile(int nt, int mt, int& tm, int& tn) {
+    const int T = nt * mt, b = blockIdx.x;
+    const int t = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);
+    tn = t / mt;
+    tm = t - tn * mt;
+}
+
 template <int WM, int WN, int TM, int TN>
-struct GkCfg {
-    static_assert(WM * WN == 4, "four waves");
+struct GdCfg {
+    static constexpr int W = WM * WN, THREADS = 64 * W;
     static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
-    static constexpr int A_BYTES = BM * GM_BK, B_BYTES = BN * GM_BK;
+    static constexpr int MT = BM / 32, NT = BN / 32;
+    static constexpr int A_BYTES = MT * GM_G * 1024, B_BYTES = 2 * NT * 1024;
     static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int SC = 0, DD = SC + 8 * BN, DX = DD + 8 * BN, XO = DX + 4 * BM, MO = XO + 32 * BM;
-    static constexpr int REC = MO + 32 * BN;
+    static constexpr int NA = MT * GM_G, NB = 2 * NT;              // DMA instructions per stage
+    static constexpr int NH = (BN + 63) / 64, ND = (BM + 63) / 64, NX = MT;  // per super-block: headers, dx, sums
+    static constexpr int HDR = 0, DX = HDR + NH * 1024, XS = DX + ND * 256;
+    static constexpr int REC = XS + NX * 1024;
     static constexpr int TOTAL = 2 * STAGE + 2 * REC;
-    static constexpr int PA = BM * 8 / GM_THREADS;  // 16-byte activation pieces a thread moves per stage
-    static constexpr int PB = BN * 4 / GM_THREADS;  // 16-byte nibble pieces (64 bytes of a row per stage)
-    static constexpr int XS = BM * 8 / GM_THREADS;  // activation group sums a thread moves per super-block
-    static_assert(PA >= 1 && PB >= 1 && XS >= 1 && BN <= GM_THREADS && BM <= GM_THREADS, "tile sizes");
-};
-
-template <class C>
-struct GkStage {
-    uint4 a[C::PA], b[C::PB];
-    uint4 hdr;  // the q4_K header (d, dmin, 12 scale bytes) of row tid, first stage of a super-block only
-    float dx;   // the activation super-block scale of row tid
-    int xs[C::XS];
-
-    __device__ __forceinline__ void load(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
-                                         const int32_t* __restrict__ xs32, const float* __restrict__ xd32, int m0, int n0, int M, int N,
-                                         int K, int st, int tid) {
-        const int sb = st >> 1, h = st & 1;
-        const int kg = K >> 5;
-#pragma unroll
-        for (int i = 0; i < C::PA; i++) {
-            const int c = tid + GM_THREADS * i;
-            const int m = min(m0 + (c >> 3), M - 1);
-            a[i] = *reinterpret_cast<const uint4*>(xq + (int64_t)m * K + st * GM_BK + (c & 7) * 16);
-        }
-#pragma unroll
-        for (int i = 0; i < C::PB; i++) {
-            const int c = tid + GM_THREADS * i;  // four consecutive threads read one row's 64 nibble bytes
-            const int n = min(n0 + (c >> 2), N - 1);
-            b[i] = *reinterpret_cast<const uint4*>(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES + 16 + 64 * h + 16 * (c & 3));
-        }
-        if (h == 0) {
-            const int n = min(n0 + min(tid, C::BN - 1), N - 1);
-            hdr = *reinterpret_cast<const uint4*>(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES);
-            const int m = min(m0 + min(tid, C::BM - 1), M - 1);
-            dx = xd32[(int64_t)m * kg + sb * 8];
-#pragma unroll
-            for (int i = 0; i < C::XS; i++) {
-                const int c = tid + GM_THREADS * i;  // row c / 8, group c % 8
-                const int mm = min(m0 + (c >> 3), M - 1);
-                xs[i] = xs32[(int64_t)mm * kg + sb * 8 + (c & 7)];
-            }
-        }
-    }
-
-    __device__ __forceinline__ void store(uint8_t* buf, uint8_t* rec, int st, int tid) const {
-#pragma unroll
-        for (int i = 0; i < C::PA; i++) {
-            const int c = tid + GM_THREADS * i;
-            const int p = c & 7;
-            *reinterpret_cast<uint4*>(buf + gm_slot(C::BM / 32, p >> 1, c >> 3, p & 1)) = a[i];
-        }
-#pragma unroll
-        for (int i = 0; i < C::PB; i++) {
-            // piece p holds nibble bytes 16p..16p+15 of the stage: the low nibbles are elements 16(p&1).. of local group
-            // 2(p>>1), the high nibbles the same elements of group 2(p>>1)+1
-            const int c = tid + GM_THREADS * i;
-            const int p = c & 3, r = c >> 2;
-            const uint32_t m4 = 0x0f0f0f0fu;
-            const uint4 v = b[i];
-            *reinterpret_cast<uint4*>(buf + C::A_BYTES + gm_slot(C::BN / 32, (p >> 1) * 2, r, p & 1)) =
-                make_uint4(v.x & m4, v.y & m4, v.z & m4, v.w & m4);
-            *reinterpret_cast<uint4*>(buf + C::A_BYTES + gm_slot(C::BN / 32, (p >> 1) * 2 + 1, r, p & 1)) =
-                make_uint4((v.x >> 4) & m4, (v.y >> 4) & m4, (v.z >> 4) & m4, (v.w >> 4) & m4);
-        }
-        if ((st & 1) == 0) {
-            if (tid < C::BN) {
-                uint8_t* sc = rec + C::SC;
-                _Float16* mo = reinterpret_cast<_Float16*>(rec + C::MO) + tid * 16;
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    uint32_t sc2, m2;
-                    kf_q4k_scales(hdr.y, hdr.z, hdr.w, j, sc2, m2);
-                    sc[(2 * j) * C::BN + tid] = (uint8_t)(sc2 & 0xffu);
-                    sc[(2 * j + 1) * C::BN + tid] = (uint8_t)(sc2 >> 8);
-                    mo[2 * j] = (_Float16)(float)(64u * (m2 & 0xffu));
-                    mo[2 * j + 1] = (_Float16)(float)(64u * (m2 >> 8));
-                    mo[8 + 2 * j] = (_Float16)(float)(m2 & 0xffu);
-                    mo[8 + 2 * j + 1] = (_Float16)(float)(m2 >> 8);
-                }
-                reinterpret_cast<float2*>(rec + C::DD)[tid] = make_float2(kf_h2f(hdr.x & 0xffffu), kf_h2f(hdr.x >> 16));
-            }
-            if (tid < C::BM) {
-                // accumulator row order: tile t, half h = (row / 4) % 2, register (row % 4) + 4 (row / 8)
-                const int t = tid >> 5, rr = tid & 31;
-                reinterpret_cast<float*>(rec + C::DX)[t * 32 + ((rr >> 2) & 1) * 16 + (rr & 3) + 4 * (rr >> 3)] = dx;
-            }
-#pragma unroll
-            for (int i = 0; i < C::XS; i++) {
-                const int c = tid + GM_THREADS * i;
-                const int v = xs[i];
-                _Float16* xo = reinterpret_cast<_Float16*>(rec + C::XO) + (c >> 3) * 16;
-                xo[c & 7] = (_Float16)(float)(v >> 6);     // |hi| <= 64: exact
-                xo[8 + (c & 7)] = (_Float16)(float)(v & 63);
-            }
-        }
-    }
 };
 
 template <int WM, int WN, int TM, int TN>
-__global__ void __launch_bounds__(GM_THREADS, 2) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
-                                                                 const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
-                                                                 const float* __restrict__ bias, const float* __restrict__ res,
-                                                                 float* __restrict__ y, int M, int N, int K) {
-    using C = GkCfg<WM, WN, TM, TN>;
-    extern __shared__ __align__(16) uint8_t smem[];
+__global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q4k_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
+                                                                    const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
+                                                                    const float* __restrict__ xd32, const float* __restrict__ bias,
+                                                                    const float* __restrict__ res, float* __restrict__ y, int M, int N,
+                                                                    int K) {
+    using C = GdCfg<WM, WN, TM, TN>;
+    // four distinct LDS objects, so that the compiler can tell a DMA into one buffer from reads of another (with one
+    // array it waits for every outstanding DMA before each LDS read)
+    __shared__ __align__(16) uint8_t buf0[C::STAGE];
+    __shared__ __align__(16) uint8_t buf1[C::STAGE];
+    __shared__ __align__(16) uint8_t rec0[C::REC];
+    __shared__ __align__(16) uint8_t rec1[C::REC];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    const int m0 = blockIdx.y * C::BM, n0 = blockIdx.x * C::BN;
-    const int st1 = K / GM_BK;
+    int tm, tn;
+    gm_tile((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int kg = K >> 5;
+    const int nsb = K / KF_Q4_K_BLOCK;
+    const int half = lane >> 5, r32 = lane & 31;
+
+    // the DMA instructions of one stage (and, with rec, of its super-block record), spread over the waves
+    auto dma = [&](int st, uint8_t* buf, uint8_t* rec) {
+        const int sb = st >> 1;
+        for (int q = wave; q < C::NA; q += C::W) {
+            const int g = q / C::MT, t = q % C::MT;
+            const int m = min(m0 + t * 32 + r32, M - 1);
+            kf_dma16(xq + (int64_t)m * K + st * GM_BK + g * 32 + half * 16, buf + q * 1024);
+        }
+        for (int q = wave; q < C::NB; q += C::W) {
+            const int p = q / C::NT, t = q % C::NT;
+            const int n = min(n0 + t * 32 + r32, N - 1);
+            kf_dma16(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES + 16 + 32 * (2 * (st & 1) + p) + half * 16,
+                     buf + C::A_BYTES + q * 1024);
+        }
+        if (rec) {
+            constexpr int NR = C::NH + C::ND + C::NX;
+            for (int q = wave; q < NR; q += C::W) {
+                if (q < C::NH) {
+                    const int n = min(n0 + q * 64 + lane, N - 1);
+                    kf_dma16(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES, rec + C::HDR + q * 1024);
+                } else if (q < C::NH + C::ND) {
+                    const int qq = q - C::NH;
+                    const int m = min(m0 + qq * 64 + lane, M - 1);
+                    kf_dma4(xd32 + (int64_t)m * kg + sb * 8, rec + C::DX + qq * 256);
+                } else {
+                    const int qq = q - C::NH - C::ND;
+                    const int m = min(m0 + qq * 32 + (lane >> 1), M - 1);
+                    kf_dma16(xs32 + (int64_t)m * kg + sb * 8 + (lane & 1) * 4, rec + C::XS + qq * 1024);
+                }
+            }
+        }
+    };
 
     v16f acc[TM][TN];
-    v16i S[TM][TN];
+    v16i slo[TM][TN], shi[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            acc[i][j] = v16f{};
-            S[i][j] = v16i{};
-        }
+        for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
 
-    GkStage<C> pf;
-    pf.load(w, row_bytes, xq, xs32, xd32, m0, n0, M, N, K, 0, tid);
-    pf.store(smem, smem + 2 * C::STAGE, 0, tid);
-    __syncthreads();
-    for (int st = 0; st < st1; st++) {
-        const uint8_t* buf = smem + (st & 1) * C::STAGE;
-        const uint8_t* rec = smem + 2 * C::STAGE + ((st >> 1) & 1) * C::REC;
-        const int gb = (st & 1) * GM_G;  // the stage's first group within its super-block
-#if !(KF_GK_ABLATE & 1)
-        pf.load(w, row_bytes, xq, xs32, xd32, m0, n0, M, N, K, min(st + 1, st1 - 1), tid);
-#endif
-        struct Ops {
-            v4i a[TM], b[TN];
-            int sc[TN];
-        };
-        auto read_ops = [&](Ops& o, int g) {
+    // one stage: pairs p = 0, 1 of the stage, pair P = 2 h + p of the super-block; the chains restart with the
+    // super-block's first group
+    auto stage = [&](const uint8_t* buf, const uint4 (&hd)[TN], int h) {
 #pragma unroll
-            for (int t = 0; t < TM; t++) o.a[t] = *reinterpret_cast<const v4i*>(buf + gm_operand(C::BM / 32, g, wm * TM + t, lane));
+        for (int p = 0; p < 2; p++) {
+            v4i bl[2][TN], bh[2][TN];
 #pragma unroll
-            for (int t = 0; t < TN; t++) {
-                o.b[t] = *reinterpret_cast<const v4i*>(buf + C::A_BYTES + gm_operand(C::BN / 32, g, wn * TN + t, lane));
-                o.sc[t] = rec[C::SC + (gb + g) * C::BN + (wn * TN + t) * 32 + (lane & 31)];
+            for (int j = 0; j < TN; j++) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(buf + C::A_BYTES + ((p * C::NT + wn * TN + j) * 64 + lane) * 16);
+                uint32_t sc2, m2;
+                kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, 2 * h + p, sc2, m2);
+                const uint32_t s0 = sc2 & 0xffu, s1 = sc2 >> 8;
+                const uint32_t l0 = s0 & 7u, u0 = s0 >> 3, l1 = s1 & 7u, u1 = s1 >> 3;
+                const uint32_t m4 = 0x0f0f0f0fu;
+                const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t lo = v[e] & m4, hi = (v[e] >> 4) & m4;
+                    bl[0][j][e] = (int)gs_pmul(lo, l0);
+                    bh[0][j][e] = (int)gs_pmul(lo, u0);
+                    bl[1][j][e] = (int)gs_pmul(hi, l1);
+                    bh[1][j][e] = (int)gs_pmul(hi, u1);
+                }
             }
-        };
-        Ops cur;
-        read_ops(cur, 0);
-#pragma unroll 1
-        for (int g = 0; g < GM_G; g++) {
-            Ops nxt;
-            read_ops(nxt, min(g + 1, GM_G - 1));
 #pragma unroll
-            for (int i = 0; i < TM; i++)
+            for (int gg = 0; gg < 2; gg++) {
+                const int g = 2 * p + gg;
+                v4i a[TM];
 #pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(cur.a[i], cur.b[j], v16i{}, 0, 0, 0);
-                    // |I_j| <= 15 * 128 * 32 and sc_j < 64: 24-bit multiplies are exact
+                for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const v4i*>(buf + ((g * C::MT + wm * TM + i) * 64 + lane) * 16);
 #pragma unroll
-                    for (int r = 0; r < 16; r++) S[i][j][r] += __mul24(c[r], cur.sc[j]);
-                }
-            cur = nxt;
-        }
-        if (st & 1) {
-            // end of a super-block: mins by MFMA, then the float rescale of S and mins, and S restarts
+                for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int i = 0; i < TM; i++) {
-                const int tr = wm * TM + i;
-                const v8h xo = *reinterpret_cast<const v8h*>(rec + C::XO + (tr * 32 + (lane & 31)) * 32 + (lane >> 5) * 16);
-                const float* dxp = reinterpret_cast<const float*>(rec + C::DX) + tr * 32 + (lane >> 5) * 16;
-                v16f dxv;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const v4f t4 = *reinterpret_cast<const v4f*>(dxp + 4 * q);
-#pragma unroll
-                    for (int e = 0; e < 4; e++) dxv[4 * q + e] = t4[e];
-                }
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    const int col = (wn * TN + j) * 32 + (lane & 31);
-                    const v8h mo = *reinterpret_cast<const v8h*>(rec + C::MO + col * 32 + (lane >> 5) * 16);
-                    const float2 dd = reinterpret_cast<const float2*>(rec + C::DD)[col];
-                    const v16f mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo, v16f{}, 0, 0, 0);
-#pragma unroll
-                    for (int r = 0; r < 16; r++) {
-                        const float t = fmaf(-dd.y, mins[r], dd.x * (float)S[i][j][r]);
-                        acc[i][j][r] = fmaf(t, dxv[r], acc[i][j][r]);
+                    for (int j = 0; j < TN; j++) {
+                        const bool z = h == 0 && g == 0;
+                        slo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bl[gg][j], z ? v16i{} : slo[i][j], 0, 0, 0);
+                        shi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bh[gg][j], z ? v16i{} : shi[i][j], 0, 0, 0);
                     }
-                    S[i][j] = v16i{};
+            }
+        }
+    };
+
+    dma(0, buf0, rec0);
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+    __syncthreads();
+#pragma unroll 1
+    for (int sb = 0; sb < nsb; sb++) {
+        // everything the super-block needs from its record is read into registers before any DMA of the
+        // super-block is issued: the record's buffer is refilled during the odd stage
+        const uint8_t* rec = (sb & 1) ? rec1 : rec0;
+        uint4 hd[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) hd[j] = *reinterpret_cast<const uint4*>(rec + C::HDR + ((wn * TN + j) * 32 + r32) * 16);
+        v4i xsv[TM][2];
+        v4f dxq[TM][4];
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int tr = wm * TM + i;
+            const int32_t* xsr = reinterpret_cast<const int32_t*>(rec + C::XS) + (tr * 32 + r32) * 8;
+            xsv[i][0] = *reinterpret_cast<const v4i*>(xsr);
+            xsv[i][1] = *reinterpret_cast<const v4i*>(xsr + 4);
+            // accumulator register r holds row (r % 4) + 8 (r / 4) + 4 (lane / 32)
+            const float* dxp = reinterpret_cast<const float*>(rec + C::DX) + tr * 32 + half * 4;
+#pragma unroll
+            for (int q = 0; q < 4; q++) dxq[i][q] = *reinterpret_cast<const v4f*>(dxp + 8 * q);
+        }
+        // even stage: fetch the odd one
+        dma(2 * sb + 1, buf1, nullptr);
+        stage(buf0, hd, 0);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        // odd stage: fetch the next super-block's even stage and record
+        if (sb + 1 < nsb) dma(2 * sb + 2, buf0, (sb & 1) ? rec0 : rec1);
+        stage(buf1, hd, 1);
+        // the super-block's rescale: mins by MFMA, then acc += dx (d S - dmin mins)
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            v8h xo;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // bsum = 64 hi + lo, hi in [-64, 63], lo in [0, 63]: both exact in f16
+                xo[e] = (_Float16)(float)(half ? (xsv[i][0][e] & 63) : (xsv[i][0][e] >> 6));
+                xo[4 + e] = (_Float16)(float)(half ? (xsv[i][1][e] & 63) : (xsv[i][1][e] >> 6));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                v8h mo;
+#pragma unroll
+                for (int pj = 0; pj < 4; pj++) {
+                    uint32_t sc2, m2;
+                    kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, pj, sc2, m2);
+                    const uint32_t f = half ? 1u : 64u;
+                    mo[2 * pj] = (_Float16)(float)(f * (m2 & 0xffu));
+                    mo[2 * pj + 1] = (_Float16)(float)(f * (m2 >> 8));
+                }
+                const float d = kf_h2f(hd[j].x & 0xffffu), dmin = kf_h2f(hd[j].x >> 16);
+                const v16f mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo, v16f{}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int s = slo[i][j][r] + (shi[i][j][r] << 3);  // |S| < 2^25: exact
+                    const float t = fmaf(-dmin, mins[r], d * (float)s);
+                    acc[i][j][r] = fmaf(t, dxq[i][r >> 2][r & 3], acc[i][j][r]);
                 }
             }
         }
-        if (st + 1 < st1) pf.store(smem + ((st + 1) & 1) * C::STAGE, smem + 2 * C::STAGE + (((st + 1) >> 1) & 1) * C::REC, st + 1, tid);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
         __syncthreads();
     }
 
@@ -655,17 +669,188 @@ __global__ void __launch_bounds__(GM_THREADS, 2) gemm_q4k_kernel(const uint8_t* 
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++) {
-            const int n = n0 + (wn * TN + j) * 32 + (lane & 31);
+            const int n = n0 + (wn * TN + j) * 32 + r32;
             if (n >= N) continue;
             const float bn = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * (lane >> 5);
+                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
                 if (m >= M) continue;
                 const int64_t o = (int64_t)m * N + n;
                 y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
             }
         }
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t gemm_q4k_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
+                               const float* bias, const float* res, float* y, int M, int N, int K, hipStream_t s) {
+    using C = GdCfg<WM, WN, TM, TN>;
+    auto* fn = gemm_q4k_dma_kernel<WM, WN, TM, TN>;
+    static_assert(C::TOTAL <= 65536, "static LDS");
+    dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
+    fn<<<grid, C::THREADS, 0, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
+}
+
+// ----------------------------------------------------------------------------------- q8_0 prefill GEMM, DMA staging
+// The product of gemm_q8_0_kernel (per group and 32 x 32 tile: the exact int32 dots I_g from v_mfma_i32_32x32x32_i8,
+// the outer product d_x (x) d_w of the f16 scales from one v_mfma_f32_32x32x16_f16 with a single non-zero k slot,
+// then a convert and an FMA per output) with all staging done by global_load_lds DMA, as in the q4_K GEMM:
+//   * activations: [group][32-row tile] 1 KB blocks in MFMA order, one DMA instruction each;
+//   * weights: a stage's four q8_0 blocks of a row are 136 bytes at row offset 136 st, 8-byte aligned; each row's
+//     16-byte aligned 144-byte window around them is copied whole ([row][144] in LDS: nine 16-byte pieces, the
+//     stage's data at offset (136 st) % 16), so the DMA needs only aligned pieces. Rows are 16-byte aligned when
+//     K % 256 == 0, and the last stage (st odd) ends exactly at the row's end;
+//   * activation scales: [row][4] f32 per stage.
+// One buffer is a static LDS array and the other the dynamic one: two distinct objects, so the compiler can tell a DMA
+// into one from reads of the other (36 KB each, above the static limit for both). Eight waves, each a 64 x 32 tile;
+// blocks in XCD order. Wave tiles of 2 x 2 measured slower (their 128 x 256 block halves the blocks per CU).
+// gemm_q8_0_kernel (register staging) remains for K % 256 != 0.
+template <int WM, int WN, int TM, int TN>
+struct GqCfg {
+    static constexpr int W = WM * WN, THREADS = 64 * W;
+    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+    static constexpr int MT = BM / 32, NT = BN / 32;
+    static constexpr int ROW = 144;                       // LDS bytes of a weight row's window
+    static constexpr int A_BYTES = MT * GM_G * 1024;
+    static constexpr int B_OFF = A_BYTES, B_BYTES = BN * ROW;
+    static constexpr int D_OFF = B_OFF + B_BYTES, D_BYTES = ((BM + 63) / 64) * 1024;
+    static constexpr int STAGE = D_OFF + D_BYTES;
+    static constexpr int NA = MT * GM_G, NB = (BN * 9 + 63) / 64, ND = (BM + 63) / 64;
+    static_assert(BN * 9 % 64 == 0, "whole DMA instructions for the weight windows");
+};
+
+template <int WM, int WN, int TM, int TN>
+__global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
+                                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd32,
+                                                                     const float* __restrict__ bias, const float* __restrict__ res,
+                                                                     float* __restrict__ y, int M, int N, int K) {
+    using C = GqCfg<WM, WN, TM, TN>;
+    __shared__ __align__(16) uint8_t buf0[C::STAGE];
+    extern __shared__ __align__(16) uint8_t buf1[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    gm_tile((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int kg = K >> 5;
+    const int nst = K / GM_BK;
+    const int half = lane >> 5, r32 = lane & 31;
+
+    auto dma = [&](int st, uint8_t* buf) {
+        for (int q = wave; q < C::NA; q += C::W) {
+            const int g = q / C::MT, t = q % C::MT;
+            const int m = min(m0 + t * 32 + r32, M - 1);
+            kf_dma16(xq + (int64_t)m * K + st * GM_BK + g * 32 + half * 16, buf + q * 1024);
+        }
+        const int64_t wbase = (int64_t)(136 * st) & ~(int64_t)15;
+        for (int q = wave; q < C::NB; q += C::W) {
+            const int p = q * 64 + lane, r = p / 9, pc = p - 9 * r;
+            const int n = min(n0 + r, N - 1);
+            kf_dma16(w + (int64_t)n * row_bytes + wbase + 16 * pc, buf + C::B_OFF + q * 1024);
+        }
+        for (int q = wave; q < C::ND; q += C::W) {
+            const int m = min(m0 + q * 64 + lane, M - 1);
+            kf_dma16(xd32 + (int64_t)m * kg + st * GM_G, buf + C::D_OFF + q * 1024);
+        }
+    };
+
+    v16f acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
+
+    // one group per trip: fully unrolled, the scheduler hoists every group's MFMAs above the rescales and spills
+    auto stage = [&](const uint8_t* buf, int st) {
+        const int wo = (136 * st) & 15;  // the stage's offset in its weight windows
+#pragma unroll 1
+        for (int g = 0; g < GM_G; g++) {
+            v4i a[TM], b[TN];
+            uint32_t sa[TM], sb[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++) {
+                a[i] = *reinterpret_cast<const v4i*>(buf + ((g * C::MT + wm * TM + i) * 64 + lane) * 16);
+                // Q8_0-kind activation scales are f16-rounded values, so this conversion is exact
+                const float dx = reinterpret_cast<const float*>(buf + C::D_OFF)[((wm * TM + i) * 32 + r32) * 4 + g];
+                sa[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)dx) & (uint32_t)(half - 1);  // lanes >= 32: zero
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint8_t* rp = buf + C::B_OFF + ((wn * TN + j) * 32 + r32) * C::ROW + wo + g * KF_Q8_0_BYTES;
+                const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(rp + 2 + 16 * half);
+                b[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                sb[j] = *reinterpret_cast<const uint16_t*>(rp);
+            }
+            v16i c[TM][TN];
+            v16f s[TM][TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
+                    const v4u ua = {sa[i], 0u, 0u, 0u}, ub = {sb[j], 0u, 0u, 0u};
+                    s[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ua), __builtin_bit_cast(v8h, ub), v16f{}, 0, 0, 0);
+                }
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) acc[i][j][r] = fmaf((float)c[i][j][r], s[i][j][r], acc[i][j][r]);
+        }
+    };
+
+    dma(0, buf0);
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+    __syncthreads();
+#pragma unroll 1
+    for (int st = 0; st < nst; st += 2) {
+        // nst is even (K % 256 == 0)
+        dma(st + 1, buf1);
+        stage(buf0, st);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        if (st + 2 < nst) dma(st + 2, buf0);
+        stage(buf1, st + 1);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+    }
+
+    // 32 x 32 accumulator layout: lane l holds column l % 32; register r holds row (r % 4) + 8 (r / 4) + 4 (l / 32)
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + (wn * TN + j) * 32 + r32;
+            if (n >= N) continue;
+            const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
+            }
+        }
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t gemm_q8_0_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
+                                float* y, int M, int N, int K, hipStream_t s) {
+    using C = GqCfg<WM, WN, TM, TN>;
+    auto* fn = gemm_q8_0_dma_kernel<WM, WN, TM, TN>;
+    static bool lds_set = false;
+    if (!lds_set) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::STAGE);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
+    dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
+    fn<<<grid, C::THREADS, C::STAGE, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
 }
 
 template <int WM, int WN, int TM, int TN>
@@ -681,22 +866,6 @@ hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
     }
     dim3 grid((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
     fn<<<grid, GM_THREADS, 2 * C::STAGE, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
-    return hipGetLastError();
-}
-
-template <int WM, int WN, int TM, int TN>
-hipError_t gemm_q4k_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
-                           const float* res, float* y, int M, int N, int K, hipStream_t s) {
-    using C = GkCfg<WM, WN, TM, TN>;
-    auto* fn = gemm_q4k_kernel<WM, WN, TM, TN>;
-    static bool lds_set = false;
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::TOTAL);
-        if (e != hipSuccess) return e;
-        lds_set = true;
-    }
-    dim3 grid((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
-    fn<<<grid, GM_THREADS, C::TOTAL, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, M, N, K);
     return hipGetLastError();
 }
 
@@ -749,6 +918,7 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
         if (M <= 16) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);
         if (M <= 64) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);  // M / 16 row blocks
     }
+    if (K % 256 == 0 && row_bytes % 16 == 0) return gemm_q8_0_dma_launch<2, 4, 2, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
     return gemm_launch<2, 2, 2, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
 }
 
@@ -757,7 +927,7 @@ hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act,
                               int N, int K, hipStream_t s) {
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
     const char* base = static_cast<const char*>(act);
-    return gemm_q4k_launch<2, 2, 2, 2>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
-                                       reinterpret_cast<const int32_t*>(base + o.s32), reinterpret_cast<const float*>(base + o.d32), bias,
-                                       res, y, M, N, K, s);
+    return gemm_q4k_dma_launch<2, 4, 2, 1>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
+                                           reinterpret_cast<const int32_t*>(base + o.s32), reinterpret_cast<const float*>(base + o.d32), bias,
+                                           res, y, M, N, K, s);
 }

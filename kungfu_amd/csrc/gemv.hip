@@ -300,20 +300,9 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
 // all its row iterations are requested before the block waits on the (small, L2-resident) activation row.
 // Requires 16-byte aligned rows (q4_K always; q8_0 when the row width is a multiple of 128).
 
-// s_waitcnt immediate waiting until at most N vector memory loads are outstanding (gfx9 encoding: vmcnt bits 3:0 and
-// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima so they are not waited on)
-#define KF_WAITCNT_VM(N) ((((N) & 15)) | (7 << 4) | (15 << 8) | ((((N) >> 4) & 3) << 14))
+__device__ __forceinline__ void gv_dma16(const void* src, void* lds_base) { kf_dma16(src, lds_base); }
 
-typedef __attribute__((address_space(3))) void kf_lds_void;
-typedef const __attribute__((address_space(1))) void kf_gbl_void;
-
-__device__ __forceinline__ void gv_dma16(const void* src, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 16, 0, 0);
-}
-
-__device__ __forceinline__ void gv_dma4(const void* src, void* lds_base) {
-    __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 4, 0, 0);
-}
+__device__ __forceinline__ void gv_dma4(const void* src, void* lds_base) { kf_dma4(src, lds_base); }
 
 struct GdLds {
     size_t sums, scales, wbuf, part, total;

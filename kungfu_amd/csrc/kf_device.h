@@ -77,3 +77,20 @@ __device__ __forceinline__ uint4 kf_load_stream_u4_unaligned(const void* p) {
     const kf_u32x4_a2 v = __builtin_nontemporal_load(reinterpret_cast<const kf_u32x4_a2*>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// s_waitcnt immediate waiting until at most N vector memory loads are outstanding (gfx9 encoding: vmcnt bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima so they are not waited on)
+#define KF_WAITCNT_VM(N) ((((N) & 15)) | (7 << 4) | (15 << 8) | ((((N) >> 4) & 3) << 14))
+
+typedef __attribute__((address_space(3))) void kf_lds_void;
+typedef const __attribute__((address_space(1))) void kf_gbl_void;
+
+// global_load_lds_dwordx4 / _dword (gfx950): lane l of one instruction writes its 16 (4) bytes at the instruction's
+// LDS base + 16 l (4 l). lds_base must be the same for every lane of the wave.
+__device__ __forceinline__ void kf_dma16(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void kf_dma4(const void* src, void* lds_base) {
+    __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 4, 0, 0);
+}
