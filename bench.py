@@ -206,6 +206,34 @@ def moe_section(dev, seed=0):
             "touched_experts": touched, "weight_bytes": wbytes, "tokens": rows, "top_k": n_used}
 
 
+def fused_section(dev):
+    """The fused activation producers (SURVEY's first "next" row): rms_norm_q8 over the hidden width and gated_act_q8
+    over the FFN width (silu, gate and up as the halves of one fused gate+up output row), at decode (1 row) and
+    prefill (2048 rows), Q8K kind (the q4_K weights' kind). GB/s over the f32 read and the scratch written; quant_act
+    of the same f32 input beside it, for the cost the fusion removes (the f32 write and re-read of the normed values)."""
+    import torch
+
+    import kungfu_amd as kf
+
+    out = {}
+    for rows in (1, 2048):
+        n = 4096
+        x = torch.from_numpy(kf.synth_normal(2, 1.0, rows * n).reshape(rows, n)).to(dev)
+        w = torch.from_numpy(kf.synth_normal(3, 1.0, n)).to(dev)
+        act = kf.alloc_act(rows, n, dev)
+        us = time_launches(lambda i: kf.rms_norm_q8(x, act, kf.ACT_Q8K, w, None, 1e-5), 200)
+        us_q = time_launches(lambda i: kf.quant_act(x, act, kf.ACT_Q8K), 200)
+        nb = 4 * rows * n + 4 * n + kf.act_bytes(rows, n)
+        out[f"rms_norm_q8_{rows}x{n}"] = {"us": round(us, 3), "GBs": round(nb / us / 1e3, 1), "quant_act_us": round(us_q, 3)}
+        n = 14336
+        gu = torch.from_numpy(kf.synth_normal(4, 1.0, rows * 2 * n).reshape(rows, 2 * n)).to(dev)
+        act = kf.alloc_act(rows, n, dev)
+        us = time_launches(lambda i: kf.gated_act_q8(gu[:, :n], gu[:, n:], act, kf.ACT_Q8K, rows, n, 2 * n), 200)
+        nb = 8 * rows * n + kf.act_bytes(rows, n)
+        out[f"gated_act_q8_{rows}x{n}"] = {"us": round(us, 3), "GBs": round(nb / us / 1e3, 1)}
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_up_traffic.md")
 
 
@@ -267,7 +295,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "fused", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -281,7 +309,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "fused": fused_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -357,6 +385,7 @@ def main():
     out["int8_gemm_q4_k"] = gemm_q4_k_section(dev)
     out["small_batch_q8_0"] = small_batch_section(dev)
     out["moe_q4_k"] = moe_section(dev)
+    out["fused_producers"] = fused_section(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -73,6 +73,27 @@ int kf_hip_act_kind(uint32_t ty);
  * 256 (Q8K kind). */
 int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void* stream);
 
+/* Fused producers: the int8 activations straight from the preceding norm or gated activation, with no f32 round
+ * trip through memory. Same scratch, kinds and width rules as kf_hip_quant_act; every f32 pointer 16-byte aligned.
+ *
+ * rms_norm of each row (x [rows][n], nullable weight w [n] and bias b [n], eps >= 0) then quantization. Replaces
+ * rms_norm_q8 (crates/kf-backend-cuda/src/kernels/fused.cu:24-45, launched at exec.rs:2439); the values quantized are
+ * the CPU backend's ops::rms_norm (crates/kf-backend-cpu/src/ops.rs:222-239) bit for bit: f64 sum of squares, IEEE
+ * square root and division, unfused multiply-adds. */
+int kf_hip_rms_norm_q8(const float* x, const float* w, const float* b, int rows, int n, float eps, int kind, void* act, void* stream);
+
+/* Activation codes of kf_hip_gated_act_q8 (those of the reference GPU's kf_act, common.cuh:93-99). */
+#define KF_GLU_SILU 0
+#define KF_GLU_RELU 2
+#define KF_GLU_RELU_SQR 4
+
+/* act(gate) * up of each row, then quantization; gate and up rows are `stride` floats apart (stride = 2 n for the
+ * two halves of one fused gate/up output row, n for separate tensors). Replaces gated_act_q8 (fused.cu:48-65,
+ * exec.rs:2441-2444) for Op::GatedAct / Op::GatedActFused without a limit; the values are ops::gated
+ * (crates/kf-backend-cpu/src/ops.rs:44-57) with silu's exp taken in f64 and rounded to f32. Other activations
+ * return KF_E_UNSUPPORTED. */
+int kf_hip_gated_act_q8(const float* gate, const float* up, int rows, int n, int stride, int act_fn, int kind, void* act, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Products on native block bytes against quantized activations.
  * y[r][o] = sum of the row's blocks (d_w * d_x * int32 dot, minus the q4_K min term) + bias[o] + res[r][o]
@@ -88,9 +109,10 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
 
 /* Batched / prefill int8 GEMM on native rows: y [rows][n_out] from `rows` activation rows of the weight type's kind.
  * q8_0 (Q8_0-kind activations, n a multiple of 128): one int8 MFMA per 32-column group gives the exact int32 block
- * dots, rescaled by the group's activation and weight scales. q4_K (Q8K-kind activations): one int8 MFMA per 32-column
- * group on the unpacked nibbles, the 6-bit scale folded in with an integer multiply-add, the mins term by an exact f16
- * MFMA per super-block, and the float rescale once per 256 columns.
+ * dots, rescaled by the group's activation and weight scales. q4_K (Q8K-kind activations, n a multiple of 256): the
+ * 6-bit scales split into two 3-bit halves folded into two int8 operand planes, so two int8 MFMA chains form the
+ * exact super-block integer; the mins term by an exact f16 MFMA per super-block, and the float rescale once per 256
+ * columns.
  * Replaces kf8_gemm_dense / Store::gemm (crates/kf-backend-cuda/src/kernels/kf8.cu:375-395, HAS_M for q4_K;
  * crates/kf-backend-cuda/src/kf8.rs:310-323) without the KF8 unpack pass (kf_unpack_i8, quant.cuh:585-601): the
  * native q8_0 / q4_K bytes are read directly. */

@@ -66,6 +66,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_act_offsets": ([I, I, P], None),
         "kf_hip_act_kind": ([U], I),
         "kf_hip_quant_act": ([P, P, I, I, I, P], I),
+        "kf_hip_rms_norm_q8": ([P, P, P, I, I, ctypes.c_float, I, P, P], I),
+        "kf_hip_gated_act_q8": ([P, P, I, I, I, I, I, P, P], I),
         "kf_hip_gemv": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_matmul": ([U, P, I, I, P, I, P, P, P, P, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
@@ -171,6 +173,21 @@ def _stream(stream) -> int | None:
 def quant_act(x, act, kind: int, stream=None) -> None:
     rows, n = x.shape
     check(lib().kf_hip_quant_act(_ptr(x), _ptr(act), rows, n, kind, _stream(stream)))
+
+
+GLU_SILU, GLU_RELU, GLU_RELU_SQR = 0, 2, 4
+
+
+def rms_norm_q8(x, act, kind: int, w=None, b=None, eps: float = 1e-5, stream=None) -> None:
+    """rms_norm of each row of x [rows][n] (nullable weight / bias [n]) quantized into `act` (kf_hip_rms_norm_q8)."""
+    rows, n = x.shape
+    check(lib().kf_hip_rms_norm_q8(_ptr(x), _ptr(w), _ptr(b), rows, n, eps, kind, _ptr(act), _stream(stream)))
+
+
+def gated_act_q8(gate, up, act, kind: int, rows: int, n: int, stride: int, act_fn: int = GLU_SILU, stream=None) -> None:
+    """act_fn(gate) * up of `rows` rows of n columns, rows `stride` floats apart, quantized into `act`
+    (kf_hip_gated_act_q8). gate/up may be views into one fused [rows][2n] tensor."""
+    check(lib().kf_hip_gated_act_q8(_ptr(gate), _ptr(up), rows, n, stride, act_fn, kind, _ptr(act), _stream(stream)))
 
 
 def gemv(ty: int, w, act, y, rows: int, n: int, n_out: int, bias=None, res=None, stream=None) -> None:

@@ -16,6 +16,10 @@
 
 // Launchers in the .hip translation units
 hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s);
+hipError_t kf_launch_rms_norm_q8(const float* x, const float* w, const float* b, float eps, void* act, int rows, int n, int kind,
+                                 hipStream_t s);
+hipError_t kf_launch_gated_act_q8(const float* gate, const float* up, int stride, int act_fn, void* act, int rows, int n, int kind,
+                                  hipStream_t s);
 hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
                            const float* bias, const float* res, float* y, int n, int n_out, int maxit, hipStream_t s);
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
@@ -128,6 +132,36 @@ int kf_hip_quant_act(const float* x, void* act, int rows, int n, int kind, void*
     if (!aligned(x, 16) || !aligned(act, KF_ACT_ALIGN)) return fail(KF_E_INVALID, "x must be 16-byte and act 256-byte aligned");
     const hipError_t e = kf_launch_quant_act(x, act, rows, n, kind, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "quant_act launch");
+}
+
+// Shared checks of the fused producers: kind, widths, alignment of the f32 inputs (16 bytes) and of the scratch
+static int check_producer(int kind, int rows, int n, const void* act) {
+    if (kind != KF_ACT_Q8_0 && kind != KF_ACT_Q8K) return fail(KF_E_UNSUPPORTED, "activation kind %d (3=Q8_0, 4=Q8K)", kind);
+    const int block = kind == KF_ACT_Q8_0 ? 32 : 256;
+    if (rows < 1 || n <= 0 || n % block != 0) return fail(KF_E_INVALID, "%d rows of %d columns for blocks of %d", rows, n, block);
+    if (!act || !aligned(act, KF_ACT_ALIGN)) return fail(KF_E_INVALID, "act must be a 256-byte aligned device pointer");
+    return KF_OK;
+}
+
+int kf_hip_rms_norm_q8(const float* x, const float* w, const float* b, int rows, int n, float eps, int kind, void* act, void* stream) {
+    const int rc = check_producer(kind, rows, n, act);
+    if (rc != KF_OK) return rc;
+    if (!x || !aligned(x, 16) || (w && !aligned(w, 16)) || (b && !aligned(b, 16)))
+        return fail(KF_E_INVALID, "x (and w, b when given) must be 16-byte aligned device pointers");
+    if (!(eps >= 0.0f)) return fail(KF_E_INVALID, "eps %g", (double)eps);
+    const hipError_t e = kf_launch_rms_norm_q8(x, w, b, eps, act, rows, n, kind, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "rms_norm_q8 launch");
+}
+
+int kf_hip_gated_act_q8(const float* gate, const float* up, int rows, int n, int stride, int act_fn, int kind, void* act, void* stream) {
+    const int rc = check_producer(kind, rows, n, act);
+    if (rc != KF_OK) return rc;
+    if (act_fn != KF_GLU_SILU && act_fn != KF_GLU_RELU && act_fn != KF_GLU_RELU_SQR)
+        return fail(KF_E_UNSUPPORTED, "activation %d (0 silu, 2 relu, 4 relu squared)", act_fn);
+    if (!gate || !up || !aligned(gate, 16) || !aligned(up, 16)) return fail(KF_E_INVALID, "gate and up must be 16-byte aligned device pointers");
+    if (stride < n || stride % 4 != 0) return fail(KF_E_INVALID, "row stride %d for %d columns (a multiple of 4, at least n)", stride, n);
+    const hipError_t e = kf_launch_gated_act_q8(gate, up, stride, act_fn, act, rows, n, kind, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "gated_act_q8 launch");
 }
 
 int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int rows,

@@ -68,6 +68,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.kfo_moe_ffn.argtypes = [U, P, P, P, I, I, I, P, I, P, P, I, P, I]
     L.kfo_moe_ffn_i8.argtypes = [U, P, P, P, I, I, I, P, I, P, P, I, P, I]
     L.kfo_silu.argtypes = [ctypes.c_float]
+    L.kfo_rms_norm.argtypes = [P, P, P, I, I, ctypes.c_float, P]
+    L.kfo_gated.argtypes = [I, P, P, I, I, I, P]
     L.kfo_silu.restype = ctypes.c_float
 
 
@@ -222,6 +224,27 @@ def moe_ffn_i8(ty, gate, up, down, n_exp, n_embd, n_ff, x, sel, wts, threads: in
 
 def silu(v: float) -> float:
     return float(lib().kfo_silu(v))
+
+
+def rms_norm(x: np.ndarray, w=None, b=None, eps: float = 1e-5) -> np.ndarray:
+    """ops::rms_norm (crates/kf-backend-cpu/src/ops.rs:222-239) of rows x [rows][n]."""
+    x = _c(x, np.float32)
+    rows, n = x.shape
+    out = np.empty_like(x)
+    rc = lib().kfo_rms_norm(_p(x), _p(None if w is None else _c(w, np.float32)), _p(None if b is None else _c(b, np.float32)),
+                            rows, n, eps, _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def gated(act: int, gate: np.ndarray, up: np.ndarray, rows: int, n: int, stride: int) -> np.ndarray:
+    """ops::gated without a limit (crates/kf-backend-cpu/src/ops.rs:44-57): act(gate) * up, act 0 silu / 2 relu /
+    4 relu squared; gate and up are flat arrays whose rows are `stride` floats apart."""
+    gate, up = _c(gate, np.float32), _c(up, np.float32)
+    out = np.empty((rows, n), np.float32)
+    rc = lib().kfo_gated(act, _p(gate), _p(up), rows, n, stride, _p(out))
+    assert rc == 0, rc
+    return out
 
 
 def load_fixture(path: str):

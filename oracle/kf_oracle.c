@@ -526,6 +526,41 @@ int kfo_matmul_i8(uint32_t ty, const uint8_t* w, int n_in, int n_out, const floa
 /* ops::silu: crates/kf-backend-cpu/src/ops.rs:6-8 */
 float kfo_silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* ops::rms_norm: crates/kf-backend-cpu/src/ops.rs:222-239. The mean square sums f32 squares in f64 in column order,
+ * divides by n in f64 and rounds to f32; inv = 1 / sqrt(ss + eps) in f32; each value is (v * inv) * w + b, w = 1 and
+ * b = 0 where absent (both exact). w, b nullable. */
+int kfo_rms_norm(const float* x, const float* w, const float* b, int rows, int n, float eps, float* out) {
+    if (rows < 0 || n <= 0) return -1;
+    for (int r = 0; r < rows; r++) {
+        const float* xr = x + (size_t)r * n;
+        float* o = out + (size_t)r * n;
+        double s = 0.0;
+        for (int i = 0; i < n; i++) s += (double)(xr[i] * xr[i]);
+        const float ss = (float)(s / (double)n);
+        const float inv = 1.0f / sqrtf(ss + eps);
+        for (int i = 0; i < n; i++) o[i] = xr[i] * inv * (w ? w[i] : 1.0f) + (b ? b[i] : 0.0f);
+    }
+    return 0;
+}
+
+/* ops::gated with no limit (crates/kf-backend-cpu/src/ops.rs:44-57) and ops::activate (:35-43) for the activations
+ * whose reference formula is exact IEEE arithmetic plus exp: act 0 silu, 2 relu, 4 relu squared (the codes of the
+ * reference GPU's kf_act, crates/kf-backend-cuda/src/kernels/common.cuh:93-99). gate and up rows are `stride` floats
+ * apart (stride = 2 n: gate and up side by side in one row). Returns -1 for other activations. */
+int kfo_gated(int act, const float* gate, const float* up, int rows, int n, int stride, float* out) {
+    if (act != 0 && act != 2 && act != 4) return -1;
+    for (int r = 0; r < rows; r++)
+        for (int i = 0; i < n; i++) {
+            const float g = gate[(size_t)r * stride + i], u = up[(size_t)r * stride + i];
+            float a;
+            if (act == 0) a = kfo_silu(g);
+            else if (act == 2) a = fmaxf(g, 0.0f);
+            else a = fmaxf(g, 0.0f) * fmaxf(g, 0.0f);
+            out[(size_t)r * n + i] = a * u;
+        }
+    return 0;
+}
+
 /* expert_matvec: crates/kf-backend-cpu/src/moe.rs:7-24, rows of one expert against round_activations(x) */
 static void expert_matvec(uint32_t ty, const uint8_t* w, int e, int n_in, int n_out, const float* x, float* y, float* xq, int nt) {
     int block, size;

@@ -86,6 +86,12 @@ int kfo_moe_ffn_i8(uint32_t ty, const uint8_t* gate, const uint8_t* up, const ui
 /* ops::silu */
 float kfo_silu(float x);
 
+/* rms_norm of rows x [rows][n] with nullable weight w [n] and bias b [n] */
+int kfo_rms_norm(const float* x, const float* w, const float* b, int rows, int n, float eps, float* out);
+
+/* gated activation act(gate) * up, act 0 silu / 2 relu / 4 relu squared; gate/up rows `stride` floats apart */
+int kfo_gated(int act, const float* gate, const float* up, int rows, int n, int stride, float* out);
+
 #ifdef __cplusplus
 }
 #endif
