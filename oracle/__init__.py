@@ -19,11 +19,13 @@ LIB_PATH = os.path.join(HERE, "build", "libkf_oracle.so")
 
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
+TYPE_Q6_K = 14
 TYPE_Q8_K = 15
 ACT_Q8_0 = 3
 ACT_Q8K = 4
 
-LAYOUT = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q8_K: (256, 292)}
+LAYOUT = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q5_K: (256, 176), TYPE_Q6_K: (256, 210), TYPE_Q8_K: (256, 292)}
 
 _lib = None
 
@@ -165,7 +167,7 @@ def block_ints(ty: int, w_row: np.ndarray, q_row: np.ndarray, sum16_row: np.ndar
     q_row = _c(q_row, np.int8).ravel()
     sum16_row = _c(sum16_row, np.int32).ravel()
     n = q_row.size
-    cnt = n // 32 if ty == TYPE_Q8_0 else 2 * (n // 256)
+    cnt = {TYPE_Q8_0: n // 32, TYPE_Q6_K: n // 256}.get(ty, 2 * (n // 256))
     out = np.zeros(cnt, np.int32)
     rc = lib().kfo_block_ints(ty, _p(w_row), n, _p(q_row), _p(sum16_row), _p(out))
     assert rc == 0

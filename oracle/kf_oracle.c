@@ -73,12 +73,15 @@ static float f16_at(const uint8_t* p) { return kfo_f16_to_f32((uint16_t)(p[0] | 
 
 /* ---------------------------------------------------------------- layouts
  * q8_0 (8, 32, 34): crates/kf-quant/src/types/q8_0.rs:4; q4_K (12, 256, 144): types/q4_k.rs:4;
+ * q5_K (13, 256, 176): types/q5_k.rs:4; q6_K (14, 256, 210): types/q6_k.rs:4;
  * q8_K (15, 256, 292): types/q8_k.rs:4; row_bytes: crates/kf-quant/src/lib.rs:17-20 */
 
 int kfo_type_info(uint32_t ty, int* block, int* size) {
     switch (ty) {
         case KFO_TYPE_Q8_0: *block = 32; *size = 34; return 0;
         case KFO_TYPE_Q4_K: *block = 256; *size = 144; return 0;
+        case KFO_TYPE_Q5_K: *block = 256; *size = 176; return 0;
+        case KFO_TYPE_Q6_K: *block = 256; *size = 210; return 0;
         case KFO_TYPE_Q8_K: *block = 256; *size = 292; return 0;
         default: return -1;
     }
@@ -89,6 +92,8 @@ int kfo_act_kind(uint32_t ty) {
     switch (ty) {
         case KFO_TYPE_Q8_0: return KFO_ACT_Q8_0;
         case KFO_TYPE_Q4_K:
+        case KFO_TYPE_Q5_K:
+        case KFO_TYPE_Q6_K:
         case KFO_TYPE_Q8_K: return KFO_ACT_Q8K;
         default: return -1;
     }
@@ -146,6 +151,16 @@ void kfo_q8_0_quantize_row(const float* x, int n, uint8_t* dst) {
     }
 }
 
+/* quads: crates/kf-quant/src/types/q6_k.rs:7-15, the signed 6-bit quant k (0..3) at offset l of a 128-element half */
+static int q6_quad(const uint8_t* ql, const uint8_t* qh, int l, int k) {
+    switch (k) {
+        case 0: return ((ql[l] & 0xF) | ((qh[l] & 3) << 4)) - 32;
+        case 1: return ((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+        case 2: return ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+        default: return ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+    }
+}
+
 /* ---------------------------------------------------------------- dequant_row
  * q8_0: crates/kf-quant/src/types/q8_0.rs:49-57; q4_K: types/q4_k.rs:64-85; q8_K: types/q8_k.rs:11-19 */
 int kfo_dequant_row(uint32_t ty, const uint8_t* src, int n, float* dst) {
@@ -173,6 +188,49 @@ int kfo_dequant_row(uint32_t ty, const uint8_t* src, int n, float* dst) {
                 for (int l = 0; l < 32; l++) {
                     out[64 * j + l] = d1 * (float)(q[l] & 0xF) - m1;
                     out[64 * j + 32 + l] = d2 * (float)(q[l] >> 4) - m2;
+                }
+            }
+        }
+        return 0;
+    }
+    if (ty == KFO_TYPE_Q5_K) {  /* types/q5_k.rs:67-93 */
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t* blk = src + 176 * b;
+            float d = f16_at(blk), mn = f16_at(blk + 2);
+            const uint8_t* scales = blk + 4;
+            const uint8_t* qh = blk + 16;
+            float* out = dst + 256 * b;
+            for (int j = 0; j < 4; j++) {
+                const uint8_t* ql = blk + 48 + 32 * j;
+                uint8_t sc, m;
+                scale_min_k4(2 * j, scales, &sc, &m);
+                float d1 = d * (float)sc, m1 = mn * (float)m;
+                scale_min_k4(2 * j + 1, scales, &sc, &m);
+                float d2 = d * (float)sc, m2 = mn * (float)m;
+                for (int l = 0; l < 32; l++) {
+                    int h1 = (qh[l] >> (2 * j)) & 1 ? 16 : 0, h2 = (qh[l] >> (2 * j + 1)) & 1 ? 16 : 0;
+                    out[64 * j + l] = d1 * (float)((ql[l] & 0xF) + h1) - m1;
+                    out[64 * j + 32 + l] = d2 * (float)((ql[l] >> 4) + h2) - m2;
+                }
+            }
+        }
+        return 0;
+    }
+    if (ty == KFO_TYPE_Q6_K) {  /* types/q6_k.rs:74-90 */
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t* blk = src + 210 * b;
+            float d = f16_at(blk + 208);
+            for (int h = 0; h < 2; h++) {
+                const uint8_t* ql = blk + 64 * h;
+                const uint8_t* qh = blk + 128 + 32 * h;
+                const uint8_t* sc = blk + 192 + 8 * h;
+                float* ys = dst + 256 * b + 128 * h;
+                for (int l = 0; l < 32; l++) {
+                    int is = l / 16;
+                    for (int k = 0; k < 4; k++) {
+                        int q = q6_quad(ql, qh, l, k);
+                        ys[l + 32 * k] = d * (float)(int8_t)sc[is + 2 * k] * (float)q;
+                    }
                 }
             }
         }
@@ -225,6 +283,48 @@ float kfo_dot_row(uint32_t ty, const uint8_t* src, const float* x, int n) {
                 acc += d * (float)sc1 * qx1 - mn * (float)m1 * sx1;
                 acc += d * (float)sc2 * qx2 - mn * (float)m2 * sx2;
             }
+        }
+    } else if (ty == KFO_TYPE_Q5_K) {  /* types/q5_k.rs:94-121 */
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t* blk = src + 176 * b;
+            float d = f16_at(blk), mn = f16_at(blk + 2);
+            const uint8_t* scales = blk + 4;
+            const uint8_t* qh = blk + 16;
+            const float* xs = x + 256 * b;
+            for (int j = 0; j < 4; j++) {
+                const uint8_t* ql = blk + 48 + 32 * j;
+                uint8_t sc1, m1, sc2, m2;
+                scale_min_k4(2 * j, scales, &sc1, &m1);
+                scale_min_k4(2 * j + 1, scales, &sc2, &m2);
+                const float* x1 = xs + 64 * j;
+                const float* x2 = x1 + 32;
+                float qx1 = 0.0f, sx1 = 0.0f, qx2 = 0.0f, sx2 = 0.0f;
+                for (int l = 0; l < 32; l++) {
+                    int h1 = ((qh[l] >> (2 * j)) & 1) << 4, h2 = ((qh[l] >> (2 * j + 1)) & 1) << 4;
+                    qx1 += (float)((ql[l] & 0xF) | h1) * x1[l];
+                    sx1 += x1[l];
+                    qx2 += (float)((ql[l] >> 4) | h2) * x2[l];
+                    sx2 += x2[l];
+                }
+                acc += d * (float)sc1 * qx1 - mn * (float)m1 * sx1;
+                acc += d * (float)sc2 * qx2 - mn * (float)m2 * sx2;
+            }
+        }
+    } else if (ty == KFO_TYPE_Q6_K) {  /* types/q6_k.rs:91-110 */
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t* blk = src + 210 * b;
+            float d = f16_at(blk + 208);
+            float sums[16] = {0};
+            for (int h = 0; h < 2; h++) {
+                const uint8_t* ql = blk + 64 * h;
+                const uint8_t* qh = blk + 128 + 32 * h;
+                const float* xn = x + 256 * b + 128 * h;
+                for (int l = 0; l < 32; l++) {
+                    int is = 8 * h + l / 16;
+                    for (int k = 0; k < 4; k++) sums[is + 2 * k] += (float)q6_quad(ql, qh, l, k) * xn[l + 32 * k];
+                }
+            }
+            for (int s = 0; s < 16; s++) acc += d * (float)(int8_t)blk[192 + s] * sums[s];
         }
     } else if (ty == KFO_TYPE_Q8_K) {
         for (int b = 0; b < n / 256; b++) {
@@ -400,6 +500,85 @@ static void dot_i8_q4_k_row(const uint8_t* src, int n, const int8_t* q, const fl
     *y = hsum8(acc);
 }
 
+/* q5_K AVX2: crates/kf-quant/src/types/q5_k.rs:7-60. The fifth bit of a nibble comes from bit 2j (low nibbles) or
+ * 2j + 1 (high nibbles) of qh[l]; otherwise q4_K's lanes. */
+static void dot_i8_q5_k_row(const uint8_t* src, int n, const int8_t* q, const float* d16, const int32_t* sum16, float* y) {
+    float acc[8] = {0};
+    for (int b = 0; b < n / 256; b++) {
+        const uint8_t* blk = src + 176 * b;
+        float d = f16_at(blk), dmin = f16_at(blk + 2);
+        int32_t sc[8], mn[16];
+        for (int s = 0; s < 8; s++) {
+            uint8_t a, m;
+            scale_min_k4(s, blk + 4, &a, &m);
+            sc[s] = a;
+            mn[2 * s] = m;
+            mn[2 * s + 1] = m;
+        }
+        const uint8_t* qh = blk + 16;
+        int32_t sumi[8] = {0};
+        for (int j = 0; j < 4; j++) {
+            const uint8_t* qs = blk + 48 + 32 * j;
+            const int8_t* q0 = q + b * 256 + 64 * j;
+            const int8_t* q1 = q0 + 32;
+            for (int i = 0; i < 8; i++) {
+                int32_t p0 = 0, p1 = 0;
+                for (int t = 0; t < 4; t++) {
+                    const int e = 4 * i + t;
+                    p0 += (int32_t)((qs[e] & 0xF) | (((qh[e] >> (2 * j)) & 1) << 4)) * q0[e];
+                    p1 += (int32_t)((qs[e] >> 4) | (((qh[e] >> (2 * j + 1)) & 1) << 4)) * q1[e];
+                }
+                sumi[i] += sc[2 * j] * p0 + sc[2 * j + 1] * p1;
+            }
+        }
+        int at = b * 16;
+        float dx = d16[at];
+        float sd = d * dx, sm = dmin * dx;
+        for (int i = 0; i < 8; i++) {
+            int32_t mins = sum16[at + i] * mn[i] + sum16[at + 8 + i] * mn[8 + i];
+            acc[i] = fmaf(sd, (float)sumi[i], acc[i]);
+            acc[i] = fmaf(-sm, (float)mins, acc[i]);
+        }
+    }
+    *y = hsum8(acc);
+}
+
+/* q6_K AVX2: crates/kf-quant/src/types/q6_k.rs:17-59. The unsigned 6-bit values (0..63) against the int8
+ * activations, lane i holding bytes 4i..4i+3 of each quad's 32-element run, lanes 0-3 scaled by sc[g] and 4-7 by
+ * sc[g + 1] (g = 8h + 2k), minus the bias 32 sc * sum16 of groups i and 8 + i. */
+static void dot_i8_q6_k_row(const uint8_t* src, int n, const int8_t* q, const float* d16, const int32_t* sum16, float* y) {
+    float acc[8] = {0};
+    for (int b = 0; b < n / 256; b++) {
+        const uint8_t* blk = src + 210 * b;
+        float d = f16_at(blk + 208);
+        const int8_t* sc = (const int8_t*)(blk + 192);
+        int32_t sumi[8] = {0};
+        for (int h = 0; h < 2; h++) {
+            const uint8_t* ql = blk + 64 * h;
+            const uint8_t* qh = blk + 128 + 32 * h;
+            for (int k = 0; k < 4; k++) {
+                const int g = 8 * h + 2 * k;
+                const int8_t* q8 = q + b * 256 + 16 * g;
+                for (int i = 0; i < 8; i++) {
+                    int32_t p = 0;
+                    for (int t = 0; t < 4; t++) {
+                        const int l = 4 * i + t;
+                        p += (q6_quad(ql, qh, l, k) + 32) * q8[l];
+                    }
+                    sumi[i] += (i < 4 ? sc[g] : sc[g + 1]) * p;
+                }
+            }
+        }
+        int at = b * 16;
+        float s = d * d16[at];
+        for (int i = 0; i < 8; i++) {
+            int32_t bias = sum16[at + i] * (sc[i] * 32) + sum16[at + 8 + i] * (sc[8 + i] * 32);
+            acc[i] = fmaf(s, (float)(sumi[i] - bias), acc[i]);
+        }
+    }
+    *y = hsum8(acc);
+}
+
 int kfo_dot_i8(uint32_t ty, const uint8_t* src, int n, const int8_t* q, const float* d16, const int32_t* sum16, int rows, float* y) {
     int n16 = n / 16;
     for (int r = 0; r < rows; r++) {
@@ -408,6 +587,8 @@ int kfo_dot_i8(uint32_t ty, const uint8_t* src, int n, const int8_t* q, const fl
         const int32_t* sr = sum16 + (size_t)r * n16;
         if (ty == KFO_TYPE_Q8_0) dot_i8_q8_0_row(src, n, qr, dr, &y[r]);
         else if (ty == KFO_TYPE_Q4_K) dot_i8_q4_k_row(src, n, qr, dr, sr, &y[r]);
+        else if (ty == KFO_TYPE_Q5_K) dot_i8_q5_k_row(src, n, qr, dr, sr, &y[r]);
+        else if (ty == KFO_TYPE_Q6_K) dot_i8_q6_k_row(src, n, qr, dr, sr, &y[r]);
         else return -1;
     }
     return 0;
@@ -440,6 +621,46 @@ int kfo_block_ints(uint32_t ty, const uint8_t* src, int n, const int8_t* q, cons
             }
             ints[2 * b] = sumi;
             ints[2 * b + 1] = mins;
+        }
+        return 0;
+    }
+    if (ty == KFO_TYPE_Q5_K) {  /* two per super-block, as q4_K: sum_s sc_s dot_s and sum_s m_s bsum_s */
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t* blk = src + 176 * b;
+            const uint8_t* qh = blk + 16;
+            int32_t sumi = 0, mins = 0;
+            for (int s = 0; s < 8; s++) {
+                uint8_t sc, m;
+                scale_min_k4(s, blk + 4, &sc, &m);
+                const uint8_t* qs = blk + 48 + 32 * (s / 2);
+                int32_t dot = 0;
+                for (int l = 0; l < 32; l++) {
+                    int w = ((s & 1) ? (qs[l] >> 4) : (qs[l] & 0xF)) | (((qh[l] >> s) & 1) << 4);
+                    dot += w * q[256 * b + 32 * s + l];
+                }
+                sumi += sc * dot;
+                mins += m * (sum16[16 * b + 2 * s] + sum16[16 * b + 2 * s + 1]);
+            }
+            ints[2 * b] = sumi;
+            ints[2 * b + 1] = mins;
+        }
+        return 0;
+    }
+    if (ty == KFO_TYPE_Q6_K) {  /* one per super-block: sum_g sc_g (dot_g of the unsigned values - 32 bsum_g) */
+        for (int b = 0; b < n / 256; b++) {
+            const uint8_t* blk = src + 210 * b;
+            const int8_t* sc = (const int8_t*)(blk + 192);
+            int32_t tot = 0;
+            for (int h = 0; h < 2; h++)
+                for (int k = 0; k < 4; k++)
+                    for (int half = 0; half < 2; half++) {
+                        const int g = 8 * h + 2 * k + half;
+                        int32_t dot = 0;
+                        for (int l = 16 * half; l < 16 * half + 16; l++)
+                            dot += (q6_quad(blk + 64 * h, blk + 128 + 32 * h, l, k) + 32) * q[256 * b + 128 * h + 32 * k + l];
+                        tot += sc[g] * (dot - 32 * sum16[16 * b + g]);
+                    }
+            ints[b] = tot;
         }
         return 0;
     }

@@ -22,6 +22,8 @@ extern "C" {
 
 #define KFO_TYPE_Q8_0 8u
 #define KFO_TYPE_Q4_K 12u
+#define KFO_TYPE_Q5_K 13u
+#define KFO_TYPE_Q6_K 14u
 #define KFO_TYPE_Q8_K 15u
 
 #define KFO_ACT_Q8_0 3
@@ -31,7 +33,7 @@ extern "C" {
 float kfo_f16_to_f32(uint16_t h);
 uint16_t kfo_f32_to_f16(float f);
 
-/* TypeInfo of q8_0 / q4_K / q8_K: returns 0 and fills block and byte size, -1 for another id */
+/* TypeInfo of q8_0 / q4_K / q5_K / q6_K / q8_K: returns 0 and fills block and byte size, -1 for another id */
 int kfo_type_info(uint32_t ty, int* block, int* size);
 
 /* Activation kind paired with a weight type (act_kind), -1 when the type is not restated here */
@@ -40,7 +42,7 @@ int kfo_act_kind(uint32_t ty);
 /* q8_0::quantize_row */
 void kfo_q8_0_quantize_row(const float* x, int n, uint8_t* dst);
 
-/* Quant::dequant_row of q8_0, q4_K, q8_K; returns -1 for another type */
+/* Quant::dequant_row of q8_0, q4_K, q5_K, q6_K, q8_K; returns -1 for another type */
 int kfo_dequant_row(uint32_t ty, const uint8_t* src, int n, float* dst);
 
 /* Quant::dot_row (float path) */

@@ -43,20 +43,23 @@ def test_layouts_match_ggml_structs():
     # parity.rs:9-31 (q4_K, q8_K) and q8_0.rs:4
     import ctypes
 
-    for ty, want in [(8, (32, 34)), (12, (256, 144)), (15, (256, 292))]:
+    for ty, want in [(8, (32, 34)), (12, (256, 144)), (13, (256, 176)), (14, (256, 210)), (15, (256, 292))]:
         b, s = ctypes.c_int(), ctypes.c_int()
         assert oracle.lib().kfo_type_info(ty, ctypes.byref(b), ctypes.byref(s)) == 0
         assert (b.value, s.value) == want
     assert oracle.lib().kfo_type_info(2, ctypes.byref(b), ctypes.byref(s)) == -1
 
 
-@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_K", 12), ("q8_K", 15)])
+ALL_FIXTURES = [("q8_0", 8), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14), ("q8_K", 15)]
+
+
+@pytest.mark.parametrize("name,ty", ALL_FIXTURES)
 def test_fixture_rows_match_type_size(name, ty):
     n, rows, blocks, _ = oracle.load_fixture(os.path.join(GOLDEN, f"{name}.bin"))
     assert blocks.size == rows * oracle.row_bytes(ty, n)
 
 
-@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_K", 12), ("q8_K", 15)])
+@pytest.mark.parametrize("name,ty", ALL_FIXTURES)
 def test_dequant_is_bit_exact_with_ggml(name, ty):
     n, rows, blocks, want = oracle.load_fixture(os.path.join(GOLDEN, f"{name}.bin"))
     got = oracle.dequant(ty, blocks, n)
@@ -100,7 +103,8 @@ def test_f32_to_f16_round_trip_and_ties():
 
 # ------------------------------------------------------------------ the reference's invariants
 
-DOT_TYPES = [(12, [("f16", 0), ("f16", 2)]), (15, [("f32", 0)])]  # parity.rs:36-43, restricted to the restated types
+DOT_TYPES = [(12, [("f16", 0), ("f16", 2)]), (13, [("f16", 0), ("f16", 2)]), (14, [("f16", 208)]),
+             (15, [("f32", 0)])]  # parity.rs:36-43, restricted to the restated types
 
 
 def _patched_row(rng, ty, n, scales):
@@ -119,7 +123,7 @@ def _patched_row(rng, ty, n, scales):
 
 
 def test_dot_row_matches_dequant_then_dot():
-    """parity.rs:132-167, same seed and scale patching, for q4_K and q8_K; plus q8_0 with its f16 scale patched."""
+    """parity.rs:132-167, same seed and scale patching, for the K types; plus q8_0 with its f16 scale patched."""
     rng = SplitMix(0x6B66646F74726F77)
     for ty, scales in DOT_TYPES + [(8, [("f16", 0)])]:
         block, _ = oracle.LAYOUT[ty]
@@ -133,7 +137,7 @@ def test_dot_row_matches_dequant_then_dot():
             assert abs(got - want) / abs(want) <= 1e-3
 
 
-@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_K", 12)])
+@pytest.mark.parametrize("name,ty", [("q8_0", 8), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14)])
 def test_dot_i8_matches_dequant_then_dot(name, ty):
     """parity.rs:169-203 on the golden rows: err <= 1e-4 * sum|p| + 1e-6 against float64."""
     rng = SplitMix(0x6465717561_6E7474)
@@ -142,13 +146,18 @@ def test_dot_i8_matches_dequant_then_dot(name, ty):
     rows = 3
     x = np.array([2.0 * rng.unit() - 1.0 for _ in range(rows * n)], np.float32).reshape(rows, n)
     q, d16, s16 = oracle.quantize_activations(kind, x)
+    checked = 0
     for r in range(min(rows_w, 4)):
         deq = oracle.dequant(ty, blocks[r], n)[0].astype(np.float64)
+        if not np.isfinite(deq).all():
+            continue  # the fixtures' random scale bytes decode to inf/nan in some rows (bit-exact above all the same)
+        checked += 1
         y = oracle.dot_i8(ty, blocks[r], q, d16, s16)
         for a in range(rows):
             xa = np.repeat(d16[a], 16).astype(np.float64) * q[a].astype(np.float64)
             p = deq * xa
             assert abs(float(y[a]) - p.sum()) <= 1e-4 * np.abs(p).sum() + 1e-6
+    assert checked >= 1
 
 
 # ------------------------------------------------------------------ integer block dots: brute force and special cases
@@ -405,3 +414,73 @@ def test_moe_ffn_i8_is_the_int8_composition_and_near_the_float_path():
     live = np.abs(flt[:3]).mean()
     assert np.abs(out - flt).max() <= 2e-2 * live
     assert not out[3].any()
+
+
+def _q5k_decode(row, n):
+    """q5_K bytes -> (d, dmin, sc, m, q[n] in 0..31): q4_K's header and nibbles, the fifth bit of element l of
+    sub-block s from bit s of qh[l] (the block definition, crates/kf-quant/src/types/q5_k.rs:67-93)."""
+    nsb = n // 256
+    blk = row.reshape(nsb, 176)
+    as_q4k = np.concatenate([blk[:, :16], blk[:, 48:]], axis=1)
+    d, dmin, sc, m, q4 = _q4k_decode(as_q4k.ravel(), n)
+    qh = blk[:, 16:48].astype(np.int64)                     # [nsb][32]
+    hb = np.stack([(qh >> s) & 1 for s in range(8)], axis=1)  # [nsb][8][32]
+    return d, dmin, sc, m, q4 + 16 * hb.reshape(nsb, 256)
+
+
+def _q6k_decode(row, n):
+    """q6_K bytes -> (d, sc[nsb][16] int8, q[n] in -32..31) by the element map of quads (q6_k.rs:7-15)."""
+    nsb = n // 256
+    blk = row.reshape(nsb, 210)
+    d = blk[:, 208:210].copy().view(np.float16)[:, 0].astype(np.float32)
+    sc = blk[:, 192:208].view(np.int8).astype(np.int64)
+    q = np.zeros((nsb, 256), np.int64)
+    for h in range(2):
+        ql = blk[:, 64 * h : 64 * h + 64].astype(np.int64)
+        qh = blk[:, 128 + 32 * h : 160 + 32 * h].astype(np.int64)
+        l = np.arange(32)
+        q[:, 128 * h + l] = (ql[:, l] & 0xF) | ((qh[:, l] & 3) << 4)
+        q[:, 128 * h + 32 + l] = (ql[:, l + 32] & 0xF) | (((qh[:, l] >> 2) & 3) << 4)
+        q[:, 128 * h + 64 + l] = (ql[:, l] >> 4) | (((qh[:, l] >> 4) & 3) << 4)
+        q[:, 128 * h + 96 + l] = (ql[:, l + 32] >> 4) | (((qh[:, l] >> 6) & 3) << 4)
+    return d, sc, q - 32
+
+
+@pytest.mark.parametrize("name,ty", [("q5_K", 13), ("q6_K", 14)])
+def test_numpy_decoders_reproduce_ggml_dequant(name, ty):
+    """The brute-force decoders below are themselves pinned to ggml's fixtures (element map and scales)."""
+    n, rows, blocks, want = oracle.load_fixture(os.path.join(GOLDEN, f"{name}.bin"))
+    for r in range(rows):
+        if ty == 13:
+            d, dmin, sc, m, q = _q5k_decode(blocks[r], n)
+            deq = (d[:, None, None] * sc[:, :, None]) * q.reshape(-1, 8, 32) - (dmin[:, None, None] * m[:, :, None])
+        else:
+            d, sc, q = _q6k_decode(blocks[r], n)
+            deq = (d[:, None, None] * sc[:, :, None]) * q.reshape(-1, 16, 16)
+        assert np.allclose(deq.reshape(-1), want[r], rtol=1e-6, atol=1e-6, equal_nan=True)
+
+
+def test_block_ints_q5_k_and_q6_k_brute_force():
+    rng = np.random.default_rng(4)
+    n = 1024
+    x = rng.standard_normal((2, n)).astype(np.float32)
+    q, d16, s16 = oracle.quantize_activations(4, x)
+    for ty in (13, 14):
+        w = rng.integers(0, 256, (3, oracle.row_bytes(ty, n)), dtype=np.uint8)
+        for r in range(3):
+            for a in range(2):
+                got = oracle.block_ints(ty, w[r], q[a], s16[a])
+                qa = q[a].astype(np.int64)
+                if ty == 13:
+                    _, _, sc, m, wq = _q5k_decode(w[r], n)
+                    dots = (wq.reshape(-1, 8, 32) * qa.reshape(-1, 8, 32)).sum(axis=2)
+                    bsum = s16[a].reshape(-1, 8, 2).sum(axis=2).astype(np.int64)
+                    want = np.stack([(sc * dots).sum(axis=1), (m * bsum).sum(axis=1)], axis=1).ravel()
+                else:
+                    _, sc, wq = _q6k_decode(w[r], n)
+                    # the signed values' group dots, which the integer form reaches as (q + 32) . x - 32 sum16
+                    dots = (wq.reshape(-1, 16, 16) * qa.reshape(-1, 16, 16)).sum(axis=2)
+                    assert np.array_equal(dots, ((wq + 32).reshape(-1, 16, 16) * qa.reshape(-1, 16, 16)).sum(axis=2)
+                                          - 32 * s16[a].reshape(-1, 16).astype(np.int64))
+                    want = (sc * dots).sum(axis=1)
+                assert np.array_equal(got, want), (ty, r, a)
