@@ -234,6 +234,33 @@ def fused_section(dev):
     return out
 
 
+def kquant_section(dev):
+    """q6_K and q5_K weights (SURVEY's second "next" row) at the Llama-3-8B shapes, batch 1 (the GEMV) and batch 8 (eight
+    activation rows against one weight pass): us per call and GB/s over weight bytes + f32 activations in and out,
+    weight copies rotated past the MALL."""
+    import kungfu_amd as kf
+
+    out = {}
+    for ty, tname in ((kf.TYPE_Q6_K, "q6_K"), (kf.TYPE_Q5_K, "q5_K")):
+        for name, n, n_out in (("o", 4096, 4096), ("gate", 4096, 14336), ("down", 14336, 4096)):
+            wb = kf.row_bytes(ty, n) * n_out
+            sh = Shape(name, ty, n, n_out, max(2, -(-2 * MALL_BYTES // wb) + 1), dev)
+            us = time_launches(sh.gemv, 100)
+            rec = {"us": round(us, 3), "GBs": round(sh.bytes / us / 1e3, 1)}
+            import torch
+
+            x8 = torch.from_numpy(kf.synth_normal(5, 1.0, 8 * n).reshape(8, n)).to(dev)
+            act8 = kf.alloc_act(8, n, dev)
+            y8 = torch.empty((8, n_out), device=dev)
+            kf.quant_act(x8, act8, kf.ACT_Q8K)
+            us8 = time_launches(lambda i: kf.gemv(ty, sh.w[i % len(sh.w)], act8, y8, 8, n, n_out), 50)
+            rec["us_8_rows"] = round(us8, 3)
+            rec["GBs_8_rows"] = round(gemv_bytes(ty, n, n_out, 8) / us8 / 1e3, 1)
+            out[f"{tname}_{name}"] = rec
+            del sh
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_up_traffic.md")
 
 
@@ -295,7 +322,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "fused", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "fused", "kquant", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -309,7 +336,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "fused": fused_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "fused": fused_section, "kquant": kquant_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -386,6 +413,7 @@ def main():
     out["small_batch_q8_0"] = small_batch_section(dev)
     out["moe_q4_k"] = moe_section(dev)
     out["fused_producers"] = fused_section(dev)
+    out["k_quants"] = kquant_section(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
     print(json.dumps(out), flush=True)

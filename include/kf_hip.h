@@ -28,9 +28,11 @@ extern "C" {
 
 #define KF_HIP_ABI_VERSION 1
 
-/* ggml type ids (crates/kf-quant/src/types/q8_0.rs:4, types/q4_k.rs:4) */
+/* ggml type ids (crates/kf-quant/src/types/q8_0.rs:4, q4_k.rs:4, q5_k.rs:4, q6_k.rs:4) */
 #define KF_TYPE_Q8_0 8u
 #define KF_TYPE_Q4_K 12u
+#define KF_TYPE_Q5_K 13u
+#define KF_TYPE_Q6_K 14u
 
 /* activation rounding kinds, the reference's round codes (crates/kf-backend-cuda/src/exec.rs:103-113) */
 #define KF_ACT_Q8_0 3
@@ -103,7 +105,10 @@ int kf_hip_gated_act_q8(const float* gate, const float* up, int rows, int n, int
 /* Decode and small-batch product of `rows` activation rows: one row is the streaming GEMV, several rows the
  * multi-row product that reads each weight row once per eight activation rows. Replaces matvec_i8_launch
  * (exec.rs:1996-2039) with the kernels matvec_i8 / matvec_i8_1 / matvec_i8_1s / mm_i8_{8,16,32} /
- * mm_frag_{8,16,24,32} (crates/kf-backend-cuda/src/kernels/quant.cuh:604-627, mm_frag.cuh:294-300). */
+ * mm_frag_{8,16,24,32} (crates/kf-backend-cuda/src/kernels/quant.cuh:604-627, mm_frag.cuh:294-300).
+ * q5_K and q6_K weights (Q8K-kind activations, any row count: one launch per eight activation rows) run their own
+ * product, the reference's q5_K / q6_K loaders (kernels/quant_q5_K.cu, quant_q6_K.cu); q6_K rows need only 2-byte
+ * alignment past the first. */
 int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                 int rows, int n, int n_out, void* stream);
 
@@ -160,9 +165,10 @@ int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* do
                    const int32_t* sel, const float* wts, int n_used, float scale, void* scratch, size_t scratch_bytes, float* out, void* stream);
 
 /* Per-block int32 results of n_out weight rows against the `rows` activation rows of `act`: q8_0 one int32 per 32-block
- * (out [n_out][rows][n/32]); q4_K (sumi, mins) per super-block (out [n_out][rows][n/256][2]). The integers of
- * dot_i8 (crates/kf-quant/src/types/q8_0.rs:10-29, types/q4_k.rs:10-58), computed by the same lane code as the
- * product kernels. No reference counterpart: it exists so the integer results can be checked bit-exact. */
+ * (out [n_out][rows][n/32]); q4_K and q5_K (sumi, mins) per super-block (out [n_out][rows][n/256][2]); q6_K one
+ * int32 per super-block, dot minus the 32-offset bias (out [n_out][rows][n/256]). The integers of dot_i8
+ * (crates/kf-quant/src/types/q8_0.rs:10-29, q4_k.rs:10-58, q5_k.rs:7-60, q6_k.rs:17-59), computed by the same lane
+ * code as the product kernels. No reference counterpart: it exists so the integer results can be checked bit-exact. */
 int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out, int32_t* out,
                       void* stream);
 
@@ -193,10 +199,14 @@ int kf_hip_backend_matmul_slice(kf_hip_backend* b, int wid, int index, const flo
  * kf_quantize_q4_k: a q4_K encoder of this library's own. The reference has none (it only reads q4_K); this one fits
  *   per sub-block an affine min/max, then 6-bit scales and mins against f16 super-block d/dmin, rounding to nearest
  *   even. Any valid encoder suffices: parity is defined on the bytes.
+ * kf_quantize_q5_k / kf_quantize_q6_k: encoders of this library's own for the same reason (q5_K: q4_K's form with 31
+ *   steps and the fifth bit in qh; q6_K: per 16 values a signed scale amax / 32 as int8 against an f16 d).
  * kf_synth_normal: SplitMix64 (the generator of crates/kf-quant/tests/parity.rs:75-88) feeding Box-Muller pairs,
  *   sigma * N(0,1) as f32: the synthetic data of the benchmark configs. */
 int kf_quantize_q8_0(const float* x, int64_t rows, int n, uint8_t* dst);
 int kf_quantize_q4_k(const float* x, int64_t rows, int n, uint8_t* dst);
+int kf_quantize_q5_k(const float* x, int64_t rows, int n, uint8_t* dst);
+int kf_quantize_q6_k(const float* x, int64_t rows, int n, uint8_t* dst);
 void kf_synth_normal(uint64_t seed, float sigma, float* out, size_t n);
 
 #ifdef __cplusplus

@@ -19,9 +19,11 @@ HEADER = os.path.join(ROOT, "include", "kf_hip.h")
 
 TYPE_Q8_0 = 8
 TYPE_Q4_K = 12
+TYPE_Q5_K = 13
+TYPE_Q6_K = 14
 ACT_Q8_0 = 3
 ACT_Q8K = 4
-BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144)}
+BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144), TYPE_Q5_K: (256, 176), TYPE_Q6_K: (256, 210)}
 
 KF_OK = 0
 KF_E_INVALID = -1
@@ -84,6 +86,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_backend_matmul_slice": ([P, I, I, P, I, I, P], I),
         "kf_quantize_q8_0": ([P, L64, I, P], I),
         "kf_quantize_q4_k": ([P, L64, I, P], I),
+        "kf_quantize_q5_k": ([P, L64, I, P], I),
+        "kf_quantize_q6_k": ([P, L64, I, P], I),
         "kf_synth_normal": ([ctypes.c_uint64, ctypes.c_float, P, S], None),
     }
     for name, (args, res) in sig.items():
@@ -144,12 +148,13 @@ def synth_normal(seed: int, sigma: float, n: int):
 
 
 def quantize(ty: int, x):
-    """Host encoder: q8_0 (quantize_row of the reference) or q4_K (this library's encoder); x [rows][n] f32."""
+    """Host encoder: q8_0 (quantize_row of the reference) or q4_K / q5_K / q6_K (this library's encoders); x [rows][n] f32."""
     np = _np()
     x = np.ascontiguousarray(np.atleast_2d(x), np.float32)
     rows, n = x.shape
     out = np.empty((rows, row_bytes(ty, n)), np.uint8)
-    fn = lib().kf_quantize_q8_0 if ty == TYPE_Q8_0 else lib().kf_quantize_q4_k
+    fn = {TYPE_Q8_0: lib().kf_quantize_q8_0, TYPE_Q4_K: lib().kf_quantize_q4_k, TYPE_Q5_K: lib().kf_quantize_q5_k,
+          TYPE_Q6_K: lib().kf_quantize_q6_k}[ty]
     rc = fn(x.ctypes.data_as(ctypes.c_void_p), rows, n, out.ctypes.data_as(ctypes.c_void_p))
     if rc != 0:
         raise KfError(rc, f"quantize type {ty} of {rows}x{n}")

@@ -16,6 +16,8 @@
 
 // Launchers in the .hip translation units
 hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s);
+hipError_t kf_launch_gemv_k(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
+                            int rows, int n, int n_out, hipStream_t s);
 hipError_t kf_launch_rms_norm_q8(const float* x, const float* w, const float* b, float eps, void* act, int rows, int n, int kind,
                                  hipStream_t s);
 hipError_t kf_launch_gated_act_q8(const float* gate, const float* up, int stride, int act_fn, void* act, int rows, int n, int kind,
@@ -61,9 +63,9 @@ bool type_info(uint32_t ty, int& block, int& bytes) {
         bytes = KF_Q8_0_BYTES;
         return true;
     }
-    if (ty == KF_TYPE_Q4_K) {
+    if (ty == KF_TYPE_Q4_K || ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) {
         block = KF_Q4_K_BLOCK;
-        bytes = KF_Q4_K_BYTES;
+        bytes = ty == KF_TYPE_Q4_K ? KF_Q4_K_BYTES : ty == KF_TYPE_Q5_K ? KF_Q5_K_BYTES : KF_Q6_K_BYTES;
         return true;
     }
     return false;
@@ -83,7 +85,7 @@ int gemv_maxit() {
 
 int check_product(uint32_t ty, const void* w, int64_t row_bytes, const void* act, float* y, int rows, int n, int n_out) {
     int block, bytes;
-    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12)", ty);
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12, q5_K=13, q6_K=14)", ty);
     if (n <= 0 || n % block != 0) return fail(KF_E_INVALID, "%d columns against blocks of %d", n, block);
     if (rows < 1) return fail(KF_E_INVALID, "%d activation rows", rows);
     if (n_out < 0) return fail(KF_E_INVALID, "%d output rows", n_out);
@@ -168,10 +170,15 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
                 int n, int n_out, void* stream) {
     const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
     if (rc != KF_OK) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // q5_K / q6_K: their own product, all rows (eight activation rows a weight pass)
+    if (ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) {
+        const hipError_t e = kf_launch_gemv_k(ty, w, row_bytes, act, bias, res, y, rows, n, n_out, s);
+        return e == hipSuccess ? KF_OK : hip_fail(e, "q5_K/q6_K product launch");
+    }
     if (n > kf_gemv_max_n()) return fail(KF_E_UNSUPPORTED, "%d columns above the %d the GEMV stages in LDS", n, kf_gemv_max_n());
     const kf_act_offsets o = kf_act_layout((size_t)rows, (size_t)n);
     const char* base = static_cast<const char*>(act);
-    hipStream_t s = static_cast<hipStream_t>(stream);
     // several rows: each weight row streamed once against up to eight staged activation rows
     if (rows > 1 && n <= kf_rows_max_n(ty)) {
         const hipError_t e = kf_launch_rows(ty, w, nullptr, 0, row_bytes, act, rows, n, n_out, nullptr, nullptr, 1, rows, 1, 1, bias, res, y, s);
@@ -196,7 +203,7 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
         const hipError_t e = kf_launch_gemm_q4k(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
         return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
     }
-    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0 and q4_K weights (type %u given)", ty);
+    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0 and q4_K weights (type %u given; q5_K and q6_K go through kf_hip_gemv)", ty);
     if (n % kf_gemm_k_multiple() != 0) return fail(KF_E_INVALID, "%d columns, the GEMM needs a multiple of %d", n, kf_gemm_k_multiple());
     const hipError_t e = kf_launch_gemm_q8_0(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
@@ -205,7 +212,7 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream) {
     int block, bytes;
-    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12)", ty);
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12, q5_K=13, q6_K=14)", ty);
     if (n_in <= 0 || n_in % block != 0) return fail(KF_E_INVALID, "%d columns against blocks of %d", n_in, block);
     const int64_t rb = (int64_t)(n_in / block) * bytes;
     const int rc = check_product(ty, w, rb, act, y, rows, n_in, n_out);
@@ -238,6 +245,7 @@ int kf_hip_moe_gemv(uint32_t ty, const void* w, const void* w_up, int64_t expert
                     int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int n_used, int per_slot, float* y, void* stream) {
     const int rc = check_product(ty, w, row_bytes, act, y, act_rows, n, n_out);
     if (rc != KF_OK) return rc;
+    if (ty != KF_TYPE_Q8_0 && ty != KF_TYPE_Q4_K) return fail(KF_E_UNSUPPORTED, "grouped expert products run q8_0 and q4_K weights (type %u)", ty);
     if (w_up && !aligned(w_up, 16)) return fail(KF_E_INVALID, "up weight base must be 16-byte aligned");
     if (!order || !offsets || n_slots < 1 || n_used < 1) return fail(KF_E_INVALID, "null order/offsets or %d slots, %d used", n_slots, n_used);
     if (expert_bytes < (int64_t)n_out * row_bytes || expert_bytes % 16 != 0)
@@ -290,7 +298,8 @@ size_t kf_hip_moe_scratch_bytes(int rows, int n_used, int n_embd, int n_ff, int 
 int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* down, int n_slots, int n_embd, int n_ff, const float* x, int rows,
                    const int32_t* sel, const float* wts, int n_used, float scale, void* scratch, size_t scratch_bytes, float* out, void* stream) {
     int block, bytes;
-    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12)", ty);
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12, q5_K=13, q6_K=14)", ty);
+    if (ty != KF_TYPE_Q8_0 && ty != KF_TYPE_Q4_K) return fail(KF_E_UNSUPPORTED, "the MoE layer runs q8_0 and q4_K experts (type %u)", ty);
     if (rows < 1 || n_used < 1 || n_slots < 1) return fail(KF_E_INVALID, "%d rows, %d used of %d slots", rows, n_used, n_slots);
     if (n_embd <= 0 || n_ff <= 0 || n_embd % block != 0 || n_ff % block != 0) return fail(KF_E_INVALID, "%d / %d columns against blocks of %d", n_embd, n_ff, block);
     if (!gate || !up || !down || !x || !sel || !wts || !scratch || !out) return fail(KF_E_INVALID, "null MoE pointer");

@@ -613,9 +613,11 @@ struct Q8Unit {
 };
 
 // Per-block integers of weight rows against activation rows, one thread per (weight row, activation row, block):
-// q8_0 one int32 per 32-block, q4_K (sumi, mins) per super-block. The check that pins the GEMV's lane arithmetic.
+// q8_0 one int32 per 32-block, q4_K and q5_K (sumi, mins) per super-block, q6_K one int32 per super-block (dot minus
+// the 32-offset bias). The check that pins the products' lane arithmetic.
 __global__ void block_ints_kernel(uint32_t ty, const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
-                                  const int32_t* __restrict__ xs32, int n, int n_out, int rows, int32_t* __restrict__ out) {
+                                  const int32_t* __restrict__ xs16, const int32_t* __restrict__ xs32, int n, int n_out, int rows,
+                                  int32_t* __restrict__ out) {
     const int per = ty == KF_TYPE_Q8_0 ? n / 32 : n / 256;
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= (int64_t)n_out * rows * per) return;
@@ -624,6 +626,32 @@ __global__ void block_ints_kernel(uint32_t ty, const uint8_t* __restrict__ w, in
     const int o = (int)(t / ((int64_t)per * rows));
     const uint8_t* row = w + (int64_t)o * row_bytes;
     const int8_t* x = xq + (int64_t)r * n;
+    if (ty == KF_TYPE_Q6_K) {  // one int32 per super-block: the four lane units' sum
+        const uint8_t* blk = row + (int64_t)b * KF_Q6_K_BYTES;
+        int tot = 0;
+        for (int j = 0; j < 4; j++) {
+            KfQ6Lane u;
+            u.load(blk, j);
+            tot += u.dot(x + b * 256, xs16 + (int64_t)r * (n / 16) + b * 16, j);
+        }
+        out[t] = tot;
+        return;
+    }
+    if (ty == KF_TYPE_Q5_K) {  // (sumi, mins) per super-block, as q4_K
+        const uint8_t* blk = row + (int64_t)b * KF_Q5_K_BYTES;
+        int sumi = 0, mins = 0;
+        for (int j = 0; j < 4; j++) {
+            KfQ5Lane u;
+            u.load(blk, j);
+            int isum, imin;
+            u.dot(x + b * 256, xs32 + (int64_t)r * (n / 32) + b * 8, j, isum, imin);
+            sumi += isum;
+            mins += imin;
+        }
+        out[2 * t] = sumi;
+        out[2 * t + 1] = mins;
+        return;
+    }
     if (ty == KF_TYPE_Q8_0) {
         Q8Unit u;
         u.load(row, b);
@@ -795,6 +823,6 @@ hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, c
     const int threads = 256;
     block_ints_kernel<<<(unsigned)((total + threads - 1) / threads), threads, 0, s>>>(
         ty, static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + off.q),
-        reinterpret_cast<const int32_t*>(base + off.s32), n, n_out, rows, out);
+        reinterpret_cast<const int32_t*>(base + off.s16), reinterpret_cast<const int32_t*>(base + off.s32), n, n_out, rows, out);
     return hipGetLastError();
 }

@@ -78,3 +78,87 @@ __device__ __forceinline__ int kf_q8_0_dot(const uint32_t* wq, const uint4 x0, c
     s = kf_dot4(wq[7], x1.w, s);
     return s;
 }
+
+// q6_K lane unit: quarter j of a super-block, i.e. half h = j >> 1 and offsets l in [16 (j & 1), +16) of the half's
+// four 32-element runs: the 16-element groups g = 8h + (j & 1) + 2k (k < 4). The lane's integer is
+// sum_k sc_g (dot_g - 32 bsum_g), with dot_g of the unsigned 6-bit values (0..63) and the int8 activations; the four
+// lanes of a super-block add up to the reference's dot - bias (crates/kf-quant/src/types/q6_k.rs:17-59), exactly.
+struct KfQ6Lane {
+    uint4 a, b, h;  // ql bytes of runs k = 0, 2 (a) and 1, 3 (b), and the qh bytes, at the lane's 16 offsets
+    int sc[4];      // the int8 scales of the lane's groups
+    float d;
+
+    // blk: the super-block's 210 bytes (2-byte aligned)
+    __device__ __forceinline__ void load(const uint8_t* blk, int j) {
+        const int hh = j >> 1, o = 16 * (j & 1);
+        a = kf_load_stream_u4_unaligned(blk + 64 * hh + o);
+        b = kf_load_stream_u4_unaligned(blk + 64 * hh + 32 + o);
+        h = kf_load_stream_u4_unaligned(blk + 128 + 32 * hh + o);
+#pragma unroll
+        for (int k = 0; k < 4; k++) sc[k] = (int)(int8_t)blk[192 + 8 * hh + (j & 1) + 2 * k];
+        d = kf_h2f(*reinterpret_cast<const uint16_t*>(blk + 208));
+    }
+
+    // x: the super-block's 256 int8 activations (16-byte aligned); s16: its 16 per-16 integer sums
+    __device__ __forceinline__ int dot(const int8_t* x, const int32_t* s16, int j) const {
+        const int hh = j >> 1, o = 16 * (j & 1);
+        const uint32_t m4 = 0x0f0f0f0fu, m30 = 0x30303030u;
+        const uint32_t av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w}, hv[4] = {h.x, h.y, h.z, h.w};
+        int isum = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            const uint4 xv = *reinterpret_cast<const uint4*>(x + 128 * hh + 32 * k + o);
+            const uint32_t xs[4] = {xv.x, xv.y, xv.z, xv.w};
+            int dt = 0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                uint32_t wq;
+                if (k == 0) wq = (av[e] & m4) | ((hv[e] << 4) & m30);
+                else if (k == 1) wq = (bv[e] & m4) | ((hv[e] << 2) & m30);
+                else if (k == 2) wq = ((av[e] >> 4) & m4) | (hv[e] & m30);
+                else wq = ((bv[e] >> 4) & m4) | ((hv[e] >> 2) & m30);
+                dt = kf_dot4(wq, xs[e], dt);
+            }
+            // |dot| <= 63 * 128 * 16 and |sc| <= 128: 24-bit multiplies are exact
+            isum += __mul24(sc[k], dt - 32 * s16[8 * hh + (j & 1) + 2 * k]);
+        }
+        return isum;
+    }
+};
+
+// q5_K lane unit: pair j of sub-blocks (2j, 2j+1), q4_K's unit with the fifth bit of element l of sub-block s taken
+// from bit s of qh[l] (crates/kf-quant/src/types/q5_k.rs:7-60); the four lanes' isum and imin add up to the
+// super-block's sumi and mins.
+struct KfQ5Lane {
+    uint4 hdr, qa, qb, ha, hb;
+
+    // blk: the super-block's 176 bytes (16-byte aligned)
+    __device__ __forceinline__ void load(const uint8_t* blk, int j) {
+        hdr = kf_load_stream_u4(blk);
+        ha = kf_load_stream_u4(blk + 16);
+        hb = kf_load_stream_u4(blk + 32);
+        qa = kf_load_stream_u4(blk + 48 + 32 * j);
+        qb = kf_load_stream_u4(blk + 64 + 32 * j);
+    }
+
+    // x: the super-block's 256 int8 activations; s32: its 8 per-32 integer sums
+    __device__ __forceinline__ void dot(const int8_t* x, const int32_t* s32, int j, int& isum, int& imin) const {
+        const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
+        const uint32_t q[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        const uint32_t hq[8] = {ha.x, ha.y, ha.z, ha.w, hb.x, hb.y, hb.z, hb.w};
+        const uint4* xl = reinterpret_cast<const uint4*>(x + 64 * j);
+        const uint4 x0 = xl[0], x1 = xl[1], x2 = xl[2], x3 = xl[3];
+        const uint32_t xlo[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+        const uint32_t xhi[8] = {x2.x, x2.y, x2.z, x2.w, x3.x, x3.y, x3.z, x3.w};
+        int dlo = 0, dhi = 0;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            dlo = kf_dot4((q[e] & m4) | (((hq[e] >> (2 * j)) & m1) << 4), xlo[e], dlo);
+            dhi = kf_dot4(((q[e] >> 4) & m4) | (((hq[e] >> (2 * j + 1)) & m1) << 4), xhi[e], dhi);
+        }
+        uint32_t sc2, m2;
+        kf_q4k_scales(hdr.y, hdr.z, hdr.w, j, sc2, m2);
+        isum = __mul24((int)(sc2 & 0xffu), dlo) + __mul24((int)(sc2 >> 8), dhi);
+        imin = __mul24((int)(m2 & 0xffu), s32[2 * j]) + __mul24((int)(m2 >> 8), s32[2 * j + 1]);
+    }
+};

@@ -5,12 +5,19 @@
 //   q4_K: 256 elements in 144 bytes, f16 d, f16 dmin, 12 bytes of packed 6-bit scales and mins for 8 sub-blocks of
 //         32, then 128 bytes of nibbles; pair j of sub-blocks (2j, 2j+1) lives in bytes 16+32j..48+32j, the low
 //         nibble of byte 16+32j+l being element 64j+l and the high nibble element 64j+32+l.
+//   q5_K (types/q5_k.rs:4): 256 elements in 176 bytes, q4_K's header (16 bytes), then qh[32] (bit s of qh[l] is the
+//         fifth bit of element l of sub-block s), then q4_K's 128 bytes of low nibbles.
+//   q6_K (types/q6_k.rs:4): 256 elements in 210 bytes, ql[128] (low 4 bits), qh[64] (high 2 bits), 16 int8 scales
+//         (one per 16 elements), f16 d at byte 208; element 128h + 32k + l (h < 2, k < 4, l < 32) is
+//         (ql[64h + l + 32 (k & 1)] >> 4 (k >> 1)) & 15 | ((qh[32h + l] >> 2k) & 3) << 4, minus 32.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
 
 #define KF_TYPE_Q8_0 8u
 #define KF_TYPE_Q4_K 12u
+#define KF_TYPE_Q5_K 13u
+#define KF_TYPE_Q6_K 14u
 
 #define KF_ACT_Q8_0 3
 #define KF_ACT_Q8K 4
@@ -19,6 +26,8 @@
 #define KF_Q8_0_BYTES 34
 #define KF_Q4_K_BLOCK 256
 #define KF_Q4_K_BYTES 144
+#define KF_Q5_K_BYTES 176
+#define KF_Q6_K_BYTES 210
 
 // Alignment of every section of the activation scratch
 #define KF_ACT_ALIGN 256

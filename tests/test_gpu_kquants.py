@@ -1,0 +1,93 @@
+"""GPU parity of the q5_K and q6_K products through the C ABI: per-block integers bit-exact against the oracle (the
+reference's dot_i8 integers), f32 outputs within |got - want| <= 1e-4 + 1e-3 |want| of the CPU backend's
+matmul_slice, for one and several activation rows, ragged shapes, bias and residual."""
+import numpy as np
+import pytest
+
+import kungfu_amd as kf
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _tensor(a, dev):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _random_blocks(ty, n_out, n_in, rng):
+    """Random block bytes with f16 scales in the range real weights use (2^-14..2^-7: d and dmin of q5_K, d of q6_K);
+    larger ones give outputs whose terms reach hundreds, where an output that cancels to near zero sits below the f32
+    rounding of its terms in any summation order."""
+    size = kf.BLOCK[ty][1]
+    w = rng.integers(0, 256, (n_out, n_in // 256, size), dtype=np.uint8)
+    for at in ((0, 2) if ty == kf.TYPE_Q5_K else (208,)):
+        bits = (((1 + rng.integers(0, 8, w.shape[:2])) << 10) | rng.integers(0, 1024, w.shape[:2])).astype(np.uint16)
+        w[:, :, at : at + 2] = bits.view(np.uint8).reshape(w.shape[0], w.shape[1], 2)
+    return w.reshape(n_out, -1)
+
+
+def _close(got, want):
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bound = 1e-4 + 1e-3 * np.abs(want.astype(np.float64))
+    assert (err <= bound).all(), f"max err {err.max():.3e} at {np.unravel_index(np.argmax(err - bound), err.shape)}"
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("rows,n,n_out", [(1, 256, 5), (2, 1024, 7), (3, 4096, 3)])
+def test_block_ints_bit_exact(cuda, ty, rows, n, n_out):
+    import torch
+
+    rng = np.random.default_rng(n + n_out + ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.act_kind(ty))
+    per = n // 256 if ty == kf.TYPE_Q6_K else 2 * (n // 256)
+    out = torch.zeros(n_out * rows * per, dtype=torch.int32, device=cuda)
+    kf.block_ints(ty, _tensor(w, cuda), act, out, rows, n, n_out)
+    got = out.cpu().numpy().reshape(n_out, rows, per)
+    q, _, s16 = oracle.quantize_activations(kf.act_kind(ty), x)
+    for o in range(n_out):
+        for r in range(rows):
+            assert np.array_equal(got[o, r], oracle.block_ints(ty, w[o], q[r], s16[r])), (o, r)
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("rows,n,n_out", [(1, 256, 1), (1, 2304, 33), (1, 4096, 520), (1, 14336, 300), (3, 1024, 77),
+                                          (8, 4096, 64), (13, 2048, 40)])
+def test_product_matches_cpu_backend(cuda, ty, rows, n, n_out):
+    """kf_hip_matmul (quant_act + the q5_K/q6_K product) against matmul_slice, with bias and residual; 13 rows take two
+    launches (eight rows a weight pass), 2304 columns a ragged wave pass (nine super-blocks)."""
+    import torch
+
+    rng = np.random.default_rng(rows * 1000 + n + n_out + ty)
+    w = kf.quantize(ty, kf.synth_normal(ty + n, 0.02, n * n_out).reshape(n_out, n))
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    bias = rng.standard_normal(n_out).astype(np.float32)
+    res = rng.standard_normal((rows, n_out)).astype(np.float32)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.empty((rows, n_out), device=cuda)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    want = oracle.matmul_slice(ty, w, n, n_out, x, bias) + res
+    _close(y.cpu().numpy(), want)
+
+
+def test_product_on_random_blocks(cuda):
+    """Random block bytes (every scale and bit pattern) at one and five rows through kf_hip_gemv directly."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    for ty in (kf.TYPE_Q5_K, kf.TYPE_Q6_K):
+        n, n_out = 1536, 29
+        w = _random_blocks(ty, n_out, n, rng)
+        for rows in (1, 5):
+            x = rng.standard_normal((rows, n)).astype(np.float32)
+            act = kf.alloc_act(rows, n, cuda)
+            kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+            y = torch.empty((rows, n_out), device=cuda)
+            kf.gemv(ty, _tensor(w, cuda), act, y, rows, n, n_out)
+            torch.cuda.synchronize()
+            _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))

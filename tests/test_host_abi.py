@@ -35,9 +35,10 @@ def test_act_layout_sections_are_aligned_and_sized():
 def test_act_kind_pairs_weight_types():
     assert kf.act_kind(kf.TYPE_Q8_0) == kf.ACT_Q8_0
     assert kf.act_kind(kf.TYPE_Q4_K) == kf.ACT_Q8K
+    assert kf.act_kind(kf.TYPE_Q6_K) == kf.ACT_Q8K
     with pytest.raises(kf.KfError) as e:
-        kf.act_kind(14)
-    assert e.value.code == kf.KF_E_UNSUPPORTED and "14" in str(e.value)
+        kf.act_kind(2)
+    assert e.value.code == kf.KF_E_UNSUPPORTED and "2" in str(e.value)
 
 
 FAKE = 0x10000  # a 256-byte aligned address the checks must reject before any HIP call
@@ -115,6 +116,52 @@ def test_quantize_q4_k_round_trip():
         rel = np.sqrt(((deq[r] - x[r]) ** 2).mean()) / np.sqrt((x[r] ** 2).mean() + 1e-30)
         if r != 1:
             assert rel < 0.12
+
+
+def test_quantize_q5_k_and_q6_k_round_trip():
+    """The library's q5_K / q6_K encoders read back through the oracle's dequant (pinned to ggml's fixtures): errors
+    within half a quantization step plus the scale roundings, zeros exact, and the expected RMS ordering."""
+    rng = np.random.default_rng(13)
+    x = (rng.standard_normal((4, 1024)) * 0.02).astype(np.float32)
+    x[1, :256] = 0.0
+    rel = {}
+    for ty, size in ((kf.TYPE_Q5_K, 176), (kf.TYPE_Q6_K, 210)):
+        w = kf.quantize(ty, x)
+        assert w.shape == (4, 4 * size)
+        deq = oracle.dequant(ty, w, 1024)
+        assert not deq[1, :256].any()
+        for r in range(4):
+            blk = w[r].reshape(-1, size)
+            for b in range(4):
+                xs = x[r, 256 * b : 256 * (b + 1)]
+                err = np.abs(deq[r, 256 * b : 256 * (b + 1)] - xs)
+                if ty == kf.TYPE_Q6_K:
+                    d = float(blk[b, 208:210].copy().view(np.float16)[0])
+                    g = xs.reshape(16, 16)
+                    # per 16: half a step of amax / 31, plus the int8 scale rounding (half of d) over 31 steps
+                    step = np.abs(g).max(axis=1) / 31
+                    assert (err.reshape(16, 16).max(axis=1) <= 0.5 * step + 31 * 0.5 * d + 1e-7).all()
+                else:
+                    d = float(blk[b, 0:2].copy().view(np.float16)[0])
+                    dmin = float(blk[b, 2:4].copy().view(np.float16)[0])
+                    g = xs.reshape(8, 32)
+                    step = (g.max(axis=1) - np.minimum(g.min(axis=1), 0)) / 31
+                    assert (err.reshape(8, 32).max(axis=1) <= 0.5 * step + 0.5 * d + 0.5 * dmin + 64 * d + 1e-7).all()
+        rel[ty] = np.sqrt(((deq - x) ** 2).mean() / (x ** 2).mean())
+    q4 = oracle.dequant(12, kf.quantize(kf.TYPE_Q4_K, x), 1024)
+    assert rel[kf.TYPE_Q6_K] < rel[kf.TYPE_Q5_K] < np.sqrt(((q4 - x) ** 2).mean() / (x ** 2).mean())
+
+
+def test_k_quant_types_take_the_k_product_and_reject_the_gemm():
+    L = kf.lib()
+    assert kf.act_kind(kf.TYPE_Q5_K) == kf.ACT_Q8K and kf.act_kind(kf.TYPE_Q6_K) == kf.ACT_Q8K
+    rc = L.kf_hip_gemm_i8(kf.TYPE_Q6_K, FAKE, kf.row_bytes(14, 4096), FAKE, None, None, FAKE, 64, 4096, 16, None)
+    assert rc == kf.KF_E_UNSUPPORTED and "kf_hip_gemv" in kf.last_error()
+    rc = L.kf_hip_moe_gemv(kf.TYPE_Q5_K, FAKE, None, kf.row_bytes(13, 4096) * 16, kf.row_bytes(13, 4096), FAKE, 1, 4096, 16,
+                           FAKE, FAKE, 1, 1, 0, FAKE, None)
+    assert rc == kf.KF_E_UNSUPPORTED and "q8_0 and q4_K" in kf.last_error()
+    rc = L.kf_hip_gemv(kf.TYPE_Q6_K, FAKE, kf.row_bytes(14, 4096) + 2, FAKE, None, None, FAKE, 1, 4096, 16, None)
+    assert rc == kf.KF_E_INVALID and "row_bytes" in kf.last_error()
 
 
 def _synth_numpy(seed, sigma, n):
