@@ -7,7 +7,11 @@
 // Design: one wave per output row at a time, four lanes per super-block (the lane units KfQ5Lane / KfQ6Lane), so a
 // wave pass covers 16 super-blocks (4096 columns) of the row; up to eight activation rows against every weight pass
 // (the weights are read once per eight rows). Activations are read from the scratch in global memory (a few KB per
-// row, L2-resident). The q6_K super-block is 210 bytes, so its loads are 2-byte aligned 16-byte loads.
+// row, L2-resident). With 16-byte aligned rows (q5_K always, q6_K when the row has a multiple of eight super-blocks)
+// a pass's bytes travel as contiguous 16-byte pieces (lane l takes pieces l, l + 64, ...: every wave load
+// instruction reads 1 KB of consecutive bytes, the pattern that streams at the chip's read rate), are parked in the
+// wave's own LDS buffer and read back by the lanes; otherwise each lane loads its unit's bytes straight from memory
+// (2-byte aligned 16-byte loads for q6_K's 210-byte super-blocks).
 #include "kf_blocks.h"
 
 #include <algorithm>
@@ -16,8 +20,10 @@ namespace {
 
 constexpr int GK_THREADS = 256;
 constexpr int GK_WAVES = GK_THREADS / 64;
+constexpr int GK_PIECES = 4;  // 16-byte pieces a lane moves per pass: 210 (q6_K) or 176 (q5_K) over 64 lanes
+constexpr int GK_WBUF = 16 * KF_Q6_K_BYTES;  // one pass of 16 super-blocks
 
-template <uint32_t TY, int R>
+template <uint32_t TY, int R, bool PARK>
 __global__ void __launch_bounds__(GK_THREADS) gemv_k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                             const int32_t* __restrict__ xs16, const int32_t* __restrict__ xs32,
                                                             const float* __restrict__ xd16, const float* __restrict__ bias,
@@ -28,18 +34,47 @@ __global__ void __launch_bounds__(GK_THREADS) gemv_k_kernel(const uint8_t* __res
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nsb = n / 256, n16 = n / 16, n32 = n / 32;
     const int j = lane & 3;
-    for (int row = blockIdx.x * GK_WAVES + wave; row < n_out; row += gridDim.x * GK_WAVES) {
+    __shared__ __align__(16) uint8_t park[PARK ? GK_WAVES * GK_WBUF : 16];
+    uint8_t* wbuf = park + (PARK ? wave * GK_WBUF : 0);
+    const int stride = gridDim.x * GK_WAVES;
+    const int npass = (nsb + 15) / 16;
+    int row = blockIdx.x * GK_WAVES + wave;  // wave-uniform
+    uint4 v[GK_PIECES];                      // the next (row, pass) item's pieces in flight (PARK)
+    auto fetch = [&](int rw, int sb0) {
+        // 16-byte pieces clamped onto the pass's last 16 bytes (no byte past the pass is read)
+        const int len = min(16, nsb - sb0) * BYTES;
+        const uint8_t* src = w + (int64_t)rw * row_bytes + (int64_t)sb0 * BYTES;
+#pragma unroll
+        for (int i = 0; i < GK_PIECES; i++) v[i] = kf_load_stream_u4(src + min(16 * (lane + 64 * i), len - 16));
+    };
+    if constexpr (PARK) {
+        if (row < n_out) fetch(row, 0);
+    }
+    for (; row < n_out; row += stride) {
         float acc[R];
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = 0.0f;
         const uint8_t* wr = w + (int64_t)row * row_bytes;
-        for (int sb0 = 0; sb0 < nsb; sb0 += 16) {
+        for (int p = 0; p < npass; p++) {
+            const int sb0 = 16 * p;
             const int sb = sb0 + (lane >> 2);
+            const uint8_t* blk;
+            if constexpr (PARK) {
+                const int len = min(16, nsb - sb0) * BYTES;
+#pragma unroll
+                for (int i = 0; i < GK_PIECES; i++) *reinterpret_cast<uint4*>(wbuf + min(16 * (lane + 64 * i), len - 16)) = v[i];
+                // the wave's next item (this row's next pass, or its next row's first) is requested before this
+                // pass is multiplied; one wave's LDS operations complete in order, so no barrier guards the buffer
+                if (p + 1 < npass) fetch(row, sb0 + 16);
+                else if (row + stride < n_out) fetch(row + stride, 0);
+                blk = wbuf + (lane >> 2) * BYTES;
+            } else {
+                blk = wr + (int64_t)sb * BYTES;
+            }
             if (sb < nsb) {
-                const uint8_t* blk = wr + (int64_t)sb * BYTES;
                 if constexpr (TY == KF_TYPE_Q6_K) {
                     KfQ6Lane u;
-                    u.load(blk, j);
+                    u.template load<PARK>(blk, j);
 #pragma unroll
                     for (int r = 0; r < R; r++) {
                         if (r < rows) {
@@ -49,7 +84,7 @@ __global__ void __launch_bounds__(GK_THREADS) gemv_k_kernel(const uint8_t* __res
                     }
                 } else {
                     KfQ5Lane u;
-                    u.load(blk, j);
+                    u.template load<PARK>(blk, j);
                     const float d = kf_h2f(u.hdr.x & 0xffffu), dmin = kf_h2f(u.hdr.x >> 16);
 #pragma unroll
                     for (int r = 0; r < R; r++) {
@@ -66,29 +101,40 @@ __global__ void __launch_bounds__(GK_THREADS) gemv_k_kernel(const uint8_t* __res
 #pragma unroll
         for (int r = 0; r < R; r++) {
             if (r < rows) {
-                const float v = kf_wave_sum(acc[r]);
+                const float vs = kf_wave_sum(acc[r]);
                 if (lane == 0) {
                     const int64_t o = (int64_t)r * ld_y + row;
-                    y[o] = v + (bias ? bias[row] : 0.0f) + (res ? res[o] : 0.0f);
+                    y[o] = vs + (bias ? bias[row] : 0.0f) + (res ? res[o] : 0.0f);
                 }
             }
         }
     }
 }
 
-template <uint32_t TY>
+int gk_cus() {
+    static int cus = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1)
+            v = 256;
+        return v;
+    }();
+    return cus;
+}
+
+template <uint32_t TY, bool PARK>
 hipError_t launch_k(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs16, const int32_t* xs32, const float* xd16,
                     const float* bias, const float* res, float* y, int rows, int n, int n_out, hipStream_t s) {
-    const int grid = (n_out + GK_WAVES - 1) / GK_WAVES;
+    // a resident grid of four blocks per CU; each wave walks its rows with the next (row, pass) in flight
+    const int grid = std::min((n_out + GK_WAVES - 1) / GK_WAVES, 4 * gk_cus());
     // rows of one launch: 1, 2, 4 or 8 (the kernel skips rows past `rows`)
     if (rows == 1)
-        gemv_k_kernel<TY, 1><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
+        gemv_k_kernel<TY, 1, PARK><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
     else if (rows == 2)
-        gemv_k_kernel<TY, 2><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
+        gemv_k_kernel<TY, 2, PARK><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
     else if (rows <= 4)
-        gemv_k_kernel<TY, 4><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
+        gemv_k_kernel<TY, 4, PARK><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
     else
-        gemv_k_kernel<TY, 8><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
+        gemv_k_kernel<TY, 8, PARK><<<grid, GK_THREADS, 0, s>>>(w, row_bytes, xq, xs16, xs32, xd16, bias, res, y, rows, n, n_out, n_out);
     return hipGetLastError();
 }
 
@@ -110,8 +156,15 @@ hipError_t kf_launch_gemv_k(uint32_t ty, const void* wv, int64_t row_bytes, cons
         const float* xd16 = reinterpret_cast<const float*>(base + o.d16) + (size_t)r0 * (n / 16);
         float* yc = y + (size_t)r0 * n_out;
         const float* rcp = res ? res + (size_t)r0 * n_out : nullptr;
-        const hipError_t e = ty == KF_TYPE_Q6_K ? launch_k<KF_TYPE_Q6_K>(w, row_bytes, xq, xs16, xs32, xd16, bias, rcp, yc, rc, n, n_out, s)
-                                                : launch_k<KF_TYPE_Q5_K>(w, row_bytes, xq, xs16, xs32, xd16, bias, rcp, yc, rc, n, n_out, s);
+        // parking needs 16-byte aligned passes: the weight base and every row start
+        const bool park = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0;
+        hipError_t e;
+        if (ty == KF_TYPE_Q6_K)
+            e = park ? launch_k<KF_TYPE_Q6_K, true>(w, row_bytes, xq, xs16, xs32, xd16, bias, rcp, yc, rc, n, n_out, s)
+                     : launch_k<KF_TYPE_Q6_K, false>(w, row_bytes, xq, xs16, xs32, xd16, bias, rcp, yc, rc, n, n_out, s);
+        else
+            e = park ? launch_k<KF_TYPE_Q5_K, true>(w, row_bytes, xq, xs16, xs32, xd16, bias, rcp, yc, rc, n, n_out, s)
+                     : launch_k<KF_TYPE_Q5_K, false>(w, row_bytes, xq, xs16, xs32, xd16, bias, rcp, yc, rc, n, n_out, s);
         if (e != hipSuccess) return e;
     }
     return hipSuccess;

@@ -88,14 +88,26 @@ struct KfQ6Lane {
     int sc[4];      // the int8 scales of the lane's groups
     float d;
 
-    // blk: the super-block's 210 bytes (2-byte aligned)
+    // blk: the super-block's 210 bytes (2-byte aligned), in global memory (LDS = false) or LDS (LDS = true)
+    template <bool LDS = false>
     __device__ __forceinline__ void load(const uint8_t* blk, int j) {
         const int hh = j >> 1, o = 16 * (j & 1);
-        a = kf_load_stream_u4_unaligned(blk + 64 * hh + o);
-        b = kf_load_stream_u4_unaligned(blk + 64 * hh + 32 + o);
-        h = kf_load_stream_u4_unaligned(blk + 128 + 32 * hh + o);
+        if constexpr (LDS) {
+            const kf_u32x4_a2 va = *reinterpret_cast<const kf_u32x4_a2*>(blk + 64 * hh + o);
+            const kf_u32x4_a2 vb = *reinterpret_cast<const kf_u32x4_a2*>(blk + 64 * hh + 32 + o);
+            const kf_u32x4_a2 vh = *reinterpret_cast<const kf_u32x4_a2*>(blk + 128 + 32 * hh + o);
+            a = make_uint4(va.x, va.y, va.z, va.w);
+            b = make_uint4(vb.x, vb.y, vb.z, vb.w);
+            h = make_uint4(vh.x, vh.y, vh.z, vh.w);
+        } else {
+            a = kf_load_stream_u4_unaligned(blk + 64 * hh + o);
+            b = kf_load_stream_u4_unaligned(blk + 64 * hh + 32 + o);
+            h = kf_load_stream_u4_unaligned(blk + 128 + 32 * hh + o);
+        }
+        // the eight scale bytes of the half as four 16-bit words; the lane's scales are bytes (j & 1) + 2k
+        const uint16_t* s2 = reinterpret_cast<const uint16_t*>(blk + 192 + 8 * hh);
 #pragma unroll
-        for (int k = 0; k < 4; k++) sc[k] = (int)(int8_t)blk[192 + 8 * hh + (j & 1) + 2 * k];
+        for (int k = 0; k < 4; k++) sc[k] = (int)(int8_t)(uint8_t)(s2[k] >> (8 * (j & 1)));
         d = kf_h2f(*reinterpret_cast<const uint16_t*>(blk + 208));
     }
 
@@ -132,13 +144,23 @@ struct KfQ6Lane {
 struct KfQ5Lane {
     uint4 hdr, qa, qb, ha, hb;
 
-    // blk: the super-block's 176 bytes (16-byte aligned)
+    // blk: the super-block's 176 bytes (16-byte aligned), in global memory (LDS = false) or LDS (LDS = true)
+    template <bool LDS = false>
     __device__ __forceinline__ void load(const uint8_t* blk, int j) {
-        hdr = kf_load_stream_u4(blk);
-        ha = kf_load_stream_u4(blk + 16);
-        hb = kf_load_stream_u4(blk + 32);
-        qa = kf_load_stream_u4(blk + 48 + 32 * j);
-        qb = kf_load_stream_u4(blk + 64 + 32 * j);
+        if constexpr (LDS) {
+            const uint4* p = reinterpret_cast<const uint4*>(blk);
+            hdr = p[0];
+            ha = p[1];
+            hb = p[2];
+            qa = p[3 + 2 * j];
+            qb = p[4 + 2 * j];
+        } else {
+            hdr = kf_load_stream_u4(blk);
+            ha = kf_load_stream_u4(blk + 16);
+            hb = kf_load_stream_u4(blk + 32);
+            qa = kf_load_stream_u4(blk + 48 + 32 * j);
+            qb = kf_load_stream_u4(blk + 64 + 32 * j);
+        }
     }
 
     // x: the super-block's 256 int8 activations; s32: its 8 per-32 integer sums
