@@ -194,6 +194,46 @@ int kf_hip_backend_matmul(kf_hip_backend* b, int wid, const float* x, int rows, 
 int kf_hip_backend_matmul_slice(kf_hip_backend* b, int wid, int index, const float* x, int rows, int cols, float* y);
 
 /* ---------------------------------------------------------------------------------------------------------------
+ * GGUF files (host). The reader of crates/kf-gguf/src/lib.rs: GGUF v2/v3, the typed key-value header (value kinds
+ * 0..12 as in the file, arrays of any kind), tensor infos with ggml dims innermost first, the data section aligned to
+ * general.alignment (32 when absent), and split files name-0000i-of-0000N.gguf opened as one. Shards are memory-mapped
+ * read-only; kf_gguf_tensor_data returns a pointer into the map (valid until kf_gguf_close), which goes straight to
+ * kf_hip_backend_add_weight as the reference's WeightSource::bytes borrows from its mmap (kf-engine/src/loader.rs).
+ * Metadata is iterated in key order (the reference keeps a BTreeMap; a repeated key keeps its last value). */
+typedef struct kf_gguf kf_gguf;
+
+/* Gguf::open (lib.rs:181-203): NULL on failure, with the reason in kf_hip_last_error(). */
+kf_gguf* kf_gguf_open(const char* path);
+void kf_gguf_close(kf_gguf* g);
+int kf_gguf_n_shards(const kf_gguf* g);
+
+/* Tensors in file order, shard by shard; kf_gguf_find_tensor is Gguf::tensor (lib.rs:209-211), KF_E_INVALID if absent. */
+int64_t kf_gguf_n_tensors(const kf_gguf* g);
+int64_t kf_gguf_find_tensor(const kf_gguf* g, const char* name);
+
+/* Tensor i: name (owned by g), up to max_dims dims, ggml type, shard, offset in its shard's data section and byte size
+ * (TensorInfo::nbytes, lib.rs:157-160: -1 when the type has no known layout or the inner dim is not a multiple of its
+ * block). Returns the number of dims. Nullable outputs. */
+int kf_gguf_tensor_info(const kf_gguf* g, int64_t i, const char** name, int64_t* dims, int max_dims, uint32_t* ggml_type, int* shard,
+                        uint64_t* offset, int64_t* nbytes);
+
+/* Gguf::bytes (lib.rs:213-219): the tensor's bytes inside its shard's map, NULL when its size is unknown or the data
+ * runs past the end of the file. */
+const void* kf_gguf_tensor_data(const kf_gguf* g, int64_t i);
+
+/* Metadata entry i (key order): key, value kind, element kind (arrays; the kind itself for scalars) and element count
+ * (1 for scalars). Typed reads follow Value::as_u64 / as_i64 / as_f64 (lib.rs:28-62): unsigned reads take non-negative
+ * signed values and bools, signed reads any integer, float reads floats and integers; idx selects an array element
+ * (0 for a scalar). */
+int64_t kf_gguf_n_kv(const kf_gguf* g);
+int64_t kf_gguf_find_kv(const kf_gguf* g, const char* key);
+int kf_gguf_kv(const kf_gguf* g, int64_t i, const char** key, uint32_t* kind, uint32_t* elem_kind, uint64_t* count);
+int kf_gguf_kv_u64(const kf_gguf* g, int64_t i, uint64_t idx, uint64_t* out);
+int kf_gguf_kv_i64(const kf_gguf* g, int64_t i, uint64_t idx, int64_t* out);
+int kf_gguf_kv_f64(const kf_gguf* g, int64_t i, uint64_t idx, double* out);
+int kf_gguf_kv_str(const kf_gguf* g, int64_t i, uint64_t idx, const char** out, uint64_t* len);
+
+/* ---------------------------------------------------------------------------------------------------------------
  * Host utilities (CPU).
  * kf_quantize_q8_0: q8_0::quantize_row (crates/kf-quant/src/types/q8_0.rs:33-42, re-exported at lib.rs:2) over rows.
  * kf_quantize_q4_k: a q4_K encoder of this library's own. The reference has none (it only reads q4_K); this one fits

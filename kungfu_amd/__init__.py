@@ -89,6 +89,20 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_quantize_q5_k": ([P, L64, I, P], I),
         "kf_quantize_q6_k": ([P, L64, I, P], I),
         "kf_synth_normal": ([ctypes.c_uint64, ctypes.c_float, P, S], None),
+        "kf_gguf_open": ([ctypes.c_char_p], P),
+        "kf_gguf_close": ([P], None),
+        "kf_gguf_n_shards": ([P], I),
+        "kf_gguf_n_tensors": ([P], L64),
+        "kf_gguf_find_tensor": ([P, ctypes.c_char_p], L64),
+        "kf_gguf_tensor_info": ([P, L64, ctypes.POINTER(ctypes.c_char_p), P, I, P, P, P, P], I),
+        "kf_gguf_tensor_data": ([P, L64], P),
+        "kf_gguf_n_kv": ([P], L64),
+        "kf_gguf_find_kv": ([P, ctypes.c_char_p], L64),
+        "kf_gguf_kv": ([P, L64, ctypes.POINTER(ctypes.c_char_p), P, P, P], I),
+        "kf_gguf_kv_u64": ([P, L64, ctypes.c_uint64, P], I),
+        "kf_gguf_kv_i64": ([P, L64, ctypes.c_uint64, P], I),
+        "kf_gguf_kv_f64": ([P, L64, ctypes.c_uint64, P], I),
+        "kf_gguf_kv_str": ([P, L64, ctypes.c_uint64, ctypes.POINTER(ctypes.c_void_p), P], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

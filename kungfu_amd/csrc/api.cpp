@@ -57,6 +57,20 @@ int fail(int code, const char* fmt, ...) {
 
 int hip_fail(hipError_t e, const char* what) { return fail(KF_E_HIP, "%s: %s", what, hipGetErrorString(e)); }
 
+}  // namespace
+
+// The thread's last error, for the other translation units of the library (gguf.cpp)
+void kf_set_error(const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+}
+
+namespace {
+
 bool type_info(uint32_t ty, int& block, int& bytes) {
     if (ty == KF_TYPE_Q8_0) {
         block = KF_Q8_0_BLOCK;
