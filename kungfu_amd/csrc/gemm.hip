@@ -443,19 +443,24 @@ __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __r
 //     [0, 63]) fills eight k slots with hi against 64 m_j and eight with lo against m_j; every product and partial sum
 //     is an integer below 2^24, so the f32 result is exact;
 //   * the float rescale runs once per super-block and output (shift-add, convert, three float operations).
-// Staging is all DMA (global_load_lds_dwordx4), no register round trip:
-//   * an A stage (128 activation columns) sits in LDS as [group][32-row tile] 1 KB blocks in MFMA order (lane l reads
-//     bytes 16 l..: row l % 32, columns 16 (l / 32).. of the group), one DMA instruction per block;
+// Staging is all DMA (buffer_load_dwordx4 ... lds), no register round trip, one stage per super-block (K = 256):
+//   * the activations sit in LDS as [group][32-row tile] 1 KB blocks in MFMA order (lane l reads bytes 16 l..: row
+//     l % 32, columns 16 (l / 32).. of the group), one DMA instruction per block;
 //   * the weights' raw nibble bytes sit as [pair][32-row tile] 1 KB blocks (lane l: row l % 32, bytes 16 (l / 32)..
 //     of the sub-block pair), in which each lane holds the bytes of its MFMA operand for both groups of the pair
 //     (low nibbles: group 2p, high nibbles: group 2p + 1); the consuming wave expands them into the two planes in
 //     registers (a mask, a shift and a packed 16-bit multiply per plane and dword);
-//   * once per super-block the rows' 16-byte headers, the activation scales dx and the activation group sums are
-//     fetched the same way into a record, double-buffered by super-block parity.
+//   * the rows' 16-byte headers, the activation scales dx and the activation group sums travel in the same stage
+//     buffer, so one barrier per super-block hands a buffer back to the DMA;
+//   * the DMA sources are buffer resources over the block's first rows: the per-lane offsets are computed once and a
+//     super-block adds only a scalar offset, so the K loop spends no vector instructions on addresses.
+// Two stage buffers (about 109 KB of LDS, one block per CU), each a distinct static array and the K loop unrolled by
+// two, so the compiler waits for a DMA only before reads of the buffer it fills.
 // Measured on gfx950, the alternatives were slower: staging through registers let the compiler sink the prefetch
-// loads to their LDS stores (the full memory latency every stage), one LDS array made it wait for every outstanding
-// DMA before each LDS read (so the buffers are distinct static arrays), and wave tiles above two 32 x 32 tiles push the
-// two chains and the float accumulator (48 registers a tile) into AGPRs, which the compiler then copies every stage.
+// loads to their LDS stores (the full memory latency every stage); one LDS array made it wait for every outstanding
+// DMA before each LDS read; 128-column stages with the record in a separate buffer (register copies of it every
+// stage) ran 7% slower; wave tiles above two 32 x 32 tiles (four waves of 4 x 1 or 2 x 2 tiles, using AGPRs) ran
+// 25-35% slower, and so did letting the two waves of a SIMD run the MFMA and rescale phases out of step.
 // Eight waves (two per SIMD), each a 64 x 32 tile; blocks in XCD order (gm_tile).
 
 // Packed 16-bit multiply of the bytes of x by a small s: exact per byte while every byte product stays below 256
@@ -479,232 +484,19 @@ __device__ __forceinline__ void gm_tile(int nt, int mt, int& tm, int& tn) {
     tm = t - tn * mt;
 }
 
-template <int WM, int WN, int TM, int TN>
-struct GdCfg {
-    static constexpr int W = WM * WN, THREADS = 64 * W;
-    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
-    static constexpr int MT = BM / 32, NT = BN / 32;
-    static constexpr int A_BYTES = MT * GM_G * 1024, B_BYTES = 2 * NT * 1024;
-    static constexpr int STAGE = A_BYTES + B_BYTES;
-    static constexpr int NA = MT * GM_G, NB = 2 * NT;              // DMA instructions per stage
-    static constexpr int NH = (BN + 63) / 64, ND = (BM + 63) / 64, NX = MT;  // per super-block: headers, dx, sums
-    static constexpr int HDR = 0, DX = HDR + NH * 1024, XS = DX + ND * 256;
-    static constexpr int REC = XS + NX * 1024;
-    static constexpr int TOTAL = 2 * STAGE + 2 * REC;
-};
-
-template <int WM, int WN, int TM, int TN>
-__global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q4k_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
-                                                                    const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
-                                                                    const float* __restrict__ xd32, const float* __restrict__ bias,
-                                                                    const float* __restrict__ res, float* __restrict__ y, int M, int N,
-                                                                    int K) {
-    using C = GdCfg<WM, WN, TM, TN>;
-    // four distinct LDS objects, so that the compiler can tell a DMA into one buffer from reads of another (with one
-    // array it waits for every outstanding DMA before each LDS read)
-    __shared__ __align__(16) uint8_t buf0[C::STAGE];
-    __shared__ __align__(16) uint8_t buf1[C::STAGE];
-    __shared__ __align__(16) uint8_t rec0[C::REC];
-    __shared__ __align__(16) uint8_t rec1[C::REC];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    gm_tile((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM, tm, tn);
-    const int m0 = tm * C::BM, n0 = tn * C::BN;
-    const int kg = K >> 5;
-    const int nsb = K / KF_Q4_K_BLOCK;
-    const int half = lane >> 5, r32 = lane & 31;
-
-    // the DMA instructions of one stage (and, with rec, of its super-block record), spread over the waves
-    auto dma = [&](int st, uint8_t* buf, uint8_t* rec) {
-        const int sb = st >> 1;
-        for (int q = wave; q < C::NA; q += C::W) {
-            const int g = q / C::MT, t = q % C::MT;
-            const int m = min(m0 + t * 32 + r32, M - 1);
-            kf_dma16(xq + (int64_t)m * K + st * GM_BK + g * 32 + half * 16, buf + q * 1024);
-        }
-        for (int q = wave; q < C::NB; q += C::W) {
-            const int p = q / C::NT, t = q % C::NT;
-            const int n = min(n0 + t * 32 + r32, N - 1);
-            kf_dma16(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES + 16 + 32 * (2 * (st & 1) + p) + half * 16,
-                     buf + C::A_BYTES + q * 1024);
-        }
-        if (rec) {
-            constexpr int NR = C::NH + C::ND + C::NX;
-            for (int q = wave; q < NR; q += C::W) {
-                if (q < C::NH) {
-                    const int n = min(n0 + q * 64 + lane, N - 1);
-                    kf_dma16(w + (int64_t)n * row_bytes + (int64_t)sb * KF_Q4_K_BYTES, rec + C::HDR + q * 1024);
-                } else if (q < C::NH + C::ND) {
-                    const int qq = q - C::NH;
-                    const int m = min(m0 + qq * 64 + lane, M - 1);
-                    kf_dma4(xd32 + (int64_t)m * kg + sb * 8, rec + C::DX + qq * 256);
-                } else {
-                    const int qq = q - C::NH - C::ND;
-                    const int m = min(m0 + qq * 32 + (lane >> 1), M - 1);
-                    kf_dma16(xs32 + (int64_t)m * kg + sb * 8 + (lane & 1) * 4, rec + C::XS + qq * 1024);
-                }
-            }
-        }
-    };
-
-    v16f acc[TM][TN];
-    v16i slo[TM][TN], shi[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
-
-    // one stage: pairs p = 0, 1 of the stage, pair P = 2 h + p of the super-block; the chains restart with the
-    // super-block's first group
-    auto stage = [&](const uint8_t* buf, const uint4 (&hd)[TN], int h) {
-#pragma unroll
-        for (int p = 0; p < 2; p++) {
-            v4i bl[2][TN], bh[2][TN];
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(buf + C::A_BYTES + ((p * C::NT + wn * TN + j) * 64 + lane) * 16);
-                uint32_t sc2, m2;
-                kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, 2 * h + p, sc2, m2);
-                const uint32_t s0 = sc2 & 0xffu, s1 = sc2 >> 8;
-                const uint32_t l0 = s0 & 7u, u0 = s0 >> 3, l1 = s1 & 7u, u1 = s1 >> 3;
-                const uint32_t m4 = 0x0f0f0f0fu;
-                const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint32_t lo = v[e] & m4, hi = (v[e] >> 4) & m4;
-                    bl[0][j][e] = (int)gs_pmul(lo, l0);
-                    bh[0][j][e] = (int)gs_pmul(lo, u0);
-                    bl[1][j][e] = (int)gs_pmul(hi, l1);
-                    bh[1][j][e] = (int)gs_pmul(hi, u1);
-                }
-            }
-#pragma unroll
-            for (int gg = 0; gg < 2; gg++) {
-                const int g = 2 * p + gg;
-                v4i a[TM];
-#pragma unroll
-                for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const v4i*>(buf + ((g * C::MT + wm * TM + i) * 64 + lane) * 16);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        const bool z = h == 0 && g == 0;
-                        slo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bl[gg][j], z ? v16i{} : slo[i][j], 0, 0, 0);
-                        shi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bh[gg][j], z ? v16i{} : shi[i][j], 0, 0, 0);
-                    }
-            }
-        }
-    };
-
-    dma(0, buf0, rec0);
-    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-    __syncthreads();
-#pragma unroll 1
-    for (int sb = 0; sb < nsb; sb++) {
-        // everything the super-block needs from its record is read into registers before any DMA of the
-        // super-block is issued: the record's buffer is refilled during the odd stage
-        const uint8_t* rec = (sb & 1) ? rec1 : rec0;
-        uint4 hd[TN];
-#pragma unroll
-        for (int j = 0; j < TN; j++) hd[j] = *reinterpret_cast<const uint4*>(rec + C::HDR + ((wn * TN + j) * 32 + r32) * 16);
-        v4i xsv[TM][2];
-        v4f dxq[TM][4];
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int tr = wm * TM + i;
-            const int32_t* xsr = reinterpret_cast<const int32_t*>(rec + C::XS) + (tr * 32 + r32) * 8;
-            xsv[i][0] = *reinterpret_cast<const v4i*>(xsr);
-            xsv[i][1] = *reinterpret_cast<const v4i*>(xsr + 4);
-            // accumulator register r holds row (r % 4) + 8 (r / 4) + 4 (lane / 32)
-            const float* dxp = reinterpret_cast<const float*>(rec + C::DX) + tr * 32 + half * 4;
-#pragma unroll
-            for (int q = 0; q < 4; q++) dxq[i][q] = *reinterpret_cast<const v4f*>(dxp + 8 * q);
-        }
-        // even stage: fetch the odd one
-        dma(2 * sb + 1, buf1, nullptr);
-        stage(buf0, hd, 0);
-        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-        __syncthreads();
-        // odd stage: fetch the next super-block's even stage and record
-        if (sb + 1 < nsb) dma(2 * sb + 2, buf0, (sb & 1) ? rec0 : rec1);
-        stage(buf1, hd, 1);
-        // the super-block's rescale: mins by MFMA, then acc += dx (d S - dmin mins)
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            v8h xo;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                // bsum = 64 hi + lo, hi in [-64, 63], lo in [0, 63]: both exact in f16
-                xo[e] = (_Float16)(float)(half ? (xsv[i][0][e] & 63) : (xsv[i][0][e] >> 6));
-                xo[4 + e] = (_Float16)(float)(half ? (xsv[i][1][e] & 63) : (xsv[i][1][e] >> 6));
-            }
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                v8h mo;
-#pragma unroll
-                for (int pj = 0; pj < 4; pj++) {
-                    uint32_t sc2, m2;
-                    kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, pj, sc2, m2);
-                    const uint32_t f = half ? 1u : 64u;
-                    mo[2 * pj] = (_Float16)(float)(f * (m2 & 0xffu));
-                    mo[2 * pj + 1] = (_Float16)(float)(f * (m2 >> 8));
-                }
-                const float d = kf_h2f(hd[j].x & 0xffffu), dmin = kf_h2f(hd[j].x >> 16);
-                const v16f mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo, v16f{}, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int s = slo[i][j][r] + (shi[i][j][r] << 3);  // |S| < 2^25: exact
-                    const float t = fmaf(-dmin, mins[r], d * (float)s);
-                    acc[i][j][r] = fmaf(t, dxq[i][r >> 2][r & 3], acc[i][j][r]);
-                }
-            }
-        }
-        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + (wn * TN + j) * 32 + r32;
-            if (n >= N) continue;
-            const float bn = bias ? bias[n] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
-                if (m >= M) continue;
-                const int64_t o = (int64_t)m * N + n;
-                y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
-            }
-        }
-}
-
-template <int WM, int WN, int TM, int TN>
-hipError_t gemm_q4k_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
-                               const float* bias, const float* res, float* y, int M, int N, int K, hipStream_t s) {
-    using C = GdCfg<WM, WN, TM, TN>;
-    auto* fn = gemm_q4k_dma_kernel<WM, WN, TM, TN>;
-    static_assert(C::TOTAL <= 65536, "static LDS");
-    dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
-    fn<<<grid, C::THREADS, 0, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, M, N, K);
-    return hipGetLastError();
-}
-
 // ----------------------------------------------------------------------------------- q8_0 prefill GEMM, DMA staging
 // The product of gemm_q8_0_kernel (per group and 32 x 32 tile: the exact int32 dots I_g from v_mfma_i32_32x32x32_i8,
 // the outer product d_x (x) d_w of the f16 scales from one v_mfma_f32_32x32x16_f16 with a single non-zero k slot,
-// then a convert and an FMA per output) with all staging done by global_load_lds DMA, as in the q4_K GEMM:
+// then a convert and an FMA per output) with all staging done by buffer_load ... lds DMA over buffer resources (per-lane
+// offsets fixed for the K loop, a stage adding a scalar offset), as in the q4_K GEMM:
 //   * activations: [group][32-row tile] 1 KB blocks in MFMA order, one DMA instruction each;
 //   * weights: a stage's four q8_0 blocks of a row are 136 bytes at row offset 136 st, 8-byte aligned; each row's
 //     16-byte aligned 144-byte window around them is copied whole ([row][144] in LDS: nine 16-byte pieces, the
 //     stage's data at offset (136 st) % 16), so the DMA needs only aligned pieces. Rows are 16-byte aligned when
 //     K % 256 == 0, and the last stage (st odd) ends exactly at the row's end;
 //   * activation scales: [row][4] f32 per stage.
-// One buffer is a static LDS array and the other the dynamic one: two distinct objects, so the compiler can tell a DMA
-// into one from reads of the other (36 KB each, above the static limit for both). Eight waves, each a 64 x 32 tile;
+// The two stage buffers (36 KB each) are distinct static LDS arrays, so the compiler can tell a DMA into one from
+// reads of the other. Eight waves, each a 64 x 32 tile;
 // blocks in XCD order. Wave tiles of 2 x 2 measured slower (their 128 x 256 block halves the blocks per CU).
 // gemm_q8_0_kernel (register staging) remains for K % 256 != 0.
 template <int WM, int WN, int TM, int TN>
@@ -728,7 +520,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
                                                                      float* __restrict__ y, int M, int N, int K) {
     using C = GqCfg<WM, WN, TM, TN>;
     __shared__ __align__(16) uint8_t buf0[C::STAGE];
-    extern __shared__ __align__(16) uint8_t buf1[];
+    __shared__ __align__(16) uint8_t buf1[C::STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
@@ -739,21 +531,41 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
     const int nst = K / GM_BK;
     const int half = lane >> 5, r32 = lane & 31;
 
+    // DMA sources: buffer resources over the tile's first rows; per-lane offsets fixed for the K loop, a stage adds
+    // only a scalar offset (rows past M or N are clamped to the last one)
+    const auto rw = kf_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
+    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
+    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    constexpr int IA = (C::NA + C::W - 1) / C::W, IB = (C::NB + C::W - 1) / C::W, ID = (C::ND + C::W - 1) / C::W;
+    int va[IA], vb[IB], vd[ID];
+#pragma unroll
+    for (int it = 0; it < IA; it++) {
+        const int q = wave + it * C::W, g = q / C::MT, t = q % C::MT;
+        va[it] = (min(m0 + t * 32 + r32, M - 1) - m0) * K + g * 32 + half * 16;
+    }
+#pragma unroll
+    for (int it = 0; it < IB; it++) {
+        const int p = (wave + it * C::W) * 64 + lane, r = p / 9, pc = p - 9 * r;
+        vb[it] = (min(n0 + r, N - 1) - n0) * (int)row_bytes + 16 * pc;
+    }
+#pragma unroll
+    for (int it = 0; it < ID; it++) vd[it] = (min(m0 + (wave + it * C::W) * 64 + lane, M - 1) - m0) * kg * 4;
     auto dma = [&](int st, uint8_t* buf) {
-        for (int q = wave; q < C::NA; q += C::W) {
-            const int g = q / C::MT, t = q % C::MT;
-            const int m = min(m0 + t * 32 + r32, M - 1);
-            kf_dma16(xq + (int64_t)m * K + st * GM_BK + g * 32 + half * 16, buf + q * 1024);
+#pragma unroll
+        for (int it = 0; it < IA; it++) {
+            const int q = wave + it * C::W;
+            if (C::NA % C::W == 0 || q < C::NA) kf_bdma16(rx, va[it], st * GM_BK, buf + q * 1024);
         }
-        const int64_t wbase = (int64_t)(136 * st) & ~(int64_t)15;
-        for (int q = wave; q < C::NB; q += C::W) {
-            const int p = q * 64 + lane, r = p / 9, pc = p - 9 * r;
-            const int n = min(n0 + r, N - 1);
-            kf_dma16(w + (int64_t)n * row_bytes + wbase + 16 * pc, buf + C::B_OFF + q * 1024);
+        const int wbase = (136 * st) & ~15;
+#pragma unroll
+        for (int it = 0; it < IB; it++) {
+            const int q = wave + it * C::W;
+            if (C::NB % C::W == 0 || q < C::NB) kf_bdma16(rw, vb[it], wbase, buf + C::B_OFF + q * 1024);
         }
-        for (int q = wave; q < C::ND; q += C::W) {
-            const int m = min(m0 + q * 64 + lane, M - 1);
-            kf_dma16(xd32 + (int64_t)m * kg + st * GM_G, buf + C::D_OFF + q * 1024);
+#pragma unroll
+        for (int it = 0; it < ID; it++) {
+            const int q = wave + it * C::W;
+            if (q < C::ND) kf_bdma16(rd, vd[it], st * GM_G * 4, buf + C::D_OFF + q * 1024);
         }
     };
 
@@ -841,15 +653,245 @@ template <int WM, int WN, int TM, int TN>
 hipError_t gemm_q8_0_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
                                 float* y, int M, int N, int K, hipStream_t s) {
     using C = GqCfg<WM, WN, TM, TN>;
-    auto* fn = gemm_q8_0_dma_kernel<WM, WN, TM, TN>;
-    static bool lds_set = false;
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, C::STAGE);
-        if (e != hipSuccess) return e;
-        lds_set = true;
-    }
     dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
-    fn<<<grid, C::THREADS, C::STAGE, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    gemm_q8_0_dma_kernel<WM, WN, TM, TN><<<grid, C::THREADS, 0, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
+}
+
+// LDS stage of the q4_K GEMM: one super-block of the block tile's activations, nibbles and record
+template <int WM, int WN, int TM, int TN>
+struct GbCfg {
+    static constexpr int W = WM * WN, THREADS = 64 * W;
+    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
+    static constexpr int MT = BM / 32, NT = BN / 32;
+    static constexpr int A_BYTES = MT * 8 * 1024;          // [group][32-row tile] 1 KB operand blocks
+    static constexpr int B_OFF = A_BYTES, B_BYTES = 4 * NT * 1024;  // [pair][32-row tile] raw nibble blocks
+    static constexpr int HDR = B_OFF + B_BYTES, NH = (BN + 63) / 64;
+    static constexpr int DX = HDR + NH * 1024, ND = (BM + 63) / 64;
+    static constexpr int XS = DX + ND * 256, NX = MT;
+    static constexpr int STAGE = XS + NX * 1024;
+    static constexpr int NA = MT * 8, NB = 4 * NT;
+};
+
+template <int WM, int WN, int TM, int TN>
+__global__ void __launch_bounds__(64 * WM * WN, 1) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
+                                                                   const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
+                                                                   const float* __restrict__ xd32, const float* __restrict__ bias,
+                                                                   const float* __restrict__ res, float* __restrict__ y, int M, int N,
+                                                                   int K) {
+    using C = GbCfg<WM, WN, TM, TN>;
+    __shared__ __align__(16) uint8_t buf0[C::STAGE];
+    __shared__ __align__(16) uint8_t buf1[C::STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WN, wn = wave % WN;
+    int tm, tn;
+    gm_tile((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM, tm, tn);
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int kg = K >> 5;
+    const int nsb = K / KF_Q4_K_BLOCK;
+    const int half = lane >> 5, r32 = lane & 31;
+
+    // DMA sources: buffer resources over the tile's first rows; the per-lane offsets are fixed for the whole K loop
+    // and a super-block only adds a wave-uniform offset (rows past M or N are clamped to the last one)
+    const auto rw = kf_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
+    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
+    const auto rs = kf_rsrc(xs32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    constexpr int IA = (C::NA + C::W - 1) / C::W, IB = (C::NB + C::W - 1) / C::W;
+    constexpr int NR = C::NH + C::ND + C::NX, IR = (NR + C::W - 1) / C::W;
+    int va[IA], vb[IB], vr[IR];
+#pragma unroll
+    for (int it = 0; it < IA; it++) {
+        const int q = wave + it * C::W, g = q / C::MT, t = q % C::MT;
+        va[it] = (min(m0 + t * 32 + r32, M - 1) - m0) * K + g * 32 + half * 16;
+    }
+#pragma unroll
+    for (int it = 0; it < IB; it++) {
+        const int q = wave + it * C::W, p = q / C::NT, t = q % C::NT;
+        vb[it] = (min(n0 + t * 32 + r32, N - 1) - n0) * (int)row_bytes + 16 + 32 * p + half * 16;
+    }
+#pragma unroll
+    for (int it = 0; it < IR; it++) {
+        const int q = wave + it * C::W;
+        if (q < C::NH) {
+            vr[it] = (min(n0 + q * 64 + lane, N - 1) - n0) * (int)row_bytes;
+        } else if (q < C::NH + C::ND) {
+            vr[it] = (min(m0 + (q - C::NH) * 64 + lane, M - 1) - m0) * kg * 4;
+        } else {
+            const int qq = q - C::NH - C::ND;
+            vr[it] = (min(m0 + qq * 32 + (lane >> 1), M - 1) - m0) * kg * 4 + (lane & 1) * 16;
+        }
+    }
+    auto dma = [&](int sb, uint8_t* buf) {
+#pragma unroll
+        for (int it = 0; it < IA; it++) {
+            const int q = wave + it * C::W;
+            if (C::NA % C::W == 0 || q < C::NA) kf_bdma16(rx, va[it], sb * KF_Q4_K_BLOCK, buf + q * 1024);
+        }
+#pragma unroll
+        for (int it = 0; it < IB; it++) {
+            const int q = wave + it * C::W;
+            if (C::NB % C::W == 0 || q < C::NB) kf_bdma16(rw, vb[it], sb * KF_Q4_K_BYTES, buf + C::B_OFF + q * 1024);
+        }
+#pragma unroll
+        for (int it = 0; it < IR; it++) {
+            const int q = wave + it * C::W;
+            if (q < C::NH) {
+                kf_bdma16(rw, vr[it], sb * KF_Q4_K_BYTES, buf + C::HDR + q * 1024);
+            } else if (q < C::NH + C::ND) {
+                kf_bdma4(rd, vr[it], sb * 32, buf + C::DX + (q - C::NH) * 256);
+            } else if (q < NR) {
+                kf_bdma16(rs, vr[it], sb * 32, buf + C::XS + (q - C::NH - C::ND) * 1024);
+            }
+        }
+    };
+
+    v16f acc[TM][TN];
+    v16i slo[TM][TN], shi[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
+
+    // the record of the super-block being rescaled, read from its stage buffer after the MFMAs
+    uint4 hd[TN];
+    v4i xsv[TM][2];
+    v4f dxq[TM][4];
+
+    auto mfma_phase = [&](const uint8_t* buf) {
+#pragma unroll
+        for (int j = 0; j < TN; j++) hd[j] = *reinterpret_cast<const uint4*>(buf + C::HDR + ((wn * TN + j) * 32 + r32) * 16);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            v4i bl[2][TN], bh[2][TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(buf + C::B_OFF + ((p * C::NT + wn * TN + j) * 64 + lane) * 16);
+                uint32_t sc2, m2;
+                kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, p, sc2, m2);
+                const uint32_t s0 = sc2 & 0xffu, s1 = sc2 >> 8;
+                const uint32_t l0 = s0 & 7u, u0 = s0 >> 3, l1 = s1 & 7u, u1 = s1 >> 3;
+                const uint32_t m4 = 0x0f0f0f0fu;
+                const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t lo = v[e] & m4, hi = (v[e] >> 4) & m4;
+                    bl[0][j][e] = (int)gs_pmul(lo, l0);
+                    bh[0][j][e] = (int)gs_pmul(lo, u0);
+                    bl[1][j][e] = (int)gs_pmul(hi, l1);
+                    bh[1][j][e] = (int)gs_pmul(hi, u1);
+                }
+            }
+#pragma unroll
+            for (int gg = 0; gg < 2; gg++) {
+                const int g = 2 * p + gg;
+                v4i a[TM];
+#pragma unroll
+                for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const v4i*>(buf + ((g * C::MT + wm * TM + i) * 64 + lane) * 16);
+#pragma unroll
+                for (int i = 0; i < TM; i++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++) {
+                        const bool z = g == 0;
+                        slo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bl[gg][j], z ? v16i{} : slo[i][j], 0, 0, 0);
+                        shi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bh[gg][j], z ? v16i{} : shi[i][j], 0, 0, 0);
+                    }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int tr = wm * TM + i;
+            const int32_t* xsr = reinterpret_cast<const int32_t*>(buf + C::XS) + (tr * 32 + r32) * 8;
+            xsv[i][0] = *reinterpret_cast<const v4i*>(xsr);
+            xsv[i][1] = *reinterpret_cast<const v4i*>(xsr + 4);
+            // accumulator register r holds row (r % 4) + 8 (r / 4) + 4 (lane / 32)
+            const float* dxp = reinterpret_cast<const float*>(buf + C::DX) + tr * 32 + half * 4;
+#pragma unroll
+            for (int q = 0; q < 4; q++) dxq[i][q] = *reinterpret_cast<const v4f*>(dxp + 8 * q);
+        }
+    };
+
+    // the super-block's rescale: mins by MFMA, then acc += dx (d S - dmin mins)
+    auto rescale = [&]() {
+        v8h mo[TN];
+        float dd[TN], dm[TN];
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+#pragma unroll
+            for (int pj = 0; pj < 4; pj++) {
+                uint32_t sc2, m2;
+                kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, pj, sc2, m2);
+                const uint32_t f = half ? 1u : 64u;
+                mo[j][2 * pj] = (_Float16)(float)(f * (m2 & 0xffu));
+                mo[j][2 * pj + 1] = (_Float16)(float)(f * (m2 >> 8));
+            }
+            dd[j] = kf_h2f(hd[j].x & 0xffffu);
+            dm[j] = kf_h2f(hd[j].x >> 16);
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            v8h xo;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                // bsum = 64 hi + lo, hi in [-64, 63], lo in [0, 63]: both exact in f16
+                xo[e] = (_Float16)(float)(half ? (xsv[i][0][e] & 63) : (xsv[i][0][e] >> 6));
+                xo[4 + e] = (_Float16)(float)(half ? (xsv[i][1][e] & 63) : (xsv[i][1][e] >> 6));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const v16f mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo[j], v16f{}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int s = slo[i][j][r] + (shi[i][j][r] << 3);  // |S| < 2^25: exact
+                    const float t = fmaf(-dm[j], mins[r], dd[j] * (float)s);
+                    acc[i][j][r] = fmaf(t, dxq[i][r >> 2][r & 3], acc[i][j][r]);
+                }
+            }
+        }
+    };
+
+    auto stage = [&](int sb, const uint8_t* cur, uint8_t* nxt) {
+        if (sb + 1 < nsb) dma(sb + 1, nxt);
+        mfma_phase(cur);
+        rescale();
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+    };
+
+    dma(0, buf0);
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+    __syncthreads();
+#pragma unroll 1
+    for (int sb = 0; sb < nsb; sb += 2) {
+        stage(sb, buf0, buf1);
+        if (sb + 1 < nsb) stage(sb + 1, buf1, buf0);
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            const int n = n0 + (wn * TN + j) * 32 + r32;
+            if (n >= N) continue;
+            const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
+            }
+        }
+}
+
+template <int WM, int WN, int TM, int TN>
+hipError_t gemm_q4k_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
+                              const float* bias, const float* res, float* y, int M, int N, int K, hipStream_t s) {
+    using C = GbCfg<WM, WN, TM, TN>;
+    static_assert(2 * C::STAGE <= 160 * 1024, "LDS");
+    dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
+    gemm_q4k_kernel<WM, WN, TM, TN><<<grid, C::THREADS, 0, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, M, N, K);
     return hipGetLastError();
 }
 
@@ -927,7 +969,9 @@ hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act,
                               int N, int K, hipStream_t s) {
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
     const char* base = static_cast<const char*>(act);
-    return gemm_q4k_dma_launch<2, 4, 2, 1>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
-                                           reinterpret_cast<const int32_t*>(base + o.s32), reinterpret_cast<const float*>(base + o.d32), bias,
-                                           res, y, M, N, K, s);
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
+    const auto* xs = reinterpret_cast<const int32_t*>(base + o.s32);
+    const auto* xd = reinterpret_cast<const float*>(base + o.d32);
+    return gemm_q4k_launch<2, 4, 2, 1>(wb, row_bytes, xq, xs, xd, bias, res, y, M, N, K, s);
 }

@@ -94,3 +94,20 @@ __device__ __forceinline__ void kf_dma16(const void* src, void* lds_base) {
 __device__ __forceinline__ void kf_dma4(const void* src, void* lds_base) {
     __builtin_amdgcn_global_load_lds((kf_gbl_void*)src, (kf_lds_void*)lds_base, 4, 0, 0);
 }
+
+// Raw buffer resource over [base, base + bytes) (stride 0, 32-bit data format word as gfx9 raw buffers need it).
+// Loads through it take a per-lane 32-bit byte offset in a VGPR plus a wave-uniform one in an SGPR, so a loop that
+// advances all lanes by the same amount pays no vector address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kf_rsrc(const void* base, uint64_t bytes) {
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+
+// buffer_load_dwordx4 / _dword ... lds: lane l writes its 16 (4) bytes read at voff + soff to lds_base + 16 l (4 l).
+__device__ __forceinline__ void kf_bdma16(__amdgpu_buffer_rsrc_t r, int voff, int soff, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (kf_lds_void*)lds_base, 16, voff, soff, 0, 0);
+}
+
+__device__ __forceinline__ void kf_bdma4(__amdgpu_buffer_rsrc_t r, int voff, int soff, void* lds_base) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (kf_lds_void*)lds_base, 4, voff, soff, 0, 0);
+}
