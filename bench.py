@@ -261,6 +261,56 @@ def kquant_section(dev):
     return out
 
 
+def group_section(dev):
+    """Grouped products at the Llama-3-8B shapes, batch 1, Q4_K: Q/K/V (4096, 1024, 1024 rows) and gate/up (14336
+    each) as separate tensors sharing one quantized input. us per layer part for separate launches, one grouped
+    launch (the segment table) and one launch over a pre-stacked copy of the same rows; weight copies rotated past
+    the MALL; GB/s over weight bytes + f32 activations in and out."""
+    import numpy as np
+    import torch
+
+    import kungfu_amd as kf
+
+    ty, n = kf.TYPE_Q4_K, 4096
+    x = torch.from_numpy(kf.synth_normal(1, 1.0, n).reshape(1, n)).to(dev)
+    act = kf.alloc_act(1, n, dev)
+    kf.quant_act(x, act, kf.ACT_Q8K)
+    out = {}
+    for part, sizes in (("qkv", (4096, 1024, 1024)), ("gate_up", (14336, 14336))):
+        total = sum(sizes)
+        wb = kf.row_bytes(ty, n) * total
+        copies = max(2, -(-2 * MALL_BYTES // wb) + 1)
+        stacked = [torch.from_numpy(make_weights(ty, n, total)).to(dev)]
+        stacked += [stacked[0].clone() for _ in range(copies - 1)]
+        rb = kf.row_bytes(ty, n)
+        bounds = np.cumsum((0,) + sizes)
+        # members are views into each stacked copy: the same bytes, addressed as separate tensors
+        members = [[stacked[c][bounds[k] : bounds[k + 1]] for k in range(len(sizes))] for c in range(copies)]
+        ys = [torch.empty((1, m), device=dev) for m in sizes]
+        y_all = torch.empty((1, total), device=dev)
+        nbytes = gemv_bytes(ty, n, total)
+
+        def separate(i):
+            for k, m in enumerate(sizes):
+                kf.gemv(ty, members[i % copies][k], act, ys[k], 1, n, m)
+
+        def grouped(i):
+            kf.gemv_group(ty, [(members[i % copies][k], ys[k], None, None) for k in range(len(sizes))], act, 1, n)
+
+        def one(i):
+            kf.gemv(ty, stacked[i % copies], act, y_all, 1, n, total)
+
+        rec = {}
+        for name, fn in (("separate", separate), ("grouped", grouped), ("stacked", one)):
+            us = time_launches(fn, 100)
+            rec[name] = {"us": round(us, 3), "GBs": round(nbytes / us / 1e3, 1)}
+        rec["launches_separate"] = len(sizes)
+        rec["weight_bytes"] = rb * total
+        out[part] = rec
+        del stacked, members
+    return out
+
+
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_up_traffic.md")
 
 
@@ -322,7 +372,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "fused", "kquant", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -336,7 +386,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "fused": fused_section, "kquant": kquant_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -414,6 +464,7 @@ def main():
     out["moe_q4_k"] = moe_section(dev)
     out["fused_producers"] = fused_section(dev)
     out["k_quants"] = kquant_section(dev)
+    out["grouped"] = group_section(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(shapes, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -129,6 +129,25 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream);
 
+/* Grouped products sharing one input (Q/K/V, or gate and up stored as separate tensors): up to KF_HIP_MAX_SEGMENTS
+ * weight matrices of one type and row width stacked along their output rows. The segment table is the reference's
+ * (quant.cuh:301-305, built by matmul_group_launch, exec.rs:1305-1314), KF_SEG_WORDS int64 words per member in HOST
+ * memory: [0] byte offset of the member's weights from w, [1] of its output from y, [2] of its bias from y or
+ * KF_SEG_NONE, [3] of its residual from y or KF_SEG_NONE, [4] its first stacked row (members in order, no gaps), [5]
+ * its row count. Member k writes y_k [rows][n_out_k]. One activation row of q8_0 / q4_K runs as one GEMV launch over
+ * all stacked rows (the reference's segmented matvec_i8, quant.cuh:447-464); other row counts and types run each
+ * member's product against the shared activations (the reference's per-member fallback, exec.rs:1334-1342). */
+#define KF_HIP_MAX_SEGMENTS 4
+#define KF_SEG_WORDS 6
+#define KF_SEG_NONE (-0x7fffffffffffffffLL - 1)
+int kf_hip_gemv_group(uint32_t ty, const void* w, int64_t row_bytes, const void* act, float* y, int rows, int n, const int64_t* segs,
+                      int nseg, void* stream);
+
+/* kf_hip_matmul for a group: quantize x once, then the grouped product (each member's product chosen by the row
+ * count as kf_hip_matmul chooses it). Replaces matmul_group_launch (exec.rs:1283-1346). */
+int kf_hip_matmul_group(uint32_t ty, const void* w, int n_in, const float* x, int rows, void* act, float* y, const int64_t* segs, int nseg,
+                        void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * MoE grouped experts (Op::MoeFfn with routed pairs: rows x n_used pairs rj = r * n_used + j, slot sel[rj] < 0 =
  * unused). Expert matrices are stacked: expert e's rows start at base + e * expert_bytes.

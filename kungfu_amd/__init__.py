@@ -72,6 +72,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_gated_act_q8": ([P, P, I, I, I, I, I, P, P], I),
         "kf_hip_gemv": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_matmul": ([U, P, I, I, P, I, P, P, P, P, P], I),
+        "kf_hip_gemv_group": ([U, P, L64, P, P, I, I, P, I, P], I),
+        "kf_hip_matmul_group": ([U, P, I, P, I, P, P, P, I, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
         "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_moe_group": ([P, I, I, P, P, P], I),
@@ -220,6 +222,38 @@ def gemm_i8(ty: int, w, act, y, rows: int, n: int, n_out: int, bias=None, res=No
 def matmul(ty: int, w, x, act, y, n_out: int, bias=None, res=None, stream=None) -> None:
     rows, n = x.shape
     check(lib().kf_hip_matmul(ty, _ptr(w), n, n_out, _ptr(x), rows, _ptr(act), _ptr(bias), _ptr(res), _ptr(y), _stream(stream)))
+
+
+SEG_NONE = -(1 << 63)
+MAX_SEGMENTS = 4
+
+
+def segment_table(members):
+    """The reference's segment words (six int64 per member, offsets from the first member's weights and output) for
+    members given as (w, y, bias, res) device tensors, bias/res None or a tensor. Returns (words, lead w, lead y)."""
+    import numpy as np
+
+    lead_w, lead_y = _ptr(members[0][0]), _ptr(members[0][1])
+    words, start = [], 0
+    for w, y, bias, res in members:
+        n_out = y.shape[-1]
+        off = lambda t: SEG_NONE if t is None else _ptr(t) - lead_y
+        words += [_ptr(w) - lead_w, _ptr(y) - lead_y, off(bias), off(res), start, n_out]
+        start += n_out
+    return np.asarray(words, dtype=np.int64), lead_w, lead_y
+
+
+def gemv_group(ty: int, members, act, rows: int, n: int, stream=None) -> None:
+    """Grouped product of members (w, y, bias, res) sharing the quantized activations act (kf_hip_gemv_group)."""
+    words, lw, ly = segment_table(members)
+    check(lib().kf_hip_gemv_group(ty, lw, row_bytes(ty, n), _ptr(act), ly, rows, n, words.ctypes.data, len(members), _stream(stream)))
+
+
+def matmul_group(ty: int, members, x, act, stream=None) -> None:
+    """Grouped Op::MatMul of members (w, y, bias, res) on one f32 input x [rows][n] (kf_hip_matmul_group)."""
+    rows, n = x.shape
+    words, lw, ly = segment_table(members)
+    check(lib().kf_hip_matmul_group(ty, lw, n, _ptr(x), rows, _ptr(act), ly, words.ctypes.data, len(members), _stream(stream)))
 
 
 def block_ints(ty: int, w, act, out, rows: int, n: int, n_out: int, stream=None) -> None:

@@ -14,6 +14,8 @@
 #include "../../include/kf_hip.h"
 #include "kf_layout.h"
 
+static_assert(KF_HIP_MAX_SEGMENTS == KF_MAX_SEGS, "one segment limit");
+
 // Launchers in the .hip translation units
 hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s);
 hipError_t kf_launch_gemv_k(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
@@ -23,7 +25,7 @@ hipError_t kf_launch_rms_norm_q8(const float* x, const float* w, const float* b,
 hipError_t kf_launch_gated_act_q8(const float* gate, const float* up, int stride, int act_fn, void* act, int rows, int n, int kind,
                                   hipStream_t s);
 hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
-                           const float* bias, const float* res, float* y, int n, int n_out, int maxit, hipStream_t s);
+                           const float* bias, const float* res, float* y, int n, int n_out, int maxit, const KfSegs* segs, hipStream_t s);
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
                                 int32_t* out, hipStream_t s);
 int kf_gemv_max_n();
@@ -96,6 +98,9 @@ int gemv_maxit() {
     const int v = e ? atoi(e) : 0;
     return v < 0 ? 0 : v;
 }
+
+int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float* bias, const float* res, float* y, int rows, int n_in,
+            int n_out, void* stream);
 
 int check_product(uint32_t ty, const void* w, int64_t row_bytes, const void* act, float* y, int rows, int n, int n_out) {
     int block, bytes;
@@ -203,7 +208,7 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
         const int32_t* xs32 = reinterpret_cast<const int32_t*>(base + o.s32) + (size_t)r * (n / 32);
         const float* xd32 = reinterpret_cast<const float*>(base + o.d32) + (size_t)r * (n / 32);
         const hipError_t e = kf_launch_gemv1(ty, w, row_bytes, xq, xs32, xd32, bias, res ? res + (size_t)r * n_out : nullptr,
-                                             y + (size_t)r * n_out, n, n_out, gemv_maxit(), s);
+                                             y + (size_t)r * n_out, n, n_out, gemv_maxit(), nullptr, s);
         if (e != hipSuccess) return hip_fail(e, "gemv launch");
     }
     return KF_OK;
@@ -233,6 +238,16 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
     if (rc != KF_OK) return rc;
     const int q = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
     if (q != KF_OK) return q;
+    return product(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The product of kf_hip_matmul once the activations are quantized
+int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float* bias, const float* res, float* y, int rows, int n_in,
+            int n_out, void* stream) {
     // the row count picks the product, as matvec_rows / multi_kind do (exec.rs:1877-1945): one row is the GEMV;
     // several q8_0 rows are the int8 GEMM, which reads each weight byte once per 128 rows
     if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
@@ -245,6 +260,105 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
         if (rows >= 128 || (rows >= 32 && blocks >= 96)) return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     }
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+}
+
+// A grouped product's members from the reference's segment words (quant.cuh:301-305): per member the byte offsets of
+// its weights from w and of its output, bias and residual from y (KF_SEG_NONE: none), its first stacked row and its
+// row count. Members must be stacked in order without gaps.
+struct Member {
+    const uint8_t* w;
+    float* y;
+    const float* bias;
+    const float* res;
+    int start, n_out;
+};
+
+int unpack_segs(const void* w, float* y, const int64_t* segs, int nseg, std::vector<Member>& out, int& total) {
+    if (!segs || nseg < 1 || nseg > KF_MAX_SEGS) return fail(KF_E_INVALID, "%d segments (1 to %d, non-null table)", nseg, KF_MAX_SEGS);
+    if (!w || !y) return fail(KF_E_INVALID, "null leader weight or output pointer");
+    out.clear();
+    total = 0;
+    char* yb = reinterpret_cast<char*>(y);
+    for (int i = 0; i < nseg; i++) {
+        const int64_t* e = segs + (size_t)i * KF_SEG_WORDS;
+        if (e[0] == KF_SEG_NONE || e[1] == KF_SEG_NONE) return fail(KF_E_INVALID, "segment %d has no weights or output", i);
+        if (e[4] != total) return fail(KF_E_INVALID, "segment %d starts at row %lld, want %d (members stacked in order)", i, (long long)e[4], total);
+        if (e[5] < 1 || e[5] > (int64_t)0x7fffffff - total) return fail(KF_E_INVALID, "segment %d has %lld rows", i, (long long)e[5]);
+        Member m;
+        m.w = static_cast<const uint8_t*>(w) + e[0];
+        m.y = reinterpret_cast<float*>(yb + e[1]);
+        m.bias = e[2] == KF_SEG_NONE ? nullptr : reinterpret_cast<const float*>(yb + e[2]);
+        m.res = e[3] == KF_SEG_NONE ? nullptr : reinterpret_cast<const float*>(yb + e[3]);
+        m.start = total;
+        m.n_out = (int)e[5];
+        if (!aligned(m.w, 16)) return fail(KF_E_INVALID, "segment %d weights must be 16-byte aligned", i);
+        if (!aligned(m.y, 4) || (m.bias && !aligned(m.bias, 4)) || (m.res && !aligned(m.res, 4)))
+            return fail(KF_E_INVALID, "segment %d output, bias or residual not 4-byte aligned", i);
+        total += m.n_out;
+        out.push_back(m);
+    }
+    return KF_OK;
+}
+
+// The grouped product over quantized activations: one GEMV launch over the stacked rows for one activation row of
+// q8_0 / q4_K, otherwise each member's product against the shared activations
+int group_product(uint32_t ty, const std::vector<Member>& ms, int64_t rb, const void* act, int rows, int n, int total, bool select,
+                  void* stream) {
+    if (rows == 1 && (ty == KF_TYPE_Q8_0 || ty == KF_TYPE_Q4_K) && n <= kf_gemv_max_n()) {
+        KfSegs sg{};
+        sg.n = (int)ms.size();
+        for (size_t i = 0; i < ms.size(); i++) {
+            sg.start[i] = ms[i].start;
+            sg.w[i] = ms[i].w;
+            sg.y[i] = ms[i].y;
+            sg.bias[i] = ms[i].bias;
+            sg.res[i] = ms[i].res;
+        }
+        const kf_act_offsets o = kf_act_layout(1, (size_t)n);
+        const char* base = static_cast<const char*>(act);
+        const hipError_t e = kf_launch_gemv1(ty, ms[0].w, rb, reinterpret_cast<const int8_t*>(base + o.q), reinterpret_cast<const int32_t*>(base + o.s32),
+                                             reinterpret_cast<const float*>(base + o.d32), nullptr, nullptr, ms[0].y, n, total, gemv_maxit(), &sg,
+                                             static_cast<hipStream_t>(stream));
+        return e == hipSuccess ? KF_OK : hip_fail(e, "grouped gemv launch");
+    }
+    for (const Member& m : ms) {
+        const int rc = select ? product(ty, m.w, rb, act, m.bias, m.res, m.y, rows, n, m.n_out, stream)
+                              : kf_hip_gemv(ty, m.w, rb, act, m.bias, m.res, m.y, rows, n, m.n_out, stream);
+        if (rc != KF_OK) return rc;
+    }
+    return KF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kf_hip_gemv_group(uint32_t ty, const void* w, int64_t row_bytes, const void* act, float* y, int rows, int n, const int64_t* segs, int nseg,
+                      void* stream) {
+    std::vector<Member> ms;
+    int total = 0;
+    int rc = unpack_segs(w, y, segs, nseg, ms, total);
+    if (rc != KF_OK) return rc;
+    rc = check_product(ty, w, row_bytes, act, y, rows, n, total);
+    if (rc != KF_OK) return rc;
+    return group_product(ty, ms, row_bytes, act, rows, n, total, false, stream);
+}
+
+int kf_hip_matmul_group(uint32_t ty, const void* w, int n_in, const float* x, int rows, void* act, float* y, const int64_t* segs, int nseg,
+                        void* stream) {
+    int block, bytes;
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12, q5_K=13, q6_K=14)", ty);
+    if (n_in <= 0 || n_in % block != 0) return fail(KF_E_INVALID, "%d columns against blocks of %d", n_in, block);
+    const int64_t rb = (int64_t)(n_in / block) * bytes;
+    std::vector<Member> ms;
+    int total = 0;
+    int rc = unpack_segs(w, y, segs, nseg, ms, total);
+    if (rc != KF_OK) return rc;
+    rc = check_product(ty, w, rb, act, y, rows, n_in, total);
+    if (rc != KF_OK) return rc;
+    rc = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
+    if (rc != KF_OK) return rc;
+    return group_product(ty, ms, rb, act, rows, n_in, total, true, stream);
 }
 
 int kf_hip_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, void* stream) {

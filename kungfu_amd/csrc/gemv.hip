@@ -89,6 +89,37 @@ struct GvStage {
     float scale[GV_SC];
 };
 
+// Stacked row o of a grouped product (KfSegs; sg.n == 0: the single matrix w). The member is picked by unrolled
+// selects on constant indices, so the table stays in kernel arguments (scalar registers when o is wave-uniform).
+struct GvRow {
+    const uint8_t* w;
+    float* y;
+    const float* bias;
+    const float* res;
+    int o;  // the row within its member
+};
+
+__device__ __forceinline__ GvRow gv_row(const KfSegs& sg, const uint8_t* w, float* y, const float* bias, const float* res, int o) {
+    GvRow r{w, y, bias, res, o};
+    if (sg.n > 0) {
+        r = GvRow{sg.w[0], sg.y[0], sg.bias[0], sg.res[0], o};
+#pragma unroll
+        for (int k = 1; k < KF_MAX_SEGS; k++)
+            if (k < sg.n && o >= sg.start[k]) r = GvRow{sg.w[k], sg.y[k], sg.bias[k], sg.res[k], o - sg.start[k]};
+    }
+    return r;
+}
+
+__device__ __forceinline__ const uint8_t* gv_row_ptr(const KfSegs& sg, const uint8_t* w, int64_t row_bytes, int o) {
+    const GvRow r = gv_row(sg, w, nullptr, nullptr, nullptr, o);
+    return r.w + (int64_t)r.o * row_bytes;
+}
+
+__device__ __forceinline__ void gv_store(const KfSegs& sg, float* y, const float* bias, const float* res, int o, float acc) {
+    const GvRow r = gv_row(sg, nullptr, y, bias, res, o);
+    r.y[r.o] = acc + (r.bias ? r.bias[r.o] : 0.0f) + (r.res ? r.res[r.o] : 0.0f);
+}
+
 template <uint32_t TY>
 __device__ __forceinline__ void gv_stage_load(GvStage& st, const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
                                               const float* __restrict__ xd32, int n) {
@@ -200,7 +231,7 @@ template <uint32_t TY, int SPW, int WPR, int MAXIT>
 __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                           const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                           const float* __restrict__ bias, const float* __restrict__ res,
-                                                          float* __restrict__ y, int n, int n_out, int iters) {
+                                                          float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
@@ -236,7 +267,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
     for (int it = 0; it < MAXIT; it++) {
         // unpredicated: an iteration or step past the end reloads a valid row or step whose result is never used
         const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
-        const uint8_t* row = w + (int64_t)o * row_bytes;
+        const uint8_t* row = gv_row_ptr(sg, w, row_bytes, o);
 #pragma unroll
         for (int i = 0; i < SPW; i++) {
             const int64_t at = min((int64_t)(sp + i * WPR), last_step) * STEP;
@@ -274,7 +305,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
             }
             acc = kf_wave_sum_dpp(acc);
             if (ln.lane == 0) {
-                if (WPR == 1) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+                if (WPR == 1) gv_store(sg, y, bias, res, o, acc);
                 else part[it * GV_WAVES + wave] = acc;
             }
         }
@@ -288,7 +319,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
             float acc = 0.0f;
 #pragma unroll
             for (int q = 0; q < WPR; q++) acc += part[it * GV_WAVES + g * WPR + q];
-            y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+            gv_store(sg, y, bias, res, o, acc);
         }
     }
 }
@@ -336,7 +367,7 @@ template <uint32_t TY, int SPW, int WPR, int MAXIT>
 __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                               const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                               const float* __restrict__ bias, const float* __restrict__ res,
-                                                              float* __restrict__ y, int n, int n_out, int iters) {
+                                                              float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
@@ -385,7 +416,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
 #pragma unroll
     for (int it = 0; it < MAXIT; it++) {
         const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
-        const uint8_t* row = w + (int64_t)o * row_bytes;
+        const uint8_t* row = gv_row_ptr(sg, w, row_bytes, o);
 #pragma unroll
         for (int i = 0; i < SPW; i++) {
             const int64_t at = min((int64_t)(sp + i * WPR), last_step) * STEP;
@@ -428,7 +459,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
             }
             acc = kf_wave_sum_dpp(acc);
             if (lane == 0) {
-                if (WPR == 1) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+                if (WPR == 1) gv_store(sg, y, bias, res, o, acc);
                 else part[it * GV_WAVES + wave] = acc;
             }
         }
@@ -443,7 +474,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
             float acc = 0.0f;
 #pragma unroll
             for (int q = 0; q < WPR; q++) acc += part[it * GV_WAVES + g * WPR + q];
-            y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+            gv_store(sg, y, bias, res, o, acc);
         }
     }
 }
@@ -457,7 +488,7 @@ template <uint32_t TY, int WPR, int D>
 __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                                const float* __restrict__ bias, const float* __restrict__ res,
-                                                               float* __restrict__ y, int n, int n_out, int iters) {
+                                                               float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;
@@ -535,7 +566,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     if (iw == 0) iw = 1;  // a wave without rows still runs the barrier; it reloads row rg of the block's first group
     auto row_ptr = [&](int it) {
         const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
-        return w + (int64_t)o * row_bytes + at;
+        return gv_row_ptr(sg, w, row_bytes, o) + at;
     };
     auto process = [&](const uint4* v, int it) {
         if (!(KF_GV_ABLATE & 4)) gv_park<TY>(wb, v, len, ln);
@@ -553,7 +584,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         acc = kf_wave_sum_dpp(acc);
         const int o = (it * B + (int)blockIdx.x) * RPB + rg;
         if (lane == 0 && o < n_out) {
-            if (WPR == 1) y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+            if (WPR == 1) gv_store(sg, y, bias, res, o, acc);
             else part[it * GV_WAVES + wave] = acc;
         }
     };
@@ -594,7 +625,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
             float acc = 0.0f;
 #pragma unroll
             for (int q = 0; q < WPR; q++) acc += part[it2 * GV_WAVES + g * WPR + q];
-            y[o] = acc + (bias ? bias[o] : 0.0f) + (res ? res[o] : 0.0f);
+            gv_store(sg, y, bias, res, o, acc);
         }
     }
 }
@@ -690,7 +721,7 @@ int cu_count() {
     return g_cu_count;
 }
 
-typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int);
+typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int, const KfSegs);
 
 // Most blocks of one kernel resident per CU at a dynamic LDS size, cached per (kernel, LDS)
 int resident_blocks(GvKernel k, size_t smem) {
@@ -711,7 +742,7 @@ int resident_blocks(GvKernel k, size_t smem) {
 
 template <uint32_t TY, int SPW, int WPR>
 hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
-                       const float* res, float* y, int n, int n_out, int maxit_env, hipStream_t s) {
+                       const float* res, float* y, int n, int n_out, int maxit_env, const KfSegs& sg, hipStream_t s) {
     constexpr int RPB = GV_WAVES / WPR;
     const int groups = (n_out + RPB - 1) / RPB;
     // row iterations per block: enough blocks that the chip is full, each block's waves holding the loads of all
@@ -726,7 +757,7 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         const size_t smem = gd_lds(TY, n, 1, WPR, 1, 1).total;
         GvKernel k = gemv_dma_kernel<TY, 1, WPR, 1>;
         if (groups <= cu_count() * resident_blocks(k, smem) && smem <= 65536) {
-            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1);
+            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1, sg);
             return hipGetLastError();
         }
     }
@@ -748,7 +779,7 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         const int iters = (groups + grid - 1) / grid;
         const size_t smem = gd_lds(TY, n, iters, WPR, 1, 1).total;
         if (smem <= 65536) {
-            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters);
+            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg);
             return hipGetLastError();
         }
     }
@@ -758,10 +789,10 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         const int iters = (groups + grid - 1) / grid;                                                                    \
         if (dma && gd_lds(TY, n, iters, WPR, M, SPW).total <= 65536) {                                                   \
             const size_t smem = gd_lds(TY, n, iters, WPR, M, SPW).total;                                                 \
-            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters); \
+            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg); \
         } else {                                                                                                         \
             const size_t smem = gv_lds(TY, n, iters, WPR).total;                                                         \
-            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters); \
+            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg); \
         }                                                                                                                \
         return hipGetLastError();                                                                                        \
     }
@@ -789,17 +820,20 @@ extern "C" int kf_gv_set_trace(void* p) { return hipMemcpyToSymbol(HIP_SYMBOL(kf
 int kf_gemv_max_n() { return 32768; }
 
 // Host launcher for one activation row, validated by the caller (api.cpp): n a multiple of the type's block,
-// n <= kf_gemv_max_n(). xq / xs32 / xd32 point at the row's int8 values, per-32 sums and per-32 scales.
+// n <= kf_gemv_max_n(). xq / xs32 / xd32 point at the row's int8 values, per-32 sums and per-32 scales. With segs
+// non-null the n_out rows are the members' rows stacked (KfSegs) and w / y / bias / res are unused.
 hipError_t kf_launch_gemv1(uint32_t ty, const void* wv, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
-                           const float* bias, const float* res, float* y, int n, int n_out, int maxit, hipStream_t s) {
+                           const float* bias, const float* res, float* y, int n, int n_out, int maxit, const KfSegs* segs, hipStream_t s) {
     if (n_out == 0) return hipSuccess;
+    KfSegs sg{};
+    if (segs) sg = *segs;
     const uint8_t* w = static_cast<const uint8_t*>(wv);
     const int steps = ty == KF_TYPE_Q4_K ? (n / 256 + 15) / 16 : (n / 32 + 63) / 64;
     const int wpr = gv_wpr(steps);
     const int spw = (steps + wpr - 1) / wpr;
 #define KF_GV(TY, SPW, WPR)                                                                                      \
     if (ty == TY && spw == SPW && wpr == WPR)                                                                    \
-        return launch_gemv<TY, SPW, WPR>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, maxit, s);
+        return launch_gemv<TY, SPW, WPR>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, maxit, sg, s);
     KF_GV(KF_TYPE_Q4_K, 1, 1)
     KF_GV(KF_TYPE_Q4_K, 1, 2)
     KF_GV(KF_TYPE_Q4_K, 1, 4)

@@ -55,3 +55,17 @@ static inline struct kf_act_offsets kf_act_layout(size_t rows, size_t n) {
     o.total = kf_align_up(o.s32 + rows * (n / 32) * 4, KF_ACT_ALIGN);
     return o;
 }
+
+// Grouped products: up to KF_MAX_SEGS weight matrices with the same type and row width, stacked along the output
+// rows and run against one quantized input. Stacked row o belongs to the last member k with start[k] <= o; its
+// row (o - start[k]) of w[k] is multiplied and written to y[k] (+ bias[k], res[k], either may be null). n == 0 is the
+// plain single product over the launch's own pointers.
+#define KF_MAX_SEGS 4
+struct KfSegs {
+    int n;
+    int start[KF_MAX_SEGS];
+    const uint8_t* w[KF_MAX_SEGS];
+    float* y[KF_MAX_SEGS];
+    const float* bias[KF_MAX_SEGS];
+    const float* res[KF_MAX_SEGS];
+};

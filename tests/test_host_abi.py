@@ -197,3 +197,33 @@ def test_synth_normal_matches_definition_and_golden():
     assert np.array_equal(np.array(gold["bits"], np.uint32), got[:64].view(np.uint32))
     big = kf.synth_normal(1, 0.02, 200000)
     assert abs(big.mean()) < 3e-4 and abs(big.std() - 0.02) < 2e-4
+
+
+def test_group_segment_table_is_validated_on_the_host():
+    """kf_hip_gemv_group / kf_hip_matmul_group reject a bad segment table before any launch."""
+    L = kf.lib()
+    N = kf.SEG_NONE
+
+    def run(words, nseg=None, w=FAKE):
+        a = np.asarray(words, dtype=np.int64)
+        rc = L.kf_hip_gemv_group(kf.TYPE_Q4_K, w, 144, FAKE, FAKE, 1, 256, a.ctypes.data if len(a) else None,
+                                 len(a) // 6 if nseg is None else nseg, None)
+        return rc, L.kf_hip_last_error().decode()
+
+    good = [0, 0, N, N, 0, 16, 144 * 16, 64, N, N, 16, 8]
+    assert run([], 0)[0] == kf.KF_E_INVALID
+    assert run(good * 3, 5)[0] == kf.KF_E_INVALID                         # above four members
+    rc, msg = run([0, 0, N, N, 0, 16, 144 * 16, 64, N, N, 17, 8])          # a gap in the stacking
+    assert rc == kf.KF_E_INVALID and "starts at row 17" in msg
+    rc, msg = run([0, 0, N, N, 0, 16, 8, 64, N, N, 16, 8])                 # member weights not 16-byte aligned
+    assert rc == kf.KF_E_INVALID and "16-byte" in msg
+    rc, msg = run([0, 0, N, N, 0, 16, N, 64, N, N, 16, 8])                 # no weights
+    assert rc == kf.KF_E_INVALID and "no weights" in msg
+    rc, msg = run([0, 0, N, N, 0, 0])                                      # an empty member
+    assert rc == kf.KF_E_INVALID and "0 rows" in msg
+    rc, msg = run([0, 0, 2, N, 0, 16])                                     # a misaligned bias
+    assert rc == kf.KF_E_INVALID and "4-byte" in msg
+    rc = L.kf_hip_matmul_group(kf.TYPE_Q4_K, FAKE, 200, FAKE, 1, FAKE, FAKE, np.asarray(good, np.int64).ctypes.data, 2, None)
+    assert rc == kf.KF_E_INVALID and "200 columns" in L.kf_hip_last_error().decode()
+    rc = L.kf_hip_matmul_group(2, FAKE, 256, FAKE, 1, FAKE, FAKE, np.asarray(good, np.int64).ctypes.data, 2, None)
+    assert rc == kf.KF_E_UNSUPPORTED
