@@ -21,8 +21,12 @@
 
 #include <algorithm>
 
-namespace {
+hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
+                              const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
+                              int per_slot, const float* bias, const float* res, float* y, hipStream_t s);
+bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu);
 
+namespace {
 
 template <uint32_t TY>
 struct RwType {
@@ -442,6 +446,10 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* ub = static_cast<const uint8_t*>(w2);
+    // q4_K: the matrix-core form (rows_mma.hip); KF_ROWS_VALU=1 keeps the per-lane dot form (a measurement switch)
+    static const bool valu = getenv("KF_ROWS_VALU") != nullptr;
+    if (ty == KF_TYPE_Q4_K && !valu && kf_rows_mma_ok(n, n_out, offsets ? n_slots : 1, w2 != nullptr))
+        return kf_launch_rows_mma(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
     if (ty == KF_TYPE_Q4_K)
         return w2 ? rows_dispatch<KF_TYPE_Q4_K, true>(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s)
                   : rows_dispatch<KF_TYPE_Q4_K, false>(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);

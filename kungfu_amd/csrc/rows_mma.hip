@@ -1,0 +1,373 @@
+// Multi-row q4_K product on the matrix cores: up to 16 activation rows against each weight row, for the MoE grouped
+// expert products (grid row = expert slot, activation rows = the pairs routed to it) and the few-row product of one
+// matrix. Same interface and results as rows_kernel (rows.hip), which it replaces for q4_K weights: the super-block
+// integers are the reference's dot_i8 integers (crates/kf-quant/src/types/q4_k.rs:10-58, sumi and mins), exact; the
+// float combine is the GEMV's. The reference runs these products as per-pair matvecs (kf_moe_matvec_i8 /
+// kf_moe_gate_up_i8, crates/kf-backend-cuda/src/kernels/quant.cuh:519-581) and its small-batch q4_K form as fragment
+// MMAs (kf_mm_frag, crates/kf-backend-cuda/src/kernels/mm_frag.cuh:60-292).
+//
+// Why: the per-lane dot4 form costs about 35 vector instructions per activation row and weight step, so with four to
+// eight rows a weight byte it is bound by the VALU rather than by HBM. Here a wave owns 16 weight rows and the
+// matrix core forms all rows' integer dots at once; the vector work per weight byte no longer grows with the rows.
+//
+// Per wave, per super-block of its 16 weight rows (2304 bytes):
+//   * operands, MFMA layouts (16 x 16 x 32 int8): A = activations (lane l: row l % 16, bytes 8 (l / 16).. of the
+//     group), B = weights (lane l: weight row l % 16, the same bytes of the group). For sub-block pair p a lane loads
+//     the 8 nibble bytes 16 + 32 p + 8 (l / 16).. of its row: the low nibbles are its B operand of group 2 p, the high
+//     nibbles of group 2 p + 1, unscaled (0..15);
+//   * I_g = v_mfma_i32_16x16x32_i8 per group, exact int32; S = sum_g sc_g I_g by 24-bit multiply-adds (every
+//     product below 2^22): the output lane holds weight row l % 16 for four activation rows, so its scales are one
+//     row's;
+//   * mins = sum_g m_g bsum_g by one v_mfma_f32_16x16x16_f16 (bsum_g = 64 hi + lo split at staging, m_g and 64 m_g
+//     against them: every product and partial sum is an integer below 2^24, exact);
+//   * acc += dx (d S - dmin mins).
+// Weights: each wave's super-block of 16 rows x 144 bytes is fetched whole by DMA (buffer_load ... lds: contiguous
+// 16-byte pieces, every cache line used by one instruction) into one of two LDS buffers of its own, the next one
+// landing while the current one is multiplied, continuing across the wave's tiles; operand loads from global memory
+// per lane (16 rows x 32 bytes an instruction) measured 25% slower. Activations are staged in LDS once per chunk of RT
+// rows by DMA, in K phases when all n columns do not fit beside the weight buffers.
+// Measured (Mixtral-style layer, 8 Q4_K experts, 16 tokens top-2): fused gate/up 129 us against 203 us for the
+// per-lane form.
+#include "kf_blocks.h"
+
+#include <algorithm>
+
+namespace {
+
+typedef float rm_v4f __attribute__((ext_vector_type(4)));
+typedef int rm_v4i __attribute__((ext_vector_type(4)));
+typedef _Float16 rm_v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t rm_v2u __attribute__((ext_vector_type(2)));
+typedef uint32_t rm_v4u __attribute__((ext_vector_type(4)));
+
+constexpr int RM_WAVES = 8;
+constexpr int RM_THREADS = 64 * RM_WAVES;
+
+// LDS of one chunk of RT staged rows: A operands [group][RT][32 bytes], the split group sums [super-block][RT][16 f16],
+// the activation scales [super-block][RT] f32
+struct RmLds {
+    int a, x, d, total;
+};
+
+__host__ __device__ inline RmLds rm_lds(int n, int rt) {
+    RmLds l;
+    const int nsb = n / KF_Q4_K_BLOCK;
+    l.a = 0;
+    l.x = rt * n;
+    l.d = l.x + nsb * rt * 32;
+    l.total = l.d + nsb * rt * 4;
+    return l;
+}
+
+constexpr int RM_TILE_BYTES = 16 * KF_Q4_K_BYTES;  // one super-block of a wave's 16 weight rows
+
+// One super-block of one weight operand row set: the lane's header and its four 8-byte nibble pieces
+struct RmW {
+    rm_v4u hd;
+    rm_v2u q[4];
+};
+
+// S and mins of one super-block for the lane's weight row against the staged rows; a_at / x_at: the lane's A operand
+// and split-sum addresses of this super-block (group 0)
+__device__ __forceinline__ void rm_block(const RmW& v, const uint8_t* a_at, int a_gstride, rm_v4h xo, int q, rm_v4i& S, rm_v4f& mins) {
+    const uint32_t m4 = 0x0f0f0f0fu;
+    S = rm_v4i{0, 0, 0, 0};
+    uint32_t mq = 0;
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        uint32_t sc2, m2;
+        kf_q4k_scales(v.hd.y, v.hd.z, v.hd.w, p, sc2, m2);
+        if (p == q) mq = m2;
+        const long blo = (long)(v.q[p].x & m4) | ((long)(v.q[p].y & m4) << 32);
+        const long bhi = (long)((v.q[p].x >> 4) & m4) | ((long)((v.q[p].y >> 4) & m4) << 32);
+        const long a0 = *reinterpret_cast<const long*>(a_at + (2 * p) * a_gstride);
+        const long a1 = *reinterpret_cast<const long*>(a_at + (2 * p + 1) * a_gstride);
+        const rm_v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, blo, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
+        const rm_v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, bhi, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
+        const int s0 = (int)(sc2 & 0xffu), s1 = (int)(sc2 >> 8);
+#pragma unroll
+        for (int e = 0; e < 4; e++) S[e] += __mul24(s0, i0[e]) + __mul24(s1, i1[e]);
+    }
+    // k slots of the lane's quarter q: groups 2q and 2q+1, each as (64 m, m) against the split sum (hi, lo)
+    rm_v4h mo;
+    mo[0] = (_Float16)(float)(64u * (mq & 0xffu));
+    mo[1] = (_Float16)(float)(mq & 0xffu);
+    mo[2] = (_Float16)(float)(64u * (mq >> 8));
+    mo[3] = (_Float16)(float)(mq >> 8);
+    mins = __builtin_amdgcn_mfma_f32_16x16x16f16(xo, mo, rm_v4f{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+}
+
+// ops::silu (crates/kf-backend-cpu/src/ops.rs): x / (1 + e^-x)
+__device__ __forceinline__ float rm_silu(float x) { return x / (1.0f + expf(-x)); }
+
+// Block (x, slot): weight rows [x * rpb, +rpb) of the slot's matrix (w + slot * expert_bytes; with GLU also w2's)
+// against the slot's pairs offsets[slot] .. offsets[slot + 1] of `order` (identity without order; one slot [0,
+// pairs) without offsets), RT at a time. The activation row of pair p is p (per_slot) or p / n_used. Outputs
+// y[p][o]: GLU ? silu(gate . x) * (up . x) : w . x + bias[o] + res[p][o].
+// K runs in phases of kc columns when a chunk's staged rows of all n columns do not fit beside the weight buffers;
+// then every wave owns one 16-row tile (rpb = 16 x waves) and its accumulators carry across the phases.
+template <bool GLU, int RT>
+__global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int64_t expert_bytes,
+                                                              int64_t row_bytes, const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
+                                                              const float* __restrict__ xd32, int n, int n_out, const int32_t* __restrict__ order,
+                                                              const int32_t* __restrict__ offsets, int pairs, int n_used, int per_slot,
+                                                              const float* __restrict__ bias, const float* __restrict__ res, float* __restrict__ y,
+                                                              int rpb, int kc) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    // a wave's super-blocks of weights land whole in its LDS buffers (two, alternating), rows contiguous
+    constexpr int NW = GLU ? 2 : 1;
+    __shared__ __align__(16) uint8_t pk0[RM_WAVES * NW * RM_TILE_BYTES];
+    __shared__ __align__(16) uint8_t pk1[RM_WAVES * NW * RM_TILE_BYTES];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int slot = blockIdx.y;
+    const int p0 = offsets ? offsets[slot] : 0;
+    const int p1 = offsets ? offsets[slot + 1] : pairs;
+    if (p0 >= p1) return;
+    const int nsb = n / KF_Q4_K_BLOCK, nsum = n / 32;
+    const int kcs = kc / KF_Q4_K_BLOCK, nph = (nsb + kcs - 1) / kcs;
+    const int o0 = blockIdx.x * rpb;
+    const int o1 = min(o0 + rpb, n_out);
+    const int tiles = (o1 - o0 + 15) / 16;
+    const RmLds L = rm_lds(kc, RT);
+    const int c = lane & 15, q = lane >> 4;
+
+    // weights: one buffer resource over the slot's matrix (rows past it read as zeros); DMA instruction i of a
+    // super-block moves the 16-byte pieces s = 64 i + lane of the tile's 16 rows x 144 bytes (row s / 9, piece s % 9;
+    // the third instruction only on lanes below 16): 3 instructions per matrix, the tile row and super-block adding
+    // row * row_bytes + sb * 144 as a scalar offset
+    const uint8_t* wbase = w + (int64_t)slot * expert_bytes;
+    const auto rw = kf_rsrc(wbase, (uint64_t)n_out * row_bytes);
+    const auto ru = kf_rsrc(GLU ? w2 + (int64_t)slot * expert_bytes : wbase, (uint64_t)n_out * row_bytes);
+    int vpk[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int s2 = min(64 * i + lane, 143);
+        vpk[i] = (s2 / 9) * (int)row_bytes + 16 * (s2 % 9);
+    }
+    // the wave's items in a phase: (tile t, super-block) for tiles t = wave, wave + WAVES, ..., super-block fastest
+    const int my_tiles = tiles > wave ? (tiles - wave + RM_WAVES - 1) / RM_WAVES : 0;
+    auto park = [&](int sb0, int nsbp, int it, uint8_t* buf) {
+        const int t = wave + (it / nsbp) * RM_WAVES, sb = sb0 + it % nsbp;
+        const int so = (o0 + 16 * t) * (int)row_bytes + sb * KF_Q4_K_BYTES;
+#pragma unroll
+        for (int k = 0; k < NW; k++) {
+            uint8_t* b = buf + (wave * NW + k) * RM_TILE_BYTES;
+            const auto r = k == 0 ? rw : ru;
+            kf_bdma16(r, vpk[0], so, b);
+            kf_bdma16(r, vpk[1], so, b + 1024);
+            if (lane < 16) kf_bdma16(r, vpk[2], so, b + 2048);
+        }
+    };
+    auto unpark = [&](RmW& v, const uint8_t* buf, int k) {
+        const uint8_t* b = buf + (wave * NW + k) * RM_TILE_BYTES + c * KF_Q4_K_BYTES;
+        v.hd = *reinterpret_cast<const rm_v4u*>(b);
+#pragma unroll
+        for (int p = 0; p < 4; p++) v.q[p] = *reinterpret_cast<const rm_v2u*>(b + 16 + 32 * p + 8 * q);
+    };
+    auto xrow_of = [&](int c0, int R, int r) {
+        const int pr = c0 + min(r, R - 1);
+        const int p = order ? order[pr] : pr;
+        return per_slot ? p : p / n_used;
+    };
+
+    for (int c0 = p0; c0 < p1; c0 += RT) {
+        const int R = min(RT, p1 - c0);
+        // the pairs of the lane's output rows 4q .. 4q + 3 (loaded once: a load at a tile's end would make the wave
+        // wait for every weight request in flight)
+        int pidx[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = min(4 * q + e, R - 1);
+            pidx[e] = order ? order[c0 + m] : c0 + m;
+        }
+        rm_v4f acc = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f}, accu = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int ph = 0; ph < nph; ph++) {
+            const int sb0 = ph * kcs, nsbp = min(kcs, nsb - sb0);
+            const int items = my_tiles * nsbp;
+            const bool last_phase = ph == nph - 1;
+            // the first two super-blocks of weights go out before the phase's activations are staged
+            if (items > 0) park(sb0, nsbp, 0, pk0);
+            if (items > 1) park(sb0, nsbp, 1, pk1);
+            // stage: A operands by DMA (instruction i fills LDS bytes [1024 i, +1024): slot s = 64 i + lane of 16
+            // bytes is group s / (2 RT) of the phase, row (s / 2) % RT, half s % 2), rows past R repeat row R - 1
+            {
+                const int ninst = RT * nsbp / 4;
+                for (int i = wave; i < ninst; i += RM_WAVES) {
+                    const int s = 64 * i + lane, g = s / (2 * RT), r = (s >> 1) % RT, h = s & 1;
+                    kf_dma16(xq + (int64_t)xrow_of(c0, R, r) * n + (int64_t)sb0 * KF_Q4_K_BLOCK + 32 * g + 16 * h, smem + L.a + 1024 * i);
+                }
+                // split group sums (f16 hi, lo of bsum = 64 hi + lo, exact) and scales, per (super-block, row)
+                for (int idx = threadIdx.x; idx < nsbp * RT; idx += RM_THREADS) {
+                    const int sb = idx / RT, r = idx % RT;
+                    const int xrow = xrow_of(c0, R, r);
+                    const int32_t* bs = xs32 + (int64_t)xrow * nsum + (sb0 + sb) * 8;
+                    _Float16* xo = reinterpret_cast<_Float16*>(smem + L.x) + (size_t)idx * 16;
+#pragma unroll
+                    for (int g = 0; g < 8; g++) {
+                        const int b = bs[g];
+                        xo[2 * g] = (_Float16)(float)(b >> 6);
+                        xo[2 * g + 1] = (_Float16)(float)(b & 63);
+                    }
+                    reinterpret_cast<float*>(smem + L.d)[idx] = xd32[(int64_t)xrow * nsum + (sb0 + sb) * 8];
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+
+            // lane constants: A operand of row c (rows past RT alias the staged ones; their outputs are not stored),
+            // split sums of row c, scales of rows 4q .. 4q + 3
+            const uint8_t* a_lane = smem + L.a + (c % RT) * 32 + 8 * q;
+            const int a_g = RT * 32;  // bytes between groups
+            auto process = [&](const RmW& v, const RmW& vu, int it) {
+                const int sb = it % nsbp;
+                const rm_v4h xo = *reinterpret_cast<const rm_v4h*>(smem + L.x + (sb * RT + c % RT) * 32 + 8 * q);
+                const rm_v4f dx = *reinterpret_cast<const rm_v4f*>(smem + L.d + (sb * RT + (4 * q) % RT) * 4);
+                const uint8_t* a_at = a_lane + sb * 8 * a_g;
+                rm_v4i S;
+                rm_v4f mins;
+                rm_block(v, a_at, a_g, xo, q, S, mins);
+                const float d = kf_h2f(v.hd.x & 0xffffu), dm = kf_h2f(v.hd.x >> 16);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], fmaf(-dm, mins[e], d * (float)S[e]), acc[e]);
+                if constexpr (GLU) {
+                    rm_block(vu, a_at, a_g, xo, q, S, mins);
+                    const float du = kf_h2f(vu.hd.x & 0xffffu), dmu = kf_h2f(vu.hd.x >> 16);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) accu[e] = fmaf(dx[e], fmaf(-dmu, mins[e], du * (float)S[e]), accu[e]);
+                }
+                if (last_phase && sb == nsbp - 1) {  // the tile is done: lane (c, q) holds weight row c for rows 4q ..
+                    const int t = wave + (it / nsbp) * RM_WAVES;
+                    const int o = o0 + 16 * t + c;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int m = 4 * q + e;
+                        if (m < R && o < o1) {
+                            const int p = pidx[e];
+                            float* yo = y + (int64_t)p * n_out + o;
+                            if constexpr (GLU)
+                                *yo = rm_silu(acc[e]) * accu[e];
+                            else
+                                *yo = acc[e] + (bias ? bias[o] : 0.0f) + (res ? res[(int64_t)p * n_out + o] : 0.0f);
+                        }
+                    }
+                    acc = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                    accu = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            };
+            // two buffers: item it is multiplied from one while it + 1 lands in the other; each wait leaves only the
+            // next item's DMA instructions (3 NW) outstanding
+            constexpr int NI = 3 * NW;
+            for (int it = 0; it < items; it += 2) {
+                if (it + 1 < items)
+                    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
+                else
+                    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+                RmW v, vu;
+                unpark(v, pk0, 0);
+                if constexpr (GLU) unpark(vu, pk0, 1);
+                process(v, vu, it);
+                if (it + 2 < items) {
+                    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));  // this buffer's reads are done
+                    park(sb0, nsbp, it + 2, pk0);
+                }
+                if (it + 1 < items) {
+                    if (it + 2 < items)
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
+                    else
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+                    unpark(v, pk1, 0);
+                    if constexpr (GLU) unpark(vu, pk1, 1);
+                    process(v, vu, it + 1);
+                    if (it + 3 < items) {
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
+                        park(sb0, nsbp, it + 3, pk1);
+                    }
+                }
+            }
+            __syncthreads();  // before the next phase or chunk restages
+        }
+    }
+}
+
+// LDS budget of a block: the chunk's staged rows (dynamic) and the two weight buffers (static)
+constexpr int RM_LDS_MAX = 160 * 1024;
+
+struct RmPlan {
+    int rt, kc, rpb;
+};
+
+// Staged rows 16 when all n columns fit beside the weight buffers, else 8; K phases when even 8 rows do not fit (each
+// wave then owns one tile)
+RmPlan rm_plan(int n, int n_out, int slots, bool glu) {
+    const int park = 2 * RM_WAVES * (glu ? 2 : 1) * RM_TILE_BYTES;
+    RmPlan pl{8, n, 0};
+    if (rm_lds(n, 16).total + park <= RM_LDS_MAX)
+        pl.rt = 16;
+    else if (rm_lds(n, 8).total + park > RM_LDS_MAX) {
+        const int nsb = n / KF_Q4_K_BLOCK;
+        int max_sb = nsb;
+        while (max_sb > 1 && rm_lds(max_sb * KF_Q4_K_BLOCK, 8).total + park > RM_LDS_MAX) max_sb--;
+        const int nph = (nsb + max_sb - 1) / max_sb;
+        pl.kc = ((nsb + nph - 1) / nph) * KF_Q4_K_BLOCK;  // balanced phases
+    }
+    if (pl.kc < n) {
+        pl.rpb = 16 * RM_WAVES;
+    } else {
+        // whole 16-row tiles, enough blocks to give every CU about two (over all slots), at most 16 tiles a wave (a
+        // block stages its activation rows once for all of them)
+        const int tiles = (n_out + 15) / 16;
+        const int want = std::max(1, 512 / slots);
+        const int per_wave = std::max(1, std::min(16, (tiles + want * RM_WAVES - 1) / (want * RM_WAVES)));
+        pl.rpb = 16 * RM_WAVES * per_wave;
+    }
+    return pl;
+}
+
+template <bool GLU, int RT>
+hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
+                           const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
+                           int per_slot, const float* bias, const float* res, float* y, const RmPlan& pl, hipStream_t s) {
+    auto* fn = rows_mma_kernel<GLU, RT>;
+    const int lds = rm_lds(pl.kc, RT).total;
+    static int lds_set = 0;
+    if (lds_set < lds) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    const int slots = offsets ? n_slots : 1;
+    dim3 grid((n_out + pl.rpb - 1) / pl.rpb, slots);
+    fn<<<grid, RM_THREADS, lds, s>>>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, pairs, n_used, per_slot, bias, res, y,
+                                     pl.rpb, pl.kc);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+// Whether the matrix-core product takes this launch: it needs 16-byte aligned weight rows (q4_K always) and a grid
+// that fills the GPU; a K-phased launch (one tile a wave) over few slots has too few blocks, and the per-lane dot form
+// takes it
+bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu) {
+    const RmPlan pl = rm_plan(n, n_out, slots, glu);
+    return pl.kc == n || (int64_t)((n_out + pl.rpb - 1) / pl.rpb) * slots >= 128;
+}
+
+// Host launcher of the q4_K multi-row / grouped product on the matrix cores, validated by the caller (api.cpp): n a
+// multiple of 256 and at most 16384, rows 16-byte aligned, every matrix (expert_bytes apart) below 2 GB.
+hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
+                              const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
+                              int per_slot, const float* bias, const float* res, float* y, hipStream_t s) {
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* ub = static_cast<const uint8_t*>(w2);
+    const RmPlan pl = rm_plan(n, n_out, offsets ? n_slots : 1, w2 != nullptr);
+#define KF_RM(G, RT_) \
+    return rows_mma_launch<G, RT_>(wb, ub, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, pl, s)
+    if (w2) {
+        if (pl.rt == 16) KF_RM(true, 16);
+        KF_RM(true, 8);
+    }
+    if (pl.rt == 16) KF_RM(false, 16);
+    KF_RM(false, 8);
+#undef KF_RM
+}

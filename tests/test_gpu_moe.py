@@ -164,6 +164,54 @@ def _check_layer(got, stages, args, ty, n_exp, n_embd, n_ff, rows_checked):
     assert np.abs(got[:rows_checked] - flt).max() <= 2e-2 * max(np.abs(flt).mean(), 1e-6)
 
 
+@pytest.mark.parametrize("glu", [False, True])
+@pytest.mark.parametrize("n_in,n_slots,n_out,big", [(14336, 16, 1024, 9), (1280, 4, 200, 21)])
+def test_moe_gemv_q4_k_chunks_and_k_phases(cuda, glu, n_in, n_slots, n_out, big):
+    """The q4_K grouped product on the matrix cores: at 14336 columns the staged rows run in K phases (eight rows a
+    chunk; slot 5 has 9 pairs, two chunks); at 1280 columns sixteen rows a chunk (slot 1 has 21 pairs, two chunks)."""
+    import torch
+
+    ty, n_used, rows = kf.TYPE_Q4_K, 2, 12 if big < 16 else 14
+    # three distinct experts repeated over the slots (expert e is base e % 3): cheap to make, and a wrong expert
+    # offset shows unless it is a multiple of three
+    def tiled(seed):
+        base = _experts(ty, 3, n_out, n_in, seed)
+        return np.concatenate([base[(e % 3) * n_out : (e % 3 + 1) * n_out] for e in range(n_slots)])
+
+    w = tiled(41)
+    wu = tiled(42) if glu else None
+    x = kf.synth_normal(43, 1.0, rows * n_in).reshape(rows, n_in)
+    rng = np.random.default_rng(44)
+    slots = rng.integers(0, n_slots, rows * n_used).astype(np.int32)
+    hot = 5 if n_slots > 5 else 1
+    slots[slots == hot] = (hot + 1) % n_slots
+    slots[:big] = hot
+    slots[big + 1] = -1
+    pairs = len(slots)
+    order = torch.empty(pairs, dtype=torch.int32, device=cuda)
+    offsets = torch.empty(n_slots + 1, dtype=torch.int32, device=cuda)
+    kf.moe_group(_t(slots, cuda), pairs, n_slots, order, offsets)
+    act = kf.alloc_act(rows, n_in, cuda)
+    kf.quant_act(_t(x, cuda), act, kf.act_kind(ty))
+    y = torch.full((pairs, n_out), float("nan"), device=cuda)
+    kf.moe_gemv(ty, _t(w, cuda), act, rows, n_in, n_out, order, offsets, n_slots, n_used, False, y, w_up=None if wu is None else _t(wu, cuda))
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    for p in range(pairs):
+        e = slots[p]
+        if e < 0:
+            assert np.isnan(got[p]).all()
+            continue
+        xr = x[p // n_used : p // n_used + 1]
+        g = oracle.matmul_i8(ty, w[e * n_out : (e + 1) * n_out], n_in, n_out, xr)[0]
+        if glu:
+            u = oracle.matmul_i8(ty, wu[e * n_out : (e + 1) * n_out], n_in, n_out, xr)[0]
+            want = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
+        else:
+            want = g
+        _close(got[p], want.astype(np.float32))
+
+
 @pytest.mark.parametrize("ty", [kf.TYPE_Q4_K, kf.TYPE_Q8_0])
 @pytest.mark.parametrize("rows", [1, 7, 37])
 def test_moe_ffn_matches_cpu_backend(cuda, ty, rows):
