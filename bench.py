@@ -172,6 +172,37 @@ def small_batch_section(dev):
     return out
 
 
+def small_batch_q4_k_section(dev):
+    """Batch 8..64 of the Llama-3-8B shapes with Q4_K weights (the reference's mm_frag range): the multi-row product
+    (kf_hip_gemv: 16 activation rows a weight pass on the matrix cores) and the tile GEMM (kf_hip_gemm_i8) alone on
+    resident quantized activations, and the whole kf_hip_matmul (quant_act + the product it selects); weight copies
+    rotated past the MALL."""
+    import torch
+
+    import kungfu_amd as kf
+
+    ty = kf.TYPE_Q4_K
+    out = {}
+    for name, n, n_out in [("qkv", 4096, 6144), ("o", 4096, 4096), ("gate", 4096, 14336), ("down", 14336, 4096)]:
+        w = torch.from_numpy(make_weights(ty, n, n_out)).to(dev)
+        ws = [w] + [w.clone() for _ in range(max(1, -(-2 * MALL_BYTES // w.numel())))]
+        res = {}
+        for m in SMALL_BATCH:
+            x = torch.from_numpy(kf.synth_normal(1, 1.0, m * n).reshape(m, n)).to(dev)
+            act = kf.alloc_act(m, n, dev)
+            y = torch.empty((m, n_out), device=dev)
+            kf.quant_act(x, act, kf.ACT_Q8K)
+            us_r = time_launches(lambda i: kf.gemv(ty, ws[i % len(ws)], act, y, m, n, n_out), 50)
+            us_g = time_launches(lambda i: kf.gemm_i8(ty, ws[i % len(ws)], act, y, m, n, n_out), 50)
+            us_mm = time_launches(lambda i: kf.matmul(ty, ws[i % len(ws)], x, act, y, n_out), 50)
+            b = gemv_bytes(ty, n, n_out, m)
+            res[str(m)] = {"rows_us": round(us_r, 2), "rows_GBs": round(b / us_r / 1e3, 1), "gemm_us": round(us_g, 2),
+                           "gemm_GBs": round(b / us_g / 1e3, 1), "matmul_us": round(us_mm, 2)}
+        out[name] = res
+        del ws, w
+    return out
+
+
 def moe_section(dev, seed=0):
     """the routed expert layer (kf_hip_moe_ffn) for 8 Q4_K experts of gate/up 4096->14336 and down
     14336->4096, 16 tokens, top-2 uniform without replacement. GB/s over the weight bytes of the touched experts (each
@@ -372,7 +403,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "moe", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "small_q4_k", "moe", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -386,7 +417,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "moe": moe_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "small_q4_k": small_batch_q4_k_section, "moe": moe_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -461,6 +492,7 @@ def main():
     out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
     out["int8_gemm_q4_k"] = gemm_q4_k_section(dev)
     out["small_batch_q8_0"] = small_batch_section(dev)
+    out["small_batch_q4_k"] = small_batch_q4_k_section(dev)
     out["moe_q4_k"] = moe_section(dev)
     out["fused_producers"] = fused_section(dev)
     out["k_quants"] = kquant_section(dev)
