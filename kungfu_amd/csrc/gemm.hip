@@ -252,10 +252,14 @@ constexpr int SK_G = 8;                        // groups per chunk
 constexpr int SK_WB = SK_G * KF_Q8_0_BYTES;    // 272 weight bytes per row per chunk
 constexpr int SK_WP = SK_WB / 16;              // 17 pieces
 constexpr int SK_STRIDE = 304;                 // LDS row stride
-constexpr int SK_TN = 2;                       // 16-column weight tiles of a wave
-constexpr int SK_ROWS = 16 * SK_TN;            // weight rows of a wave
-constexpr int SK_WI = (SK_ROWS * SK_WP + 63) / 64;  // 9 load instructions for the weights
-constexpr int SK_WAVE_LDS = SK_ROWS * SK_STRIDE;    // 9728 bytes: also holds one partial tile (TM x TN x 1 KB)
+// A wave's weight tile: TN 16-column tiles (two for wide outputs, one when the output has at most one block of 16
+// columns per CU, so that every CU gets a block)
+template <int TN>
+struct SkGeo {
+    static constexpr int ROWS = 16 * TN;                     // weight rows of a wave
+    static constexpr int WI = (ROWS * SK_WP + 63) / 64;      // load instructions for the weights (9 for TN = 2)
+    static constexpr int WAVE_LDS = ROWS * SK_STRIDE;        // 9728 bytes for TN = 2: also holds one partial tile
+};
 
 // The activation operands and scales of one chunk, loaded together when the chunk starts (they are small and stay
 // in L2, shared by every block)
@@ -283,12 +287,13 @@ struct SkAct {
     }
 };
 
-template <int MR>
+template <int MR, int SK_TN>
 __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
                                                                                const int8_t* __restrict__ xq, const float* __restrict__ xd32,
                                                                                const float* __restrict__ bias, const float* __restrict__ res,
                                                                                float* __restrict__ y, int M, int N, int K) {
     constexpr int TM = SkAct<MR>::TM;
+    constexpr int SK_ROWS = SkGeo<SK_TN>::ROWS, SK_WI = SkGeo<SK_TN>::WI, SK_WAVE_LDS = SkGeo<SK_TN>::WAVE_LDS;
     extern __shared__ __align__(16) uint8_t smem[];
     const int W = blockDim.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -911,24 +916,24 @@ hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
     return hipGetLastError();
 }
 
-template <int MR>
+template <int MR, int TN>
 hipError_t gemm_small_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
                              float* y, int M, int N, int K, int W, hipStream_t s) {
-    static_assert(SK_WAVE_LDS >= SkAct<MR>::TM * SK_TN * 4 * 64 * 4, "a wave region holds a partial tile");
-    auto* fn = gemm_q8_0_small_kernel<MR>;
+    static_assert(SkGeo<TN>::WAVE_LDS >= SkAct<MR>::TM * TN * 4 * 64 * 4, "a wave region holds a partial tile");
+    auto* fn = gemm_q8_0_small_kernel<MR, TN>;
     static bool lds_set = false;
     if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, 8 * SK_WAVE_LDS);
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, 8 * SkGeo<TN>::WAVE_LDS);
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    fn<<<dim3((N + SK_ROWS - 1) / SK_ROWS, (M + MR - 1) / MR), 64 * W, W * SK_WAVE_LDS, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    fn<<<dim3((N + SkGeo<TN>::ROWS - 1) / SkGeo<TN>::ROWS, (M + MR - 1) / MR), 64 * W, W * SkGeo<TN>::WAVE_LDS, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
     return hipGetLastError();
 }
 
 // Waves per block of the small-batch kernel: enough blocks x waves to fill the GPU (about 4096 waves), at least two
 // chunks a wave, a power of two; KF_GEMM_SMALL_W overrides it (a tuning knob)
-int small_waves(int M, int N, int K) {
+int small_waves(int M, int N, int K, int rows_per_block) {
     static const int forced = [] {
         const char* e = getenv("KF_GEMM_SMALL_W");
         return e ? atoi(e) : 0;
@@ -936,10 +941,20 @@ int small_waves(int M, int N, int K) {
     const int cap = 8;
     const int rblocks = (M + 15) / 16;
     if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
-    const int tiles = (N + SK_ROWS - 1) / SK_ROWS, chunks = K / 256;
+    const int tiles = (N + rows_per_block - 1) / rows_per_block, chunks = K / 256;
     int w = 1;
     while (w < cap && tiles * rblocks * w < 4096 && chunks / (2 * w) >= 2) w *= 2;
     return w;
+}
+
+// Compute units of the current device (cached per process; the build targets one gfx950 device model)
+int gm_cus() {
+    static const int n = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+        return v;
+    }();
+    return n;
 }
 
 }  // namespace
@@ -956,9 +971,12 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
     const auto* wb = static_cast<const uint8_t*>(w);
     // the small-batch kernel reads whole 16-byte pieces of rows, which needs 16-byte aligned rows (K % 256 == 0)
     if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31)) {
-        const int wv = small_waves(M, N, K);
-        if (M <= 16) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);
-        if (M <= 64) return gemm_small_launch<16>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, wv, s);  // M / 16 row blocks
+        if (M <= 64) {  // M / 16 row blocks
+            // one 16-column tile a wave when that still gives at most one block per CU (a block holds a CU), else two
+            if ((int64_t)((N + 15) / 16) * ((M + 15) / 16) <= gm_cus())
+                return gemm_small_launch<16, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 16), s);
+            return gemm_small_launch<16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 32), s);
+        }
     }
     if (K % 256 == 0 && row_bytes % 16 == 0) return gemm_q8_0_dma_launch<2, 4, 2, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
     return gemm_launch<2, 2, 2, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
