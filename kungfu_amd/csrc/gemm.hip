@@ -932,13 +932,13 @@ hipError_t gemm_small_launch(const uint8_t* w, int64_t row_bytes, const int8_t* 
 }
 
 // Waves per block of the small-batch kernel: enough blocks x waves to fill the GPU (about 4096 waves), at least two
-// chunks a wave, a power of two; KF_GEMM_SMALL_W overrides it (a tuning knob)
+// chunks a wave, a power of two, at most four; KF_GEMM_SMALL_W overrides it (a tuning knob)
 int small_waves(int M, int N, int K, int rows_per_block) {
     static const int forced = [] {
         const char* e = getenv("KF_GEMM_SMALL_W");
         return e ? atoi(e) : 0;
     }();
-    const int cap = 8;
+    const int cap = 4;  // measured: four waves (more chunks each) beat eight on every Llama shape at M = 8..64
     const int rblocks = (M + 15) / 16;
     if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
     const int tiles = (N + rows_per_block - 1) / rows_per_block, chunks = K / 256;
@@ -973,7 +973,11 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
     if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31)) {
         if (M <= 64) {  // M / 16 row blocks
             // one 16-column tile a wave when that still gives at most one block per CU (a block holds a CU), else two
-            if ((int64_t)((N + 15) / 16) * ((M + 15) / 16) <= gm_cus())
+            static const int tn = [] {  // KF_GEMM_SMALL_TN: a tuning knob
+                const char* e = getenv("KF_GEMM_SMALL_TN");
+                return e ? atoi(e) : 0;
+            }();
+            if (tn == 1 || (tn != 2 && (int64_t)((N + 15) / 16) * ((M + 15) / 16) <= gm_cus()))
                 return gemm_small_launch<16, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 16), s);
             return gemm_small_launch<16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 32), s);
         }
