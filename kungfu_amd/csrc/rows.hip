@@ -23,8 +23,8 @@
 
 hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
                               const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
-                              int per_slot, const float* bias, const float* res, float* y, hipStream_t s);
-bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu);
+                              int per_slot, int avg_rows, const float* bias, const float* res, float* y, hipStream_t s);
+bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu, int avg_rows);
 
 namespace {
 
@@ -448,8 +448,12 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
     const auto* ub = static_cast<const uint8_t*>(w2);
     // q4_K: the matrix-core form (rows_mma.hip); KF_ROWS_VALU=1 keeps the per-lane dot form (a measurement switch)
     static const bool valu = getenv("KF_ROWS_VALU") != nullptr;
-    if (ty == KF_TYPE_Q4_K && !valu && kf_rows_mma_ok(n, n_out, offsets ? n_slots : 1, w2 != nullptr))
-        return kf_launch_rows_mma(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
+    // the activation rows a slot gets on average (grouped: every pair of act_rows x n_used, or one per row)
+    const int slots = offsets ? n_slots : 1;
+    const int avg_rows = offsets ? (per_slot ? act_rows : act_rows * n_used) / std::max(1, slots) : pairs;
+    if (ty == KF_TYPE_Q4_K && !valu && kf_rows_mma_ok(n, n_out, slots, w2 != nullptr, avg_rows))
+        return kf_launch_rows_mma(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, avg_rows, bias,
+                                  res, y, s);
     if (ty == KF_TYPE_Q4_K)
         return w2 ? rows_dispatch<KF_TYPE_Q4_K, true>(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s)
                   : rows_dispatch<KF_TYPE_Q4_K, false>(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);

@@ -106,7 +106,7 @@ __device__ __forceinline__ float rm_silu(float x) { return x / (1.0f + expf(-x))
 // y[p][o]: GLU ? silu(gate . x) * (up . x) : w . x + bias[o] + res[p][o].
 // K runs in phases of kc columns when a chunk's staged rows of all n columns do not fit beside the weight buffers;
 // then every wave owns one 16-row tile (rpb = 16 x waves) and its accumulators carry across the phases.
-template <bool GLU, int RT>
+template <bool GLU, int RT, int NB>
 __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __restrict__ w, const uint8_t* __restrict__ w2, int64_t expert_bytes,
                                                               int64_t row_bytes, const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
                                                               const float* __restrict__ xd32, int n, int n_out, const int32_t* __restrict__ order,
@@ -114,10 +114,11 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
                                                               const float* __restrict__ bias, const float* __restrict__ res, float* __restrict__ y,
                                                               int rpb, int kc) {
     extern __shared__ __align__(16) uint8_t smem[];
-    // a wave's super-blocks of weights land whole in its LDS buffers (two, alternating), rows contiguous
+    // a wave's super-blocks of weights land whole in its LDS buffers (NB of them, in rotation), rows contiguous
     constexpr int NW = GLU ? 2 : 1;
     __shared__ __align__(16) uint8_t pk0[RM_WAVES * NW * RM_TILE_BYTES];
     __shared__ __align__(16) uint8_t pk1[RM_WAVES * NW * RM_TILE_BYTES];
+    __shared__ __align__(16) uint8_t pk2[NB > 2 ? RM_WAVES * NW * RM_TILE_BYTES : 16];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slot = blockIdx.y;
@@ -186,9 +187,10 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
             const int sb0 = ph * kcs, nsbp = min(kcs, nsb - sb0);
             const int items = my_tiles * nsbp;
             const bool last_phase = ph == nph - 1;
-            // the first two super-blocks of weights go out before the phase's activations are staged
+            // the first NB super-blocks of weights go out before the phase's activations are staged
             if (items > 0) park(sb0, nsbp, 0, pk0);
             if (items > 1) park(sb0, nsbp, 1, pk1);
+            if (NB > 2 && items > 2) park(sb0, nsbp, 2, pk2);
             // stage: A operands by DMA (instruction i fills LDS bytes [1024 i, +1024): slot s = 64 i + lane of 16
             // bytes is group s / (2 RT) of the phase, row (s / 2) % RT, half s % 2), rows past R repeat row R - 1
             {
@@ -255,35 +257,30 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
                     accu = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
                 }
             };
-            // two buffers: item it is multiplied from one while it + 1 lands in the other; each wait leaves only the
-            // next item's DMA instructions (3 NW) outstanding
+            // NB buffers in rotation: item j is multiplied from one while j + 1 .. j + NB - 1 land in the others; each
+            // wait leaves only those items' DMA instructions (3 NW each) outstanding
             constexpr int NI = 3 * NW;
-            for (int it = 0; it < items; it += 2) {
-                if (it + 1 < items)
+            auto step = [&](uint8_t* buf, int j) {
+                const int ahead = min(NB - 1, items - 1 - j);
+                if (ahead >= 2)
+                    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(2 * NI));
+                else if (ahead == 1)
                     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
                 else
                     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
                 RmW v, vu;
-                unpark(v, pk0, 0);
-                if constexpr (GLU) unpark(vu, pk0, 1);
-                process(v, vu, it);
-                if (it + 2 < items) {
+                unpark(v, buf, 0);
+                if constexpr (GLU) unpark(vu, buf, 1);
+                process(v, vu, j);
+                if (j + NB < items) {
                     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));  // this buffer's reads are done
-                    park(sb0, nsbp, it + 2, pk0);
+                    park(sb0, nsbp, j + NB, buf);
                 }
-                if (it + 1 < items) {
-                    if (it + 2 < items)
-                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
-                    else
-                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-                    unpark(v, pk1, 0);
-                    if constexpr (GLU) unpark(vu, pk1, 1);
-                    process(v, vu, it + 1);
-                    if (it + 3 < items) {
-                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
-                        park(sb0, nsbp, it + 3, pk1);
-                    }
-                }
+            };
+            for (int it = 0; it < items; it += NB) {
+                step(pk0, it);
+                if (it + 1 < items) step(pk1, it + 1);
+                if (NB > 2 && it + 2 < items) step(pk2, it + 2);
             }
             __syncthreads();  // before the next phase or chunk restages
         }
@@ -294,23 +291,39 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
 constexpr int RM_LDS_MAX = 160 * 1024;
 
 struct RmPlan {
-    int rt, kc, rpb;
+    int rt, nb, kc, rpb;
 };
 
-// Staged rows 16 when all n columns fit beside the weight buffers, else 8; K phases when even 8 rows do not fit (each
-// wave then owns one tile)
-RmPlan rm_plan(int n, int n_out, int slots, bool glu) {
-    const int park = 2 * RM_WAVES * (glu ? 2 : 1) * RM_TILE_BYTES;
-    RmPlan pl{8, n, 0};
-    if (rm_lds(n, 16).total + park <= RM_LDS_MAX)
-        pl.rt = 16;
-    else if (rm_lds(n, 8).total + park > RM_LDS_MAX) {
+// Staged rows per chunk (16 or 8), weight buffers per wave (3 or 2) and K phases. Preferred: 16 rows with three
+// buffers; with few pairs a slot (at most 8 on average) 8 rows with three buffers before 16 with two; K phases (each
+// wave then owns one tile) when even 8 rows of all n columns do not fit.
+RmPlan rm_plan(int n, int n_out, int slots, bool glu, int avg_rows) {
+    const int buf = RM_WAVES * (glu ? 2 : 1) * RM_TILE_BYTES;
+    auto fits = [&](int rt, int nb) { return rm_lds(n, rt).total + nb * buf <= RM_LDS_MAX; };
+    RmPlan pl{8, 2, n, 0};
+    if (fits(16, 3))
+        pl = RmPlan{16, 3, n, 0};
+    else if (avg_rows <= 8 && fits(8, 3))
+        pl = RmPlan{8, 3, n, 0};
+    else if (fits(16, 2))
+        pl = RmPlan{16, 2, n, 0};
+    else if (fits(8, 3))
+        pl = RmPlan{8, 3, n, 0};
+    else if (fits(8, 2))
+        pl = RmPlan{8, 2, n, 0};
+    else {
+        pl = RmPlan{8, 3, n, 0};
         const int nsb = n / KF_Q4_K_BLOCK;
         int max_sb = nsb;
-        while (max_sb > 1 && rm_lds(max_sb * KF_Q4_K_BLOCK, 8).total + park > RM_LDS_MAX) max_sb--;
+        while (max_sb > 1 && rm_lds(max_sb * KF_Q4_K_BLOCK, 8).total + 3 * buf > RM_LDS_MAX) max_sb--;
         const int nph = (nsb + max_sb - 1) / max_sb;
         pl.kc = ((nsb + nph - 1) / nph) * KF_Q4_K_BLOCK;  // balanced phases
     }
+    static const int forced_nb = [] {  // KF_RM_NB: a measurement knob (2 or 3 buffers)
+        const char* e = getenv("KF_RM_NB");
+        return e ? atoi(e) : 0;
+    }();
+    if (forced_nb == 2) pl.nb = 2;
     if (pl.kc < n) {
         pl.rpb = 16 * RM_WAVES;
     } else {
@@ -324,11 +337,11 @@ RmPlan rm_plan(int n, int n_out, int slots, bool glu) {
     return pl;
 }
 
-template <bool GLU, int RT>
+template <bool GLU, int RT, int NB>
 hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
                            const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
                            int per_slot, const float* bias, const float* res, float* y, const RmPlan& pl, hipStream_t s) {
-    auto* fn = rows_mma_kernel<GLU, RT>;
+    auto* fn = rows_mma_kernel<GLU, RT, NB>;
     const int lds = rm_lds(pl.kc, RT).total;
     static int lds_set = 0;
     if (lds_set < lds) {
@@ -348,8 +361,8 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
 // Whether the matrix-core product takes this launch: it needs 16-byte aligned weight rows (q4_K always) and a grid
 // that fills the GPU; a K-phased launch (one tile a wave) over few slots has too few blocks, and the per-lane dot form
 // takes it
-bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu) {
-    const RmPlan pl = rm_plan(n, n_out, slots, glu);
+bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu, int avg_rows) {
+    const RmPlan pl = rm_plan(n, n_out, slots, glu, avg_rows);
     return pl.kc == n || (int64_t)((n_out + pl.rpb - 1) / pl.rpb) * slots >= 128;
 }
 
@@ -357,17 +370,21 @@ bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu) {
 // multiple of 256 and at most 16384, rows 16-byte aligned, every matrix (expert_bytes apart) below 2 GB.
 hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, const int8_t* xq, const int32_t* xs32,
                               const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
-                              int per_slot, const float* bias, const float* res, float* y, hipStream_t s) {
+                              int per_slot, int avg_rows, const float* bias, const float* res, float* y, hipStream_t s) {
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* ub = static_cast<const uint8_t*>(w2);
-    const RmPlan pl = rm_plan(n, n_out, offsets ? n_slots : 1, w2 != nullptr);
-#define KF_RM(G, RT_) \
-    return rows_mma_launch<G, RT_>(wb, ub, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, pl, s)
+    const RmPlan pl = rm_plan(n, n_out, offsets ? n_slots : 1, w2 != nullptr, avg_rows);
+#define KF_RM(G, RT_, NB_) \
+    return rows_mma_launch<G, RT_, NB_>(wb, ub, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, pl, s)
+#define KF_RM_NB(G, RT_) \
+    if (pl.nb == 3) KF_RM(G, RT_, 3); \
+    KF_RM(G, RT_, 2)
     if (w2) {
-        if (pl.rt == 16) KF_RM(true, 16);
-        KF_RM(true, 8);
+        if (pl.rt == 16) { KF_RM_NB(true, 16); }
+        KF_RM_NB(true, 8);
     }
-    if (pl.rt == 16) KF_RM(false, 16);
-    KF_RM(false, 8);
+    if (pl.rt == 16) { KF_RM_NB(false, 16); }
+    KF_RM_NB(false, 8);
+#undef KF_RM_NB
 #undef KF_RM
 }
