@@ -24,6 +24,7 @@
 //     lane loads its MFMA operand pieces straight from memory (no LDS staging) several groups ahead, and the waves'
 //     partial tiles are summed in LDS in a fixed tree order.
 #include "kf_blocks.h"
+#include "kf_host.h"
 #include "kf_device.h"
 
 #include <algorithm>
@@ -905,12 +906,9 @@ hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
                        int M, int N, int K, hipStream_t s) {
     using C = GmCfg<WM, WN, TM, TN>;
     auto* fn = gemm_q8_0_kernel<WM, WN, TM, TN>;
-    static bool lds_set = false;  // the double-buffered stage needs more than the default 64 KB of LDS
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, 2 * C::STAGE);
-        if (e != hipSuccess) return e;
-        lds_set = true;
-    }
+    // the double-buffered stage needs more than the default 64 KB of LDS
+    const hipError_t e = kf_raise_lds(reinterpret_cast<const void*>(fn), 2 * C::STAGE);
+    if (e != hipSuccess) return e;
     dim3 grid((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
     fn<<<grid, GM_THREADS, 2 * C::STAGE, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
     return hipGetLastError();
@@ -921,12 +919,8 @@ hipError_t gemm_small_launch(const uint8_t* w, int64_t row_bytes, const int8_t* 
                              float* y, int M, int N, int K, int W, hipStream_t s) {
     static_assert(SkGeo<TN>::WAVE_LDS >= SkAct<MR>::TM * TN * 4 * 64 * 4, "a wave region holds a partial tile");
     auto* fn = gemm_q8_0_small_kernel<MR, TN>;
-    static bool lds_set = false;
-    if (!lds_set) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, 8 * SkGeo<TN>::WAVE_LDS);
-        if (e != hipSuccess) return e;
-        lds_set = true;
-    }
+    const hipError_t e = kf_raise_lds(reinterpret_cast<const void*>(fn), 8 * SkGeo<TN>::WAVE_LDS);
+    if (e != hipSuccess) return e;
     fn<<<dim3((N + SkGeo<TN>::ROWS - 1) / SkGeo<TN>::ROWS, (M + MR - 1) / MR), 64 * W, W * SkGeo<TN>::WAVE_LDS, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
     return hipGetLastError();
 }

@@ -17,6 +17,7 @@
 #include <type_traits>
 
 #include "kf_blocks.h"
+#include "kf_host.h"
 
 #include <algorithm>
 
@@ -708,17 +709,14 @@ __global__ void block_ints_kernel(uint32_t ty, const uint8_t* __restrict__ w, in
     }
 }
 
-int g_cu_count = 0;
-
+// Compute units of the first device the process launches on (thread-safe static; the build targets one device model)
 int cu_count() {
-    if (g_cu_count == 0) {
+    static const int n = [] {
         int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            g_cu_count = v;
-        else
-            g_cu_count = 256;
-    }
-    return g_cu_count;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+        return v;
+    }();
+    return n;
 }
 
 typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int, const KfSegs);
@@ -730,8 +728,10 @@ int resident_blocks(GvKernel k, size_t smem) {
         size_t smem;
         int v;
     };
+    static std::mutex mu;  // launchers may run on several threads (one per stream)
     static Entry cache[64];
     static int used = 0;
+    std::lock_guard<std::mutex> g(mu);
     for (int i = 0; i < used; i++)
         if (cache[i].k == k && cache[i].smem == smem) return cache[i].v;
     int v = 0;

@@ -112,7 +112,7 @@ __global__ void __launch_bounds__(GK_THREADS) gemv_k_kernel(const uint8_t* __res
 }
 
 int gk_cus() {
-    static int cus = [] {
+    static const int cus = [] {
         int dev = 0, v = 0;
         if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1)
             v = 256;

@@ -18,6 +18,7 @@
 // wave, conflict free), with their per-32 integer sums and scales. The next row's weights are requested before the
 // current row is multiplied.
 #include "kf_blocks.h"
+#include "kf_host.h"
 
 #include <algorithm>
 
@@ -375,11 +376,9 @@ hipError_t rows_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_bytes
                        int per_slot, const float* bias, const float* res, float* y, hipStream_t s) {
     auto* fn = rows_kernel<TY, RMAX, GLU, STEPS>;
     const int lds = RMAX * rw_row_lds<TY>(n);
-    static int lds_set = 0;
-    if (lds > 65536 && lds_set < lds) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (lds > 65536) {
+        const hipError_t e = kf_raise_lds(reinterpret_cast<const void*>(fn), lds);
         if (e != hipSuccess) return e;
-        lds_set = lds;
     }
     constexpr int threads = rw_threads<STEPS, GLU>();
     constexpr int waves = threads / 64;

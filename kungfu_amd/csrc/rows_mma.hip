@@ -29,6 +29,7 @@
 // Measured (Mixtral-style layer, 8 Q4_K experts, 16 tokens top-2): fused gate/up 129 us against 203 us for the
 // per-lane form.
 #include "kf_blocks.h"
+#include "kf_host.h"
 
 #include <algorithm>
 
@@ -343,12 +344,8 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
                            int per_slot, const float* bias, const float* res, float* y, const RmPlan& pl, hipStream_t s) {
     auto* fn = rows_mma_kernel<GLU, RT, NB>;
     const int lds = rm_lds(pl.kc, RT).total;
-    static int lds_set = 0;
-    if (lds_set < lds) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(fn), hipFuncAttributeMaxDynamicSharedMemorySize, lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    const hipError_t e = kf_raise_lds(reinterpret_cast<const void*>(fn), lds);
+    if (e != hipSuccess) return e;
     const int slots = offsets ? n_slots : 1;
     dim3 grid((n_out + pl.rpb - 1) / pl.rpb, slots);
     fn<<<grid, RM_THREADS, lds, s>>>(w, w2, expert_bytes, row_bytes, xq, xs32, xd32, n, n_out, order, offsets, pairs, n_used, per_slot, bias, res, y,
