@@ -355,10 +355,12 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
 
 }  // namespace
 
-// Whether the matrix-core product takes this launch: it needs 16-byte aligned weight rows (q4_K always) and a grid
-// that fills the GPU; a K-phased launch (one tile a wave) over few slots has too few blocks, and the per-lane dot form
-// takes it
+// Whether the matrix-core product takes this launch: it needs 16-byte aligned weight rows (q4_K always), matrices
+// below 2 GB and a grid that fills the GPU; a K-phased launch (one tile a wave) over few slots has too few blocks, and
+// the per-lane dot form takes it
 bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu, int avg_rows) {
+    // row offsets within a matrix travel as 32-bit scalar offsets
+    if ((int64_t)n_out * (n / KF_Q4_K_BLOCK) * KF_Q4_K_BYTES >= (1ll << 31)) return false;
     const RmPlan pl = rm_plan(n, n_out, slots, glu, avg_rows);
     return pl.kc == n || (int64_t)((n_out + pl.rpb - 1) / pl.rpb) * slots >= 128;
 }
