@@ -122,13 +122,17 @@ __global__ void __launch_bounds__(QA_THREADS) quant_act_kernel(const float* __re
 // correctly rounded f32 square root and division, then walks the row's 1024-column spans computing (v * inv) * w + b
 // unfused: the values the CPU rounds, so the quantized integers agree bit for bit (an f64 sum in another order rounds
 // to the same f32 except within ~1e-16 of a rounding boundary). The second pass over the row hits L2.
-__global__ void __launch_bounds__(QA_THREADS) rms_norm_q8_kernel(const float* __restrict__ x, const float* __restrict__ w,
-                                                                 const float* __restrict__ b, float eps, QA_OUT, int n, int kind) {
-    __shared__ double part[QA_THREADS / 64];
+// T threads a row: 256 when the rows fill the GPU, 1024 for a few rows (decode), where one block's passes over the
+// row are the whole latency
+template <int T>
+__global__ void __launch_bounds__(T) rms_norm_q8_kernel(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ b,
+                                                        float eps, QA_OUT, int n, int kind) {
+    constexpr int SPAN = 4 * T;
+    __shared__ double part[T / 64];
     const int row = blockIdx.x;
     const float* xr = x + (size_t)row * n;
     double s = 0.0;
-    for (int i = threadIdx.x * 4; i < n; i += QA_SPAN) {
+    for (int i = threadIdx.x * 4; i < n; i += SPAN) {
         const float4 t = *reinterpret_cast<const float4*>(xr + i);
         const float a0 = t.x * t.x, a1 = t.y * t.y, a2 = t.z * t.z, a3 = t.w * t.w;
         s += (double)a0;
@@ -142,13 +146,13 @@ __global__ void __launch_bounds__(QA_THREADS) rms_norm_q8_kernel(const float* __
     __syncthreads();
     double t = 0.0;
 #pragma unroll
-    for (int k = 0; k < QA_THREADS / 64; k++) t += part[k];
+    for (int k = 0; k < T / 64; k++) t += part[k];
     const float ss = (float)(t / (double)n);
     // f32 square root and division, each correctly rounded: evaluated in f64 and rounded once (exact for both
     // operations, since 53 >= 2 * 24 + 2); the f32 intrinsics measured one ulp off on some rows
     const float r = (float)sqrt((double)(ss + eps));
     const float inv = (float)(1.0 / (double)r);
-    for (int base = 0; base < n; base += QA_SPAN) {
+    for (int base = 0; base < n; base += SPAN) {
         const int c0 = base + threadIdx.x * 4;
         const bool in = c0 < n;
         float v[4];
@@ -221,7 +225,10 @@ hipError_t kf_launch_rms_norm_q8(const float* x, const float* w, const float* b,
                                  hipStream_t s) {
     QA_ARGS(act);
     (void)grid;
-    rms_norm_q8_kernel<<<rows, QA_THREADS, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, n, kind);
+    if (rows < 64)
+        rms_norm_q8_kernel<1024><<<rows, 1024, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, n, kind);
+    else
+        rms_norm_q8_kernel<QA_THREADS><<<rows, QA_THREADS, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, n, kind);
     return hipGetLastError();
 }
 
