@@ -222,6 +222,15 @@ def test_moe_ffn_matches_cpu_backend(cuda, ty, rows):
     assert not got[dead].any()
 
 
+@pytest.mark.parametrize("rows", [1, 7, 37])
+def test_moe_ffn_128_experts_top_8(cuda, rows):
+    """128 experts, top-8 (the reference's 128-of-8 MoE test, crates/kf-backend-cuda/tests/moe.rs:79-117): many slots
+    with a few pairs each, many with none."""
+    n_exp, n_embd, n_ff, n_used = 128, 256, 512, 8
+    args, got, stages = _moe_layer(cuda, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows, n_used, 60 + rows)
+    _check_layer(got, stages, args, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows)
+
+
 def test_moe_ffn_config_c5_first_tokens(cuda):
     """Config C5 at full size (8 experts of Q4_K 4096 -> 14336 -> 4096, 16 tokens, top-2): the first two tokens
     against the CPU backend (every token is independent of the others)."""

@@ -376,3 +376,20 @@ def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
         kf.gemv(kf.TYPE_Q8_0, w, one, yr, 1, n, n_out)
         torch.cuda.synchronize()
         _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q8_0, kf.TYPE_Q4_K])
+@pytest.mark.parametrize("rows", [1, 2, 5, 8, 9, 13, 16, 23, 32, 33, 40])
+def test_matmul_reference_row_counts(cuda, ty, rows):
+    """kf_hip_matmul at the row counts of the reference's differential test (crates/kf-backend-cuda/tests/quant.rs:46-64),
+    200 output rows (off the 16-row groups): whichever product the row count selects matches the CPU backend."""
+    n, n_out = 1024, 200
+    w = _weights(ty, n_out, n, 70 + rows)
+    x = kf.synth_normal(71 + rows, 1.0, rows * n).reshape(rows, n)
+    act = kf.alloc_act(rows, n, cuda)
+    import torch
+
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
