@@ -252,13 +252,10 @@ int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float
     // several q8_0 rows are the int8 GEMM, which reads each weight byte once per 128 rows
     if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
         return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
-    // q4_K: the multi-row product streams each weight row once per eight activation rows, the tile GEMM once per 128
-    // rows but with one block per 128 x 128 output tile; the GEMM is taken from 128 rows, or from 32 when it has at
-    // least 96 blocks to spread over the GPU (measured crossovers at the Llama shapes)
-    if (ty == KF_TYPE_Q4_K && n_out > 0) {
-        const int64_t blocks = (int64_t)((n_out + 127) / 128) * ((rows + 127) / 128);
-        if (rows >= 128 || (rows >= 32 && blocks >= 96)) return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
-    }
+    // q4_K: the multi-row product streams each weight row once per 16 activation rows on the matrix cores, the tile
+    // GEMM once per 128 rows; measured at the Llama shapes the multi-row product is faster up to 64 rows (gate at 64
+    // rows: a tie), so the GEMM is taken from 96 rows
+    if (ty == KF_TYPE_Q4_K && n_out > 0 && rows >= 96) return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
 }
 

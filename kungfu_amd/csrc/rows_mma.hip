@@ -353,6 +353,124 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
     return hipGetLastError();
 }
 
+// ------------------------------------------------------------------------------------------ one-slot form
+// The few-row product of one matrix (no slots) has too few 16-row tiles to give every wave its own, and staging the
+// activation rows per block would cost as much as the block's weights. Here a block's eight waves split K over
+// TILES tiles (KP = 8 / TILES waves a tile, each taking super-blocks kpart, kpart + KP, ...), and each wave fetches,
+// per super-block, its tile's weights and exactly the activation data it multiplies them with (16 rows x 256 int8
+// columns in MFMA order, their 32-column sums and scales) by DMA into one of its two LDS buffers: nine DMA
+// instructions a super-block for every wave. (Operand loads into registers instead made the compiler copy the loaded
+// registers at every loop pass, waiting for all loads in flight.) The KP partials of a tile are summed in LDS in
+// kpart order (deterministic). Rows run in chunks of 16.
+constexpr int RD_A = RM_TILE_BYTES, RD_S = RD_A + 8 * 16 * 32, RD_D = RD_S + 16 * 8 * 4, RD_BUF = RD_D + 16 * 4 + 64;  // 7104 bytes
+
+template <int TILES>
+__global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                                const int32_t* __restrict__ xs32, const float* __restrict__ xd32, int n, int n_out,
+                                                                int rows, const float* __restrict__ bias, const float* __restrict__ res,
+                                                                float* __restrict__ y) {
+    constexpr int KP = RM_WAVES / TILES;
+    __shared__ __align__(16) uint8_t pk0[RM_WAVES * RD_BUF];
+    __shared__ __align__(16) uint8_t pk1[RM_WAVES * RD_BUF];
+    __shared__ __align__(16) rm_v4f part[RM_WAVES * 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tl = wave / KP, kpart = wave % KP;
+    const int c = lane & 15, q = lane >> 4;
+    const int nsb = n / KF_Q4_K_BLOCK, nsum = n / 32;
+    const int orow = (blockIdx.x * TILES + tl) * 16;  // the wave's tile
+    const int items = nsb > kpart ? (nsb - kpart + KP - 1) / KP : 0;
+
+    const auto rw = kf_rsrc(w, (uint64_t)n_out * row_bytes);  // rows past n_out read as zeros
+    int vpk[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const int s2 = min(64 * i + lane, 143);
+        vpk[i] = (s2 / 9) * (int)row_bytes + 16 * (s2 % 9);
+    }
+
+    for (int c0 = 0; c0 < rows; c0 += 16) {
+        const int R = min(16, rows - c0);
+        // activation sources of the chunk (rows past R repeat row R - 1): A pieces (instruction i: groups 2 i, 2 i + 1;
+        // lane l: group 2 i + l / 32, row (l / 2) % 16, half l % 2), sums (lane l < 32: row l / 2, four sums from 4 (l % 2)),
+        // scales (lane l < 16: row l)
+        const auto rx = kf_rsrc(xq + (int64_t)c0 * n, (uint64_t)R * n);
+        const auto rs = kf_rsrc(xs32 + (int64_t)c0 * nsum, (uint64_t)R * nsum * 4);
+        const auto rd = kf_rsrc(xd32 + (int64_t)c0 * nsum, (uint64_t)R * nsum * 4);
+        int va[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) va[i] = min((lane >> 1) & 15, R - 1) * n + 32 * (2 * i + (lane >> 5)) + 16 * (lane & 1);
+        const int vs = min(lane >> 1 & 15, R - 1) * nsum * 4 + 16 * (lane & 1);
+        const int vd = min(lane & 15, R - 1) * nsum * 4;
+        auto park = [&](int j, uint8_t* buf) {
+            const int sb = kpart + KP * j;
+            const int so = orow * (int)row_bytes + sb * KF_Q4_K_BYTES;
+            uint8_t* b = buf + wave * RD_BUF;
+            kf_bdma16(rw, vpk[0], so, b);
+            kf_bdma16(rw, vpk[1], so, b + 1024);
+            if (lane < 16) kf_bdma16(rw, vpk[2], so, b + 2048);
+#pragma unroll
+            for (int i = 0; i < 4; i++) kf_bdma16(rx, va[i], sb * KF_Q4_K_BLOCK, b + RD_A + 1024 * i);
+            if (lane < 32) kf_bdma16(rs, vs, sb * 32, b + RD_S);
+            if (lane < 16) kf_bdma4(rd, vd, sb * 32, b + RD_D);
+        };
+        constexpr int NI = 9;  // DMA instructions a super-block, every wave
+        rm_v4f acc = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (items > 0) park(0, pk0);
+        if (items > 1) park(1, pk1);
+        auto step = [&](uint8_t* buf, int j) {
+            if (j + 1 < items)
+                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
+            else
+                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+            const uint8_t* b = buf + wave * RD_BUF;
+            RmW v;
+            v.hd = *reinterpret_cast<const rm_v4u*>(b + c * KF_Q4_K_BYTES);
+#pragma unroll
+            for (int p = 0; p < 4; p++) v.q[p] = *reinterpret_cast<const rm_v2u*>(b + c * KF_Q4_K_BYTES + 16 + 32 * p + 8 * q);
+            const int2 bs = *reinterpret_cast<const int2*>(b + RD_S + (c * 8 + 2 * q) * 4);
+            const rm_v4f dx = *reinterpret_cast<const rm_v4f*>(b + RD_D + 16 * q);
+            rm_v4h xo;
+            xo[0] = (_Float16)(float)(bs.x >> 6);
+            xo[1] = (_Float16)(float)(bs.x & 63);
+            xo[2] = (_Float16)(float)(bs.y >> 6);
+            xo[3] = (_Float16)(float)(bs.y & 63);
+            rm_v4i S;
+            rm_v4f mins;
+            rm_block(v, b + RD_A + c * 32 + 8 * q, 16 * 32, xo, q, S, mins);
+            const float d = kf_h2f(v.hd.x & 0xffffu), dm = kf_h2f(v.hd.x >> 16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], fmaf(-dm, mins[e], d * (float)S[e]), acc[e]);
+            if (j + 2 < items) {
+                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));  // this buffer's reads are done
+                park(j + 2, buf);
+            }
+        };
+        for (int it = 0; it < items; it += 2) {
+            step(pk0, it);
+            if (it + 1 < items) step(pk1, it + 1);
+        }
+        // the KP partials of each tile, in kpart order
+        part[wave * 64 + lane] = acc;
+        __syncthreads();
+        if (kpart == 0) {
+            rm_v4f t = part[(tl * KP) * 64 + lane];
+#pragma unroll
+            for (int k = 1; k < KP; k++) t += part[(tl * KP + k) * 64 + lane];
+            const int o = orow + c;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = 4 * q + e;
+                if (m < R && o < n_out) {
+                    const int64_t at = (int64_t)(c0 + m) * n_out + o;
+                    y[at] = t[e] + (bias ? bias[o] : 0.0f) + (res ? res[at] : 0.0f);
+                }
+            }
+        }
+        __syncthreads();  // before the next chunk reuses the partials and buffers
+    }
+}
+
 }  // namespace
 
 // Whether the matrix-core product takes this launch: it needs 16-byte aligned weight rows (q4_K always), matrices
@@ -386,4 +504,28 @@ hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_byte
     KF_RM_NB(false, 8);
 #undef KF_RM_NB
 #undef KF_RM
+}
+
+// Host launcher of the one-slot q4_K few-row product (rows_mma_1_kernel), validated by the caller: n a multiple of
+// 256, the matrix below 2 GB. Tiles per block chosen so the grid has about one block per CU or more.
+hipError_t kf_launch_rows_mma_1(const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n, int n_out,
+                                int rows, const float* bias, const float* res, float* y, hipStream_t s) {
+    if ((int64_t)n_out * row_bytes >= (1ll << 31) || (int64_t)rows * n >= (1ll << 31)) return hipErrorInvalidValue;
+    const int tiles = (n_out + 15) / 16;
+    static const int forced = [] {  // KF_RM1_TILES: a tuning knob (1, 2, 4 or 8 tiles a block)
+        const char* e = getenv("KF_RM1_TILES");
+        return e ? atoi(e) : 0;
+    }();
+    const int tpb = forced == 1 || forced == 2 || forced == 4 || forced == 8 ? forced : tiles >= 4 * 256 ? 4 : tiles >= 2 * 256 ? 2 : 1;
+    const auto* wb = static_cast<const uint8_t*>(w);
+#define KF_R1(T)                                                                                                   \
+    {                                                                                                              \
+        rows_mma_1_kernel<T><<<(tiles + T - 1) / T, RM_THREADS, 0, s>>>(wb, row_bytes, xq, xs32, xd32, n, n_out, rows, bias, res, y); \
+        return hipGetLastError();                                                                                  \
+    }
+    if (tpb == 8) KF_R1(8)
+    if (tpb == 4) KF_R1(4)
+    if (tpb == 2) KF_R1(2)
+    KF_R1(1)
+#undef KF_R1
 }
