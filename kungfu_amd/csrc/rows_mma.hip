@@ -134,13 +134,12 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
     const RmLds L = rm_lds(kc, RT);
     const int c = lane & 15, q = lane >> 4;
 
-    // weights: one buffer resource over the slot's matrix (rows past it read as zeros); DMA instruction i of a
-    // super-block moves the 16-byte pieces s = 64 i + lane of the tile's 16 rows x 144 bytes (row s / 9, piece s % 9;
-    // the third instruction only on lanes below 16): 3 instructions per matrix, the tile row and super-block adding
-    // row * row_bytes + sb * 144 as a scalar offset
+    // weights: a buffer resource from the tile's first row to the slot matrix's last (rows past it read as zeros);
+    // DMA instruction i of a super-block moves the 16-byte pieces s = 64 i + lane of the tile's 16 rows x 144 bytes
+    // (row s / 9, piece s % 9; the third instruction only on lanes below 16): 3 instructions per matrix, the
+    // super-block adding sb * 144 as a scalar offset
     const uint8_t* wbase = w + (int64_t)slot * expert_bytes;
-    const auto rw = kf_rsrc(wbase, (uint64_t)n_out * row_bytes);
-    const auto ru = kf_rsrc(GLU ? w2 + (int64_t)slot * expert_bytes : wbase, (uint64_t)n_out * row_bytes);
+    const uint8_t* ubase = GLU ? w2 + (int64_t)slot * expert_bytes : wbase;
     int vpk[3];
 #pragma unroll
     for (int i = 0; i < 3; i++) {
@@ -151,11 +150,16 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
     const int my_tiles = tiles > wave ? (tiles - wave + RM_WAVES - 1) / RM_WAVES : 0;
     auto park = [&](int sb0, int nsbp, int it, uint8_t* buf) {
         const int t = wave + (it / nsbp) * RM_WAVES, sb = sb0 + it % nsbp;
-        const int so = (o0 + 16 * t) * (int)row_bytes + sb * KF_Q4_K_BYTES;
+        // the resource starts at the tile's first row and ends at the matrix's last, so the hardware range check on
+        // the per-lane offset returns zeros for the tile's rows past n_out instead of reading past the matrix
+        const int trow = o0 + 16 * t;
+        const int64_t tb = (int64_t)trow * row_bytes;
+        const uint64_t left = (uint64_t)(n_out - trow) * row_bytes;
+        const int so = sb * KF_Q4_K_BYTES;
 #pragma unroll
         for (int k = 0; k < NW; k++) {
             uint8_t* b = buf + (wave * NW + k) * RM_TILE_BYTES;
-            const auto r = k == 0 ? rw : ru;
+            const auto r = kf_rsrc((k == 0 ? wbase : ubase) + tb, left);
             kf_bdma16(r, vpk[0], so, b);
             kf_bdma16(r, vpk[1], so, b + 1024);
             if (lane < 16) kf_bdma16(r, vpk[2], so, b + 2048);
@@ -381,7 +385,10 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
     const int orow = (blockIdx.x * TILES + tl) * 16;  // the wave's tile
     const int items = nsb > kpart ? (nsb - kpart + KP - 1) / KP : 0;
 
-    const auto rw = kf_rsrc(w, (uint64_t)n_out * row_bytes);  // rows past n_out read as zeros
+    // the resource starts at the wave's tile (the last tile's start for a wave past n_out) and ends at the matrix's
+    // last row: the hardware range check on the per-lane offset returns zeros for rows past n_out
+    const int trow = min(orow, (n_out - 1) & ~15);
+    const auto rw = kf_rsrc(w + (int64_t)trow * row_bytes, (uint64_t)(n_out - trow) * row_bytes);
     int vpk[3];
 #pragma unroll
     for (int i = 0; i < 3; i++) {
@@ -404,7 +411,7 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
         const int vd = min(lane & 15, R - 1) * nsum * 4;
         auto park = [&](int j, uint8_t* buf) {
             const int sb = kpart + KP * j;
-            const int so = orow * (int)row_bytes + sb * KF_Q4_K_BYTES;
+            const int so = sb * KF_Q4_K_BYTES;
             uint8_t* b = buf + wave * RD_BUF;
             kf_bdma16(rw, vpk[0], so, b);
             kf_bdma16(rw, vpk[1], so, b + 1024);
@@ -529,3 +536,4 @@ hipError_t kf_launch_rows_mma_1(const void* w, int64_t row_bytes, const int8_t* 
     KF_R1(1)
 #undef KF_R1
 }
+
