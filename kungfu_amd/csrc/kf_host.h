@@ -21,3 +21,18 @@ inline hipError_t kf_raise_lds(const void* fn, int bytes) {
     if (e == hipSuccess) cur = bytes;
     return e;
 }
+
+// Compute units of the current device, read once per device and remembered under a lock (256 if the query fails).
+inline int kf_cu_count() {
+    static std::mutex mu;
+    static std::map<int, int> cus;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    std::lock_guard<std::mutex> g(mu);
+    auto it = cus.find(dev);
+    if (it != cus.end()) return it->second;
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
+    cus[dev] = v;
+    return v;
+}

@@ -523,7 +523,19 @@ hipError_t kf_launch_rows_mma_1(const void* w, int64_t row_bytes, const int8_t* 
         const char* e = getenv("KF_RM1_TILES");
         return e ? atoi(e) : 0;
     }();
-    const int tpb = forced == 1 || forced == 2 || forced == 4 || forced == 8 ? forced : tiles >= 4 * 256 ? 4 : tiles >= 2 * 256 ? 2 : 1;
+    // a block's two stage buffers per wave hold most of a CU's LDS, so one block runs per CU: the fewest tiles a block
+    // whose grid still fits in one round of the CUs (QKV at 4096 x 6144: 192 blocks of two tiles, 8.5 us at 8 rows,
+    // against 384 blocks of one tile in two rounds, 10.7 us)
+    int tpb = forced == 1 || forced == 2 || forced == 4 || forced == 8 ? forced : 0;
+    if (tpb == 0) {
+        const int cus = kf_cu_count();
+        tpb = 8;
+        for (int t = 1; t < 8; t *= 2)
+            if ((tiles + t - 1) / t <= cus) {
+                tpb = t;
+                break;
+            }
+    }
     const auto* wb = static_cast<const uint8_t*>(w);
 #define KF_R1(T)                                                                                                   \
     {                                                                                                              \

@@ -393,3 +393,19 @@ def test_matmul_reference_row_counts(cuda, ty, rows):
     kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+@pytest.mark.parametrize("n_out", [4104, 8232, 16400])
+def test_matmul_q4_k_few_rows_tiles_per_block(cuda, n_out):
+    """q4_K few-row product of one matrix with two, four and eight 16-row tiles a block (the tile count follows the
+    number of tiles against the CU count; ragged last tile) against the CPU backend's matmul_slice."""
+    import torch
+
+    ty, n, rows = kf.TYPE_Q4_K, 1024, 8
+    w = _weights(ty, n_out, n, n_out)
+    x = kf.synth_normal(n_out + 1, 1.0, rows * n).reshape(rows, n)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
