@@ -243,6 +243,24 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
 
 }  // extern "C"
 
+// q4_K: whether the tile GEMM beats the few-row product. The few-row product streams the weights once per 16
+// activation rows: about 0.28 us per MB and pass plus 1 us. A GEMM block computes a 128 x 128 tile over all of K, about
+// 12 us per 1024 columns, and its grid runs in rounds of one block a CU. Fitted at the Llama shapes, 8-256 rows:
+// QKV and O keep the few-row product to 128 and 192 rows, gate takes the GEMM from 96 rows, down (32 column tiles
+// against 14336 columns) keeps the few-row product to 256 rows.
+// Rows wider than the few-row product stages go one GEMV launch per row, so the GEMM takes them from 96 rows.
+static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
+    if (rows < 64) return false;
+    if (n_in > kf_rows_max_n(KF_TYPE_Q4_K)) return rows >= 96;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    const double mb = (double)n_out * row_bytes / 1e6;
+    const double t_rows = ((rows + 15) / 16) * (0.28 * mb + 1.0);
+    const int64_t blocks = (int64_t)((n_out + 127) / 128) * ((rows + 127) / 128);
+    const double t_gemm = 12.0 * n_in / 1024.0 * (double)((blocks + cus - 1) / cus);
+    return t_gemm < t_rows;
+}
+
 namespace {
 
 // The product of kf_hip_matmul once the activations are quantized
@@ -252,10 +270,8 @@ int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float
     // several q8_0 rows are the int8 GEMM, which reads each weight byte once per 128 rows
     if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
         return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
-    // q4_K: the multi-row product streams each weight row once per 16 activation rows on the matrix cores, the tile
-    // GEMM once per 128 rows; measured at the Llama shapes the multi-row product is faster up to 64 rows (gate at 64
-    // rows: a tie), so the GEMM is taken from 96 rows
-    if (ty == KF_TYPE_Q4_K && n_out > 0 && rows >= 96) return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+    if (ty == KF_TYPE_Q4_K && n_out > 0 && q4k_gemm_pays(rows, n_in, n_out, rb))
+        return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
 }
 

@@ -409,3 +409,19 @@ def test_matmul_q4_k_few_rows_tiles_per_block(cuda, n_out):
     kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+@pytest.mark.parametrize("rows", [96, 128, 192, 256])
+def test_matmul_q4_k_many_rows(cuda, rows):
+    """kf_hip_matmul on q4_K between the few-row product and the tile GEMM (the cost model picks either, ragged
+    n_out) against the CPU backend's matmul_slice."""
+    import torch
+
+    ty, n, n_out = kf.TYPE_Q4_K, 1024, 200
+    w = _weights(ty, n_out, n, 90 + rows)
+    x = kf.synth_normal(91 + rows, 1.0, rows * n).reshape(rows, n)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
