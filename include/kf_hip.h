@@ -125,7 +125,8 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
                    int rows, int n, int n_out, void* stream);
 
 /* The whole Op::MatMul of one weight: quantize x into `act` (device scratch of kf_hip_act_bytes(rows, n_in)) and run
- * the product the row count selects. Replaces matmul_launch (exec.rs:2061-2093). */
+ * the product the row count and shape select (q4_K: the few-row product or the tile GEMM, whichever a cost model
+ * fitted on MI355X favours). Replaces matmul_launch (exec.rs:2061-2093). */
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream);
 
