@@ -179,7 +179,8 @@ size_t kf_hip_moe_scratch_bytes(int rows, int n_used, int n_embd, int n_ff, int 
 
 /* The routed expert layer with silu gating: quantize x, group the pairs, fused gate/up product, quantize the hidden
  * rows, down product, weighted combine. gate and up are [n_slots][n_ff][row of n_embd], down [n_slots][n_embd][row
- * of n_ff], all of type ty. out [rows][n_embd]. Replaces expert_launches (crates/kf-backend-cuda/src/exec.rs:2378-2386)
+ * of n_ff], all of type ty. out [rows][n_embd]. A pair whose slot is outside [0, n_slots) contributes nothing (the
+ * grouping skips it and so does the combine). Replaces expert_launches (crates/kf-backend-cuda/src/exec.rs:2378-2386)
  * for int8-capable experts resident on the device. */
 int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* down, int n_slots, int n_embd, int n_ff, const float* x, int rows,
                    const int32_t* sel, const float* wts, int n_used, float scale, void* scratch, size_t scratch_bytes, float* out, void* stream);

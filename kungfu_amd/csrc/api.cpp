@@ -5,6 +5,8 @@
 // product kernel chosen by the number of activation rows.
 #include <hip/hip_runtime.h>
 
+#include <climits>
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -12,6 +14,7 @@
 #include <vector>
 
 #include "../../include/kf_hip.h"
+#include "kf_host.h"
 #include "kf_layout.h"
 
 static_assert(KF_HIP_MAX_SEGMENTS == KF_MAX_SEGS, "one segment limit");
@@ -41,7 +44,7 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
                           const float* bias, const float* res, float* y, hipStream_t s);
 hipError_t kf_launch_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, hipStream_t s);
 hipError_t kf_launch_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used,
-                                 int n_embd, float scale, hipStream_t s);
+                                 int n_embd, float scale, int n_slots, hipStream_t s);
 
 namespace {
 
@@ -252,8 +255,7 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
 static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
     if (rows < 64) return false;
     if (n_in > kf_rows_max_n(KF_TYPE_Q4_K)) return rows >= 96;
-    int dev = 0, cus = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1) cus = 256;
+    const int cus = kf_cu_count();
     const double mb = (double)n_out * row_bytes / 1e6;
     const double t_rows = ((rows + 15) / 16) * (0.28 * mb + 1.0);
     const int64_t blocks = (int64_t)((n_out + 127) / 128) * ((rows + 127) / 128);
@@ -401,7 +403,8 @@ int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots
                        float scale, void* stream) {
     if (rows < 0 || n_used < 1 || n_embd < 0) return fail(KF_E_INVALID, "%d rows, %d used, %d columns", rows, n_used, n_embd);
     if (rows > 0 && n_embd > 0 && (!part || !wts || !slots || !out)) return fail(KF_E_INVALID, "null combine pointer");
-    const hipError_t e = kf_launch_moe_combine(part, wts, slots, host, out, rows, n_used, n_embd, scale, static_cast<hipStream_t>(stream));
+    // every pair with a slot >= 0 has a part row: the caller wrote them
+    const hipError_t e = kf_launch_moe_combine(part, wts, slots, host, out, rows, n_used, n_embd, scale, INT_MAX, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "moe_combine launch");
 }
 
@@ -465,7 +468,12 @@ int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* do
         rc = kf_hip_moe_gemv(ty, gate, up, eb_gu, rb_in, xact, rows, n_embd, n_ff, order, offsets, n_slots, n_used, 0, hidden, stream);
     if (rc == KF_OK) rc = kf_hip_quant_act(hidden, hact, pairs, n_ff, kind_of(ty), stream);
     if (rc == KF_OK) rc = kf_hip_moe_gemv(ty, down, nullptr, eb_dn, rb_ff, hact, pairs, n_ff, n_embd, order, offsets, n_slots, n_used, 1, part, stream);
-    if (rc == KF_OK) rc = kf_hip_moe_combine(part, wts, sel, nullptr, out, rows, n_used, n_embd, scale, stream);
+    // moe_group skips pairs whose slot is n_slots or more, so their part rows are never written: the combine skips them
+    // too rather than reading stale scratch
+    if (rc == KF_OK) {
+        const hipError_t e = kf_launch_moe_combine(part, wts, sel, nullptr, out, rows, n_used, n_embd, scale, n_slots, static_cast<hipStream_t>(stream));
+        if (e != hipSuccess) rc = hip_fail(e, "moe_combine launch");
+    }
     return rc;
 }
 

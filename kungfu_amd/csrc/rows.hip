@@ -355,18 +355,19 @@ __global__ void __launch_bounds__(256) moe_group_kernel(const int32_t* __restric
     }
 }
 
-// out[r][o] = sum over j of the row's pairs rj = r * n_used + j with slots[rj] >= 0 of wts[rj] * scale * part[rj][o]
-// (+ host[r][o]), j in order
+// out[r][o] = sum over j of the row's pairs rj = r * n_used + j with 0 <= slots[rj] < n_slots of
+// wts[rj] * scale * part[rj][o] (+ host[r][o]), j in order; pairs outside the slots were skipped by the grouping, so
+// their part rows were never written
 __global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ part, const float* __restrict__ wts, const int32_t* __restrict__ slots,
                                                           const float* __restrict__ host, float* __restrict__ out, int rows, int n_used, int n_embd,
-                                                          float scale) {
+                                                          float scale, int n_slots) {
     const int64_t total = (int64_t)rows * n_embd;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / n_embd, o = i - r * n_embd;
         float acc = 0.0f;
         for (int j = 0; j < n_used; j++) {
             const int64_t rj = r * n_used + j;
-            if (slots[rj] >= 0) acc += wts[rj] * scale * part[rj * n_embd + o];
+            if (slots[rj] >= 0 && slots[rj] < n_slots) acc += wts[rj] * scale * part[rj * n_embd + o];
         }
         out[i] = acc + (host ? host[i] : 0.0f);
     }
@@ -472,10 +473,10 @@ hipError_t kf_launch_moe_group(const int32_t* slots, int total, int n_slots, int
 }
 
 hipError_t kf_launch_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used,
-                                 int n_embd, float scale, hipStream_t s) {
+                                 int n_embd, float scale, int n_slots, hipStream_t s) {
     const int64_t total = (int64_t)rows * n_embd;
     if (total == 0) return hipSuccess;
     const int grid = (int)std::min<int64_t>((total + 255) / 256, 4096);
-    moe_combine_kernel<<<grid, 256, 0, s>>>(part, wts, slots, host, out, rows, n_used, n_embd, scale);
+    moe_combine_kernel<<<grid, 256, 0, s>>>(part, wts, slots, host, out, rows, n_used, n_embd, scale, n_slots);
     return hipGetLastError();
 }

@@ -256,3 +256,32 @@ def test_multi_row_gemv_matches_cpu_backend(cuda, ty, n, rows):
     kf.gemv(ty, _t(w, cuda), act, y, rows, n, n_out, bias=_t(bias, cuda), res=_t(res, cuda))
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x, bias) + res)
+
+
+def test_moe_ffn_skips_slots_past_the_end(cuda):
+    """kf_hip_moe_ffn with routed ids of n_slots or more: the grouping skips such pairs, and the layer's output equals
+    the same layer with those pairs unused (-1), bit for bit, rather than reading scratch the products never wrote."""
+    import torch
+
+    ty, n_exp, n_embd, n_ff, rows, n_used = kf.TYPE_Q4_K, 4, 512, 768, 9, 2
+    gate = _experts(ty, n_exp, n_ff, n_embd, 90)
+    up = _experts(ty, n_exp, n_ff, n_embd, 91)
+    down = _experts(ty, n_exp, n_embd, n_ff, 92)
+    x = kf.synth_normal(93, 1.0, rows * n_embd).reshape(rows, n_embd)
+    sel, wts = _routing(rows, n_used, n_exp, 94)
+    sel_far = sel.copy()
+    sel_far[::3, 1] = n_exp + 5
+    sel_far[4, 0] = n_exp
+    sel_none = np.where(sel_far >= n_exp, -1, sel_far).astype(np.int32)
+    g_, u_, d_, x_, w_ = (_t(a, cuda) for a in (gate, up, down, x, wts))
+    scratch = torch.empty(kf.moe_scratch_bytes(rows, n_used, n_embd, n_ff, n_exp), dtype=torch.uint8, device=cuda)
+    outs = []
+    for s in (sel_none, sel_far):
+        # fill the scratch with NaN bytes first, so a read of an unwritten part row shows
+        scratch.fill_(0xFF)
+        out = torch.full((rows, n_embd), float("nan"), device=cuda)
+        kf.moe_ffn(ty, g_, u_, d_, n_exp, n_embd, n_ff, x_, _t(s, cuda), w_, out, scratch)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0], outs[1])

@@ -315,7 +315,7 @@ def test_gemm_q4_k_random_blocks_and_extreme_sums(cuda):
 @pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
 def test_gemm_q4_k_prefill_shapes_match_gemv(cuda, n, n_out):
     """Q4_K at the Llama-3-8B shapes and M = 2048: every 97th row of the GEMM against the GEMV of that row on the same
-    quantized activations (the GEMV is pinned to the CPU backend above)."""
+    quantized activations, and the sampled rows against the CPU backend's matmul_slice (rows are independent)."""
     import torch
 
     rows = 2048
@@ -335,6 +335,10 @@ def test_gemm_q4_k_prefill_shapes_match_gemv(cuda, n, n_out):
         kf.gemv(kf.TYPE_Q4_K, w, one, yr, 1, n, n_out)
         torch.cuda.synchronize()
         _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())
+    # rows are independent: the sampled rows against the CPU backend itself
+    sample = list(range(0, rows, 97))
+    want = oracle.matmul_slice(kf.TYPE_Q4_K, w.cpu().numpy(), n, n_out, x[sample].cpu().numpy())
+    _close(y[sample].cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("rows,n_out", [(9, 96), (40, 96), (40, 12300), (200, 96)])
@@ -356,7 +360,7 @@ def test_matmul_q4_k_many_rows(cuda, rows, n_out):
 @pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
 def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
     """Config C4 at full size (M = 2048): every 97th row of the GEMM against the GEMV of that row on the same
-    quantized activations (the GEMV is pinned to the CPU backend above); the CPU oracle is too slow at this size."""
+    quantized activations, and the sampled rows against the CPU backend's matmul_slice (rows are independent)."""
     import torch
 
     rows = 2048
@@ -376,6 +380,10 @@ def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
         kf.gemv(kf.TYPE_Q8_0, w, one, yr, 1, n, n_out)
         torch.cuda.synchronize()
         _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())
+    # rows are independent: the sampled rows against the CPU backend itself
+    sample = list(range(0, rows, 97))
+    want = oracle.matmul_slice(kf.TYPE_Q8_0, w.cpu().numpy(), n, n_out, x[sample].cpu().numpy())
+    _close(y[sample].cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("ty", [kf.TYPE_Q8_0, kf.TYPE_Q4_K])
@@ -412,7 +420,7 @@ def test_matmul_q4_k_few_rows_tiles_per_block(cuda, n_out):
 
 
 @pytest.mark.parametrize("rows", [96, 128, 192, 256])
-def test_matmul_q4_k_many_rows(cuda, rows):
+def test_matmul_q4_k_cost_model_rows(cuda, rows):
     """kf_hip_matmul on q4_K between the few-row product and the tile GEMM (the cost model picks either, ragged
     n_out) against the CPU backend's matmul_slice."""
     import torch
@@ -425,3 +433,28 @@ def test_matmul_q4_k_many_rows(cuda, rows):
     kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+LLAMA_SHAPES = {"qkv": (4096, 6144), "o": (4096, 4096), "gate": (4096, 14336), "down": (14336, 4096)}
+
+
+@pytest.mark.parametrize("shape", list(LLAMA_SHAPES))
+@pytest.mark.parametrize("rows", [8, 16, 32, 64])
+def test_matmul_q8_0_small_batch_llama_shapes(cuda, shape, rows):
+    """Config C3: kf_hip_matmul on Q8_0 weights at the Llama-3-8B shapes and 8 / 16 / 32 / 64 activation rows (the
+    small-batch product), every 7th output column against the CPU backend's matmul_slice on those weight rows (output
+    columns are independent) (crates/kf-backend-cuda/tests/quant.rs:46-112)."""
+    import torch
+
+    n, n_out = LLAMA_SHAPES[shape]
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=200 + n_out)
+    x = kf.synth_normal(201 + rows, 1.0, rows * n).reshape(rows, n)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.matmul(kf.TYPE_Q8_0, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    cols = np.arange(0, n_out, 7)
+    want = oracle.matmul_slice(kf.TYPE_Q8_0, np.ascontiguousarray(w[cols]), n, len(cols), x)
+    got = y.cpu().numpy()
+    assert np.isfinite(got).all()
+    _close(got[:, cols], want)
