@@ -130,6 +130,21 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream);
 
+/* kf_hip_matmul without the `act` argument, for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The activation
+ * scratch is a static device array of KF_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the process
+ * ends; the call allocates nothing (no hipMalloc / hipFree / allocating library routine). Calls whose activations need
+ * more (kf_hip_act_bytes(rows, n_in) > KF_NOALLOC_SCRATCH_BYTES, e.g. above 2048 x 16384) fail with KF_E_INVALID.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams, two threads) race, so
+ * callers serialise them (one stream per GPU, or events). The array keeps the last call's contents; nothing in it needs
+ * to start at zero (each call overwrites what it reads). */
+#define KF_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, const float* bias,
+                          const float* res, float* y, void* stream);
+
+/* KF_NOALLOC_SCRATCH_BYTES of the loaded library. No reference counterpart. */
+size_t kf_hip_noalloc_scratch_bytes(void);
+
 /* Grouped products sharing one input (Q/K/V, or gate and up stored as separate tensors): up to KF_HIP_MAX_SEGMENTS
  * weight matrices of one type and row width stacked along their output rows. The segment table is the reference's
  * (quant.cuh:301-305, built by matmul_group_launch, exec.rs:1305-1314), KF_SEG_WORDS int64 words per member in HOST

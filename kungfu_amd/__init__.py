@@ -72,6 +72,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_gated_act_q8": ([P, P, I, I, I, I, I, P, P], I),
         "kf_hip_gemv": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_matmul": ([U, P, I, I, P, I, P, P, P, P, P], I),
+        "kf_hip_matmul_noalloc": ([U, P, I, I, P, I, P, P, P, P], I),
+        "kf_hip_noalloc_scratch_bytes": ([], S),
         "kf_hip_gemv_group": ([U, P, L64, P, P, I, I, P, I, P], I),
         "kf_hip_matmul_group": ([U, P, I, P, I, P, P, P, I, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
@@ -222,6 +224,12 @@ def gemm_i8(ty: int, w, act, y, rows: int, n: int, n_out: int, bias=None, res=No
 def matmul(ty: int, w, x, act, y, n_out: int, bias=None, res=None, stream=None) -> None:
     rows, n = x.shape
     check(lib().kf_hip_matmul(ty, _ptr(w), n, n_out, _ptr(x), rows, _ptr(act), _ptr(bias), _ptr(res), _ptr(y), _stream(stream)))
+
+
+def matmul_noalloc(ty: int, w, x, y, n_out: int, bias=None, res=None, stream=None) -> None:
+    """kf_hip_matmul_noalloc: kf_hip_matmul with the library's static per-GPU activation scratch (no allocation)."""
+    rows, n = x.shape
+    check(lib().kf_hip_matmul_noalloc(ty, _ptr(w), n, n_out, _ptr(x), rows, _ptr(bias), _ptr(res), _ptr(y), _stream(stream)))
 
 
 SEG_NONE = -(1 << 63)

@@ -1,0 +1,71 @@
+// kf_hip_matmul_noalloc: kf_hip_matmul for callers that cannot allocate device memory (code under HIP graph capture,
+// tight serving loops, harnesses that forbid hipMalloc). The activation scratch that kf_hip_matmul takes as an
+// argument is instead a file-scope device array of KF_NOALLOC_SCRATCH_BYTES, one copy per GPU, held until the process
+// ends. No reference counterpart.
+//
+// In host code the array's name is only a host-side stand-in, not a device address: every host use goes through the
+// device address that hipGetSymbolAddress returns, looked up once per device (with that device current) on the
+// device's first call and kept per device.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "../../include/kf_hip.h"
+#include "kf_layout.h"
+
+void kf_set_error(const char* fmt, ...);
+
+namespace {
+
+static __device__ __align__(256) uint8_t scratch[KF_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+
+// The device address of `scratch` on `dev` (looked up on first use), or nullptr with the error recorded
+void* scratch_ptr(int dev) {
+    static std::mutex mu;
+    static void* ptr[kMaxDevices] = {};
+    if (dev < 0 || dev >= kMaxDevices) {
+        kf_set_error("device %d: at most %d devices", dev, kMaxDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(mu);
+    if (!ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            kf_set_error("hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+            return nullptr;
+        }
+        ptr[dev] = p;
+    }
+    return ptr[dev];
+}
+
+}  // namespace
+
+extern "C" size_t kf_hip_noalloc_scratch_bytes(void) { return KF_NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, const float* bias,
+                                     const float* res, float* y, void* stream) {
+    if (rows < 0 || n_in <= 0) {
+        kf_set_error("%d rows of %d columns", rows, n_in);
+        return KF_E_INVALID;
+    }
+    const size_t need = kf_hip_act_bytes(rows, n_in);
+    if (need > KF_NOALLOC_SCRATCH_BYTES) {
+        kf_set_error("%d rows of %d columns need %zu bytes of activation scratch, the no-allocation entry point holds %zu", rows, n_in, need,
+                     (size_t)KF_NOALLOC_SCRATCH_BYTES);
+        return KF_E_INVALID;
+    }
+    int dev = 0;
+    const hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        kf_set_error("hipGetDevice: %s", hipGetErrorString(e));
+        return KF_E_HIP;
+    }
+    void* act = scratch_ptr(dev);
+    if (!act) return KF_E_HIP;
+    // quant_act writes every byte of the scratch that the product reads, so nothing is cleared between calls
+    return kf_hip_matmul(ty, w, n_in, n_out, x, rows, act, bias, res, y, stream);
+}
