@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define KF_HIP_ABI_VERSION 1
+#define KF_HIP_ABI_VERSION 2
 
 /* ggml type ids (crates/kf-quant/src/types/q8_0.rs:4, q4_k.rs:4, q5_k.rs:4, q6_k.rs:4) */
 #define KF_TYPE_Q8_0 8u
@@ -54,16 +54,21 @@ const char* kf_hip_last_error(void);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Activation quantization.
- * The int8 activation scratch of `rows` rows of `n` columns (the reference's ActI8, crates/kf-quant/src/lib.rs:48-78,
- * as laid out on the device by act_scratch_all, crates/kf-backend-cuda/src/kf8.rs:338-357):
+ * The int8 activation scratch of `rows` rows of `n` columns (the reference's ActI8, crates/kf-quant/src/lib.rs:48-78):
  *   q int8 [rows][n] | d16 f32 [rows][n/16] | s16 int32 [rows][n/16] | d32 f32 [rows][n/32] | s32 int32 [rows][n/32]
- * each section 256-byte aligned from the base. */
+ *   | xa f16 [rows][ceil(n/256)][16]
+ * each section 256-byte aligned from the base. xa (Q8K kind only) holds per 256 columns the eight per-32 sums split as
+ * hi = floor(s / 64), lo = s - 64 hi (hi first), the operand of the q4_K GEMM's mins product.
+ * This is NOT the reference's device layout act_scratch_all (crates/kf-backend-cuda/src/kf8.rs:338-357): that one
+ * aligns sections to 16 bytes, keeps the sums as f32 and its fragment array xa in another form. A port sizes and
+ * offsets this scratch with kf_hip_act_bytes / kf_hip_act_offsets, never with act_scratch_bytes. The integers and
+ * scales themselves are the reference's, bit for bit. */
 
 /* Bytes of that scratch. */
 size_t kf_hip_act_bytes(int rows, int n);
 
-/* Byte offsets of the five sections inside it (out[0..4] = q, d16, s16, d32, s32). */
-void kf_hip_act_offsets(int rows, int n, size_t out[5]);
+/* Byte offsets of the six sections inside it (out[0..5] = q, d16, s16, d32, s32, xa). */
+void kf_hip_act_offsets(int rows, int n, size_t out[6]);
 
 /* Activation kind the reference pairs with a weight type (act_kind, crates/kf-quant/src/lib.rs:154-163), or
  * KF_E_UNSUPPORTED. */

@@ -145,7 +145,7 @@ def act_bytes(rows: int, n: int) -> int:
 
 
 def act_offsets(rows: int, n: int) -> list[int]:
-    out = (ctypes.c_size_t * 5)()
+    out = (ctypes.c_size_t * 6)()
     lib().kf_hip_act_offsets(rows, n, out)
     return list(out)
 
@@ -314,6 +314,15 @@ def act_views(act, rows: int, n: int):
     d32 = act[o[3] : o[3] + rows * (n // 32) * 4].view(torch.float32).view(rows, n // 32)
     s32 = act[o[4] : o[4] + rows * (n // 32) * 4].view(torch.int32).view(rows, n // 32)
     return q, d16, s16, d32, s32
+
+
+def act_xa(act, rows: int, n: int):
+    """The xa section (Q8K kind): f16 [rows][ceil(n / 256)][16], per 256 columns the eight per-32 sums as hi then lo."""
+    import torch
+
+    o = act_offsets(rows, n)
+    nsb = (n + 255) // 256
+    return act[o[5] : o[5] + rows * nsb * 32].view(torch.float16).view(rows, nsb, 16)
 
 
 class Backend:

@@ -133,13 +133,14 @@ size_t kf_hip_act_bytes(int rows, int n) {
     return kf_act_layout((size_t)rows, (size_t)n).total;
 }
 
-void kf_hip_act_offsets(int rows, int n, size_t out[5]) {
+void kf_hip_act_offsets(int rows, int n, size_t out[6]) {
     const kf_act_offsets o = kf_act_layout((size_t)(rows < 0 ? 0 : rows), (size_t)(n < 0 ? 0 : n));
     out[0] = o.q;
     out[1] = o.d16;
     out[2] = o.s16;
     out[3] = o.d32;
     out[4] = o.s32;
+    out[5] = o.xa;
 }
 
 int kf_hip_act_kind(uint32_t ty) {
@@ -247,10 +248,9 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
 }  // extern "C"
 
 // q4_K: whether the tile GEMM beats the few-row product. The few-row product streams the weights once per 16
-// activation rows: about 0.28 us per MB and pass plus 1 us. A GEMM block computes a 128 x 128 tile over all of K, about
-// 12 us per 1024 columns, and its grid runs in rounds of one block a CU. Fitted at the Llama shapes, 8-256 rows:
-// QKV and O keep the few-row product to 128 and 192 rows, gate takes the GEMM from 96 rows, down (32 column tiles
-// against 14336 columns) keeps the few-row product to 256 rows.
+// activation rows: about 0.28 us per MB and pass plus 1 us. A GEMM block computes a 128 x 256 tile over all of K, about
+// 24 us per 1024 columns (measured at M = 2048: 333 us for 3.5 rounds of 16 super-blocks), and its grid runs in rounds of
+// one block a CU. The few-row constants were fitted at the Llama shapes, 8-256 rows.
 // Rows wider than the few-row product stages go one GEMV launch per row, so the GEMM takes them from 96 rows.
 static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
     if (rows < 64) return false;
@@ -258,8 +258,8 @@ static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
     const int cus = kf_cu_count();
     const double mb = (double)n_out * row_bytes / 1e6;
     const double t_rows = ((rows + 15) / 16) * (0.28 * mb + 1.0);
-    const int64_t blocks = (int64_t)((n_out + 127) / 128) * ((rows + 127) / 128);
-    const double t_gemm = 12.0 * n_in / 1024.0 * (double)((blocks + cus - 1) / cus);
+    const int64_t blocks = (int64_t)((n_out + 255) / 256) * ((rows + 127) / 128);
+    const double t_gemm = 24.0 * n_in / 1024.0 * (double)((blocks + cus - 1) / cus);
     return t_gemm < t_rows;
 }
 

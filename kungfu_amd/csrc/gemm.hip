@@ -435,47 +435,6 @@ __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __r
     }
 }
 
-// ------------------------------------------------------------------------------------------- q4_K prefill GEMM
-// y[m][n] = sum over super-blocks b of dx[m][b] * (d[n][b] * S_b[m][n] - dmin[n][b] * mins_b[m][n]) (+ bias + res),
-// with S_b = sum_j sc_j[n] * I_j[m][n] and mins_b = sum_j m_j[n] * bsum_j[m] the reference's per-super-block integers
-// (crates/kf-quant/src/types/q4_k.rs:10-58); the reference GPU path first unpacks q4_K into int8 + per-32 float scale
-// and min and runs a float-rescaled GEMM (crates/kf-backend-cuda/src/kernels/quant.cuh:585-601, kf8.cu:253-310).
-//
-// Here the native bytes feed the matrix core and S_b stays an exact integer formed by it:
-//   * the 6-bit scale is split as sc_j = 8 sh_j + sl_j (sh_j, sl_j in [0, 7]), so the nibble products q * sl_j and
-//     q * sh_j (at most 105) are int8 operands; two int32 MFMA chains per 32 x 32 tile run through the super-block,
-//     S_lo = sum_j X_j . (q_j sl_j) and S_hi = sum_j X_j . (q_j sh_j), and S_b = 8 S_hi + S_lo;
-//   * mins_b is one v_mfma_f32_32x32x16_f16 per super-block and tile: bsum_j = 64 hi + lo (hi in [-64, 63], lo in
-//     [0, 63]) fills eight k slots with hi against 64 m_j and eight with lo against m_j; every product and partial sum
-//     is an integer below 2^24, so the f32 result is exact;
-//   * the float rescale runs once per super-block and output (shift-add, convert, three float operations).
-// Staging is all DMA (buffer_load_dwordx4 ... lds), no register round trip, one stage per super-block (K = 256):
-//   * the activations sit in LDS as [group][32-row tile] 1 KB blocks in MFMA order (lane l reads bytes 16 l..: row
-//     l % 32, columns 16 (l / 32).. of the group), one DMA instruction per block;
-//   * the weights' raw nibble bytes sit as [pair][32-row tile] 1 KB blocks (lane l: row l % 32, bytes 16 (l / 32)..
-//     of the sub-block pair), in which each lane holds the bytes of its MFMA operand for both groups of the pair
-//     (low nibbles: group 2p, high nibbles: group 2p + 1); the consuming wave expands them into the two planes in
-//     registers (a mask, a shift and a packed 16-bit multiply per plane and dword);
-//   * the rows' 16-byte headers, the activation scales dx and the activation group sums travel in the same stage
-//     buffer, so one barrier per super-block hands a buffer back to the DMA;
-//   * the DMA sources are buffer resources over the block's first rows: the per-lane offsets are computed once and a
-//     super-block adds only a scalar offset, so the K loop spends no vector instructions on addresses.
-// Two stage buffers (about 109 KB of LDS, one block per CU), each a distinct static array and the K loop unrolled by
-// two, so the compiler waits for a DMA only before reads of the buffer it fills.
-// Measured on gfx950, the alternatives were slower: staging through registers let the compiler sink the prefetch
-// loads to their LDS stores (the full memory latency every stage); one LDS array made it wait for every outstanding
-// DMA before each LDS read; 128-column stages with the record in a separate buffer (register copies of it every
-// stage) ran 7% slower; wave tiles above two 32 x 32 tiles (four waves of 4 x 1 or 2 x 2 tiles, using AGPRs) ran
-// 25-35% slower, and so did letting the two waves of a SIMD run the MFMA and rescale phases out of step.
-// Eight waves (two per SIMD), each a 64 x 32 tile; blocks in XCD order (gm_tile).
-
-// Packed 16-bit multiply of the bytes of x by a small s: exact per byte while every byte product stays below 256
-__device__ __forceinline__ uint32_t gs_pmul(uint32_t x, uint32_t s) {
-    typedef unsigned short v2us __attribute__((ext_vector_type(2)));
-    const v2us r = __builtin_bit_cast(v2us, x) * v2us{(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, r);
-}
-
 // XCD-aware tile order. Workgroups go to the eight XCDs round-robin by linear block id, and each XCD has its own L2.
 // Block b runs tile t = (b % 8) * (T / 8) + b / 8, so XCD x works through the contiguous tile range
 // [x T / 8, (x + 1) T / 8). Tiles are numbered M-fastest, so an XCD's range is a few weight tiles against every
@@ -664,243 +623,6 @@ hipError_t gemm_q8_0_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_
     return hipGetLastError();
 }
 
-// LDS stage of the q4_K GEMM: one super-block of the block tile's activations, nibbles and record
-template <int WM, int WN, int TM, int TN>
-struct GbCfg {
-    static constexpr int W = WM * WN, THREADS = 64 * W;
-    static constexpr int BM = 32 * WM * TM, BN = 32 * WN * TN;
-    static constexpr int MT = BM / 32, NT = BN / 32;
-    static constexpr int A_BYTES = MT * 8 * 1024;          // [group][32-row tile] 1 KB operand blocks
-    static constexpr int B_OFF = A_BYTES, B_BYTES = 4 * NT * 1024;  // [pair][32-row tile] raw nibble blocks
-    static constexpr int HDR = B_OFF + B_BYTES, NH = (BN + 63) / 64;
-    static constexpr int DX = HDR + NH * 1024, ND = (BM + 63) / 64;
-    static constexpr int XS = DX + ND * 256, NX = MT;
-    static constexpr int STAGE = XS + NX * 1024;
-    static constexpr int NA = MT * 8, NB = 4 * NT;
-};
-
-template <int WM, int WN, int TM, int TN>
-__global__ void __launch_bounds__(64 * WM * WN, 1) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
-                                                                   const int8_t* __restrict__ xq, const int32_t* __restrict__ xs32,
-                                                                   const float* __restrict__ xd32, const float* __restrict__ bias,
-                                                                   const float* __restrict__ res, float* __restrict__ y, int M, int N,
-                                                                   int K) {
-    using C = GbCfg<WM, WN, TM, TN>;
-    __shared__ __align__(16) uint8_t buf0[C::STAGE];
-    __shared__ __align__(16) uint8_t buf1[C::STAGE];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    gm_tile((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM, tm, tn);
-    const int m0 = tm * C::BM, n0 = tn * C::BN;
-    const int kg = K >> 5;
-    const int nsb = K / KF_Q4_K_BLOCK;
-    const int half = lane >> 5, r32 = lane & 31;
-
-    // DMA sources: buffer resources over the tile's first rows; the per-lane offsets are fixed for the whole K loop
-    // and a super-block only adds a wave-uniform offset (rows past M or N are clamped to the last one)
-    const auto rw = kf_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
-    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
-    const auto rs = kf_rsrc(xs32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
-    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
-    constexpr int IA = (C::NA + C::W - 1) / C::W, IB = (C::NB + C::W - 1) / C::W;
-    constexpr int NR = C::NH + C::ND + C::NX, IR = (NR + C::W - 1) / C::W;
-    int va[IA], vb[IB], vr[IR];
-#pragma unroll
-    for (int it = 0; it < IA; it++) {
-        const int q = wave + it * C::W, g = q / C::MT, t = q % C::MT;
-        va[it] = (min(m0 + t * 32 + r32, M - 1) - m0) * K + g * 32 + half * 16;
-    }
-#pragma unroll
-    for (int it = 0; it < IB; it++) {
-        const int q = wave + it * C::W, p = q / C::NT, t = q % C::NT;
-        vb[it] = (min(n0 + t * 32 + r32, N - 1) - n0) * (int)row_bytes + 16 + 32 * p + half * 16;
-    }
-#pragma unroll
-    for (int it = 0; it < IR; it++) {
-        const int q = wave + it * C::W;
-        if (q < C::NH) {
-            vr[it] = (min(n0 + q * 64 + lane, N - 1) - n0) * (int)row_bytes;
-        } else if (q < C::NH + C::ND) {
-            vr[it] = (min(m0 + (q - C::NH) * 64 + lane, M - 1) - m0) * kg * 4;
-        } else {
-            const int qq = q - C::NH - C::ND;
-            vr[it] = (min(m0 + qq * 32 + (lane >> 1), M - 1) - m0) * kg * 4 + (lane & 1) * 16;
-        }
-    }
-    auto dma = [&](int sb, uint8_t* buf) {
-#pragma unroll
-        for (int it = 0; it < IA; it++) {
-            const int q = wave + it * C::W;
-            if (C::NA % C::W == 0 || q < C::NA) kf_bdma16(rx, va[it], sb * KF_Q4_K_BLOCK, buf + q * 1024);
-        }
-#pragma unroll
-        for (int it = 0; it < IB; it++) {
-            const int q = wave + it * C::W;
-            if (C::NB % C::W == 0 || q < C::NB) kf_bdma16(rw, vb[it], sb * KF_Q4_K_BYTES, buf + C::B_OFF + q * 1024);
-        }
-#pragma unroll
-        for (int it = 0; it < IR; it++) {
-            const int q = wave + it * C::W;
-            if (q < C::NH) {
-                kf_bdma16(rw, vr[it], sb * KF_Q4_K_BYTES, buf + C::HDR + q * 1024);
-            } else if (q < C::NH + C::ND) {
-                kf_bdma4(rd, vr[it], sb * 32, buf + C::DX + (q - C::NH) * 256);
-            } else if (q < NR) {
-                kf_bdma16(rs, vr[it], sb * 32, buf + C::XS + (q - C::NH - C::ND) * 1024);
-            }
-        }
-    };
-
-    v16f acc[TM][TN];
-    v16i slo[TM][TN], shi[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
-
-    // the record of the super-block being rescaled, read from its stage buffer after the MFMAs
-    uint4 hd[TN];
-    v4i xsv[TM][2];
-    v4f dxq[TM][4];
-
-    auto mfma_phase = [&](const uint8_t* buf) {
-#pragma unroll
-        for (int j = 0; j < TN; j++) hd[j] = *reinterpret_cast<const uint4*>(buf + C::HDR + ((wn * TN + j) * 32 + r32) * 16);
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            v4i bl[2][TN], bh[2][TN];
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(buf + C::B_OFF + ((p * C::NT + wn * TN + j) * 64 + lane) * 16);
-                uint32_t sc2, m2;
-                kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, p, sc2, m2);
-                const uint32_t s0 = sc2 & 0xffu, s1 = sc2 >> 8;
-                const uint32_t l0 = s0 & 7u, u0 = s0 >> 3, l1 = s1 & 7u, u1 = s1 >> 3;
-                const uint32_t m4 = 0x0f0f0f0fu;
-                const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    const uint32_t lo = v[e] & m4, hi = (v[e] >> 4) & m4;
-                    bl[0][j][e] = (int)gs_pmul(lo, l0);
-                    bh[0][j][e] = (int)gs_pmul(lo, u0);
-                    bl[1][j][e] = (int)gs_pmul(hi, l1);
-                    bh[1][j][e] = (int)gs_pmul(hi, u1);
-                }
-            }
-#pragma unroll
-            for (int gg = 0; gg < 2; gg++) {
-                const int g = 2 * p + gg;
-                v4i a[TM];
-#pragma unroll
-                for (int i = 0; i < TM; i++) a[i] = *reinterpret_cast<const v4i*>(buf + ((g * C::MT + wm * TM + i) * 64 + lane) * 16);
-#pragma unroll
-                for (int i = 0; i < TM; i++)
-#pragma unroll
-                    for (int j = 0; j < TN; j++) {
-                        const bool z = g == 0;
-                        slo[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bl[gg][j], z ? v16i{} : slo[i][j], 0, 0, 0);
-                        shi[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], bh[gg][j], z ? v16i{} : shi[i][j], 0, 0, 0);
-                    }
-            }
-        }
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            const int tr = wm * TM + i;
-            const int32_t* xsr = reinterpret_cast<const int32_t*>(buf + C::XS) + (tr * 32 + r32) * 8;
-            xsv[i][0] = *reinterpret_cast<const v4i*>(xsr);
-            xsv[i][1] = *reinterpret_cast<const v4i*>(xsr + 4);
-            // accumulator register r holds row (r % 4) + 8 (r / 4) + 4 (lane / 32)
-            const float* dxp = reinterpret_cast<const float*>(buf + C::DX) + tr * 32 + half * 4;
-#pragma unroll
-            for (int q = 0; q < 4; q++) dxq[i][q] = *reinterpret_cast<const v4f*>(dxp + 8 * q);
-        }
-    };
-
-    // the super-block's rescale: mins by MFMA, then acc += dx (d S - dmin mins)
-    auto rescale = [&]() {
-        v8h mo[TN];
-        float dd[TN], dm[TN];
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-#pragma unroll
-            for (int pj = 0; pj < 4; pj++) {
-                uint32_t sc2, m2;
-                kf_q4k_scales(hd[j].y, hd[j].z, hd[j].w, pj, sc2, m2);
-                const uint32_t f = half ? 1u : 64u;
-                mo[j][2 * pj] = (_Float16)(float)(f * (m2 & 0xffu));
-                mo[j][2 * pj + 1] = (_Float16)(float)(f * (m2 >> 8));
-            }
-            dd[j] = kf_h2f(hd[j].x & 0xffffu);
-            dm[j] = kf_h2f(hd[j].x >> 16);
-        }
-#pragma unroll
-        for (int i = 0; i < TM; i++) {
-            v8h xo;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                // bsum = 64 hi + lo, hi in [-64, 63], lo in [0, 63]: both exact in f16
-                xo[e] = (_Float16)(float)(half ? (xsv[i][0][e] & 63) : (xsv[i][0][e] >> 6));
-                xo[4 + e] = (_Float16)(float)(half ? (xsv[i][1][e] & 63) : (xsv[i][1][e] >> 6));
-            }
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                const v16f mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo[j], v16f{}, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int s = slo[i][j][r] + (shi[i][j][r] << 3);  // |S| < 2^25: exact
-                    const float t = fmaf(-dm[j], mins[r], dd[j] * (float)s);
-                    acc[i][j][r] = fmaf(t, dxq[i][r >> 2][r & 3], acc[i][j][r]);
-                }
-            }
-        }
-    };
-
-    auto stage = [&](int sb, const uint8_t* cur, uint8_t* nxt) {
-        if (sb + 1 < nsb) dma(sb + 1, nxt);
-        mfma_phase(cur);
-        rescale();
-        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-        __syncthreads();
-    };
-
-    dma(0, buf0);
-    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-    __syncthreads();
-#pragma unroll 1
-    for (int sb = 0; sb < nsb; sb += 2) {
-        stage(sb, buf0, buf1);
-        if (sb + 1 < nsb) stage(sb + 1, buf1, buf0);
-    }
-
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++) {
-            const int n = n0 + (wn * TN + j) * 32 + r32;
-            if (n >= N) continue;
-            const float bn = bias ? bias[n] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = m0 + (wm * TM + i) * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
-                if (m >= M) continue;
-                const int64_t o = (int64_t)m * N + n;
-                y[o] = acc[i][j][r] + bn + (res ? res[o] : 0.0f);
-            }
-        }
-}
-
-template <int WM, int WN, int TM, int TN>
-hipError_t gemm_q4k_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32,
-                              const float* bias, const float* res, float* y, int M, int N, int K, hipStream_t s) {
-    using C = GbCfg<WM, WN, TM, TN>;
-    static_assert(2 * C::STAGE <= 160 * 1024, "LDS");
-    dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
-    gemm_q4k_kernel<WM, WN, TM, TN><<<grid, C::THREADS, 0, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, M, N, K);
-    return hipGetLastError();
-}
-
 template <int WM, int WN, int TM, int TN>
 hipError_t gemm_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res, float* y,
                        int M, int N, int K, hipStream_t s) {
@@ -955,6 +677,8 @@ int gm_cus() {
 
 int kf_gemm_k_multiple() { return GM_BK; }
 
+
+
 // Host launcher, validated by the caller (api.cpp): K a multiple of 128, Q8_0-kind activations in `act`
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s) {
@@ -978,16 +702,4 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
     }
     if (K % 256 == 0 && row_bytes % 16 == 0) return gemm_q8_0_dma_launch<2, 4, 2, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
     return gemm_launch<2, 2, 2, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
-}
-
-// Host launcher of the q4_K GEMM, validated by the caller (api.cpp): K a multiple of 256, Q8K-kind activations in `act`
-hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
-                              int N, int K, hipStream_t s) {
-    const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
-    const char* base = static_cast<const char*>(act);
-    const auto* wb = static_cast<const uint8_t*>(w);
-    const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
-    const auto* xs = reinterpret_cast<const int32_t*>(base + o.s32);
-    const auto* xd = reinterpret_cast<const float*>(base + o.d32);
-    return gemm_q4k_launch<2, 4, 2, 1>(wb, row_bytes, xq, xs, xd, bias, res, y, M, N, K, s);
 }

@@ -41,8 +41,12 @@ static inline size_t kf_align_up(size_t v, size_t a) { return (v + a - 1) / a * 
 //   s16  int32 [rows][n/16]   integer sum of every 16 columns
 //   d32  f32   [rows][n/32]   scale of every 32 columns
 //   s32  int32 [rows][n/32]   integer sum of every 32 columns
+//   xa   f16   [rows][ceil(n/256)][16]  Q8K kind only: per 256 columns the matrix-core operand of the q4_K mins
+//        term, hi_j = floor(s32_j / 64) for the eight 32-column groups j, then lo_j = s32_j - 64 hi_j (hi in
+//        [-64, 63], lo in [0, 63], both exact in f16), the counterpart of the reference's fragment array xa
+//        (crates/kf-backend-cuda/src/kf8.rs:338-357); left unwritten by the Q8_0 kind
 struct kf_act_offsets {
-    size_t q, d16, s16, d32, s32, total;
+    size_t q, d16, s16, d32, s32, xa, total;
 };
 
 static inline struct kf_act_offsets kf_act_layout(size_t rows, size_t n) {
@@ -52,7 +56,8 @@ static inline struct kf_act_offsets kf_act_layout(size_t rows, size_t n) {
     o.s16 = kf_align_up(o.d16 + rows * (n / 16) * 4, KF_ACT_ALIGN);
     o.d32 = kf_align_up(o.s16 + rows * (n / 16) * 4, KF_ACT_ALIGN);
     o.s32 = kf_align_up(o.d32 + rows * (n / 32) * 4, KF_ACT_ALIGN);
-    o.total = kf_align_up(o.s32 + rows * (n / 32) * 4, KF_ACT_ALIGN);
+    o.xa = kf_align_up(o.s32 + rows * (n / 32) * 4, KF_ACT_ALIGN);
+    o.total = kf_align_up(o.xa + rows * ((n + 255) / 256) * 32, KF_ACT_ALIGN);
     return o;
 }
 

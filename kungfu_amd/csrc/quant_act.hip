@@ -23,7 +23,7 @@ constexpr int QA_SPAN = QA_THREADS * 4;  // columns one block covers
 // per-32 scales and integer sums. Every thread of the wave calls it (the reductions are wave-wide).
 __device__ __forceinline__ void qa_emit(const float (&v)[4], int c0, bool in, int n, int kind, int row, int8_t* __restrict__ q,
                                         float* __restrict__ d16, int32_t* __restrict__ s16, float* __restrict__ d32,
-                                        int32_t* __restrict__ s32) {
+                                        int32_t* __restrict__ s32, _Float16* __restrict__ xa) {
     const int lane = threadIdx.x & 63;
     int qi[4];
     float d;
@@ -91,6 +91,12 @@ __device__ __forceinline__ void qa_emit(const float (&v)[4], int c0, bool in, in
         const size_t g = (size_t)row * (n >> 5) + (c0 >> 5);
         d32[g] = d;
         s32[g] = sum32;
+        if (kind == KF_ACT_Q8K) {
+            // the mins operand of the q4_K GEMM: sum32 = 64 hi + lo
+            _Float16* xr = xa + ((size_t)row * ((n + 255) >> 8) + (c0 >> 8)) * 16 + ((c0 >> 5) & 7);
+            xr[0] = (_Float16)(float)(sum32 >> 6);
+            xr[8] = (_Float16)(float)(sum32 & 63);
+        }
     }
 }
 
@@ -105,7 +111,7 @@ __device__ __forceinline__ void qa_load4(const float* p, bool in, float (&v)[4])
     }
 }
 
-#define QA_OUT int8_t *__restrict__ q, float *__restrict__ d16, int32_t *__restrict__ s16, float *__restrict__ d32, int32_t *__restrict__ s32
+#define QA_OUT int8_t *__restrict__ q, float *__restrict__ d16, int32_t *__restrict__ s16, float *__restrict__ d32, int32_t *__restrict__ s32, _Float16 *__restrict__ xa
 
 __global__ void __launch_bounds__(QA_THREADS) quant_act_kernel(const float* __restrict__ x, QA_OUT, int n, int kind) {
     const int row = blockIdx.y;
@@ -113,7 +119,7 @@ __global__ void __launch_bounds__(QA_THREADS) quant_act_kernel(const float* __re
     const bool in = c0 < n;
     float v[4];
     qa_load4(x + (size_t)row * n + c0, in, v);
-    qa_emit(v, c0, in, n, kind, row, q, d16, s16, d32, s32);
+    qa_emit(v, c0, in, n, kind, row, q, d16, s16, d32, s32, xa);
 }
 
 // rms_norm (crates/kf-backend-cpu/src/ops.rs:222-239) fused with the quantization, in place of the reference's
@@ -168,7 +174,7 @@ __global__ void __launch_bounds__(T) rms_norm_q8_kernel(const float* __restrict_
                 v[j] = u + bv[j];
             }
         }
-        qa_emit(v, c0, in, n, kind, row, q, d16, s16, d32, s32);
+        qa_emit(v, c0, in, n, kind, row, q, d16, s16, d32, s32, xa);
     }
 }
 
@@ -199,7 +205,7 @@ __global__ void __launch_bounds__(QA_THREADS) gated_act_q8_kernel(const float* _
             v[j] = a * u[j];
         }
     }
-    qa_emit(v, c0, in, n, kind, row, q, d16, s16, d32, s32);
+    qa_emit(v, c0, in, n, kind, row, q, d16, s16, d32, s32, xa);
 }
 
 }  // namespace
@@ -212,12 +218,13 @@ __global__ void __launch_bounds__(QA_THREADS) gated_act_q8_kernel(const float* _
     int32_t* s16 = reinterpret_cast<int32_t*>(base + o.s16);                                                  \
     float* d32 = reinterpret_cast<float*>(base + o.d32);                                                      \
     int32_t* s32 = reinterpret_cast<int32_t*>(base + o.s32);                                                  \
+    _Float16* xa = reinterpret_cast<_Float16*>(base + o.xa);                                                  \
     dim3 grid((n + QA_SPAN - 1) / QA_SPAN, rows)
 
 // Host launchers, validated by the caller (api.cpp): n a multiple of the kind's block, rows >= 1
 hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s) {
     QA_ARGS(act);
-    quant_act_kernel<<<grid, QA_THREADS, 0, s>>>(x, q, d16, s16, d32, s32, n, kind);
+    quant_act_kernel<<<grid, QA_THREADS, 0, s>>>(x, q, d16, s16, d32, s32, xa, n, kind);
     return hipGetLastError();
 }
 
@@ -226,15 +233,15 @@ hipError_t kf_launch_rms_norm_q8(const float* x, const float* w, const float* b,
     QA_ARGS(act);
     (void)grid;
     if (rows < 64)
-        rms_norm_q8_kernel<1024><<<rows, 1024, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, n, kind);
+        rms_norm_q8_kernel<1024><<<rows, 1024, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, xa, n, kind);
     else
-        rms_norm_q8_kernel<QA_THREADS><<<rows, QA_THREADS, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, n, kind);
+        rms_norm_q8_kernel<QA_THREADS><<<rows, QA_THREADS, 0, s>>>(x, w, b, eps, q, d16, s16, d32, s32, xa, n, kind);
     return hipGetLastError();
 }
 
 hipError_t kf_launch_gated_act_q8(const float* gate, const float* up, int stride, int act_fn, void* act, int rows, int n, int kind,
                                   hipStream_t s) {
     QA_ARGS(act);
-    gated_act_q8_kernel<<<grid, QA_THREADS, 0, s>>>(gate, up, stride, act_fn, q, d16, s16, d32, s32, n, kind);
+    gated_act_q8_kernel<<<grid, QA_THREADS, 0, s>>>(gate, up, stride, act_fn, q, d16, s16, d32, s32, xa, n, kind);
     return hipGetLastError();
 }

@@ -57,6 +57,11 @@ def test_quant_act_bit_exact(cuda, kind, rows, n):
     assert np.array_equal(s16, ws)
     assert np.array_equal(d32.view(np.uint32), wd[:, ::2].view(np.uint32))
     assert np.array_equal(s32, ws[:, ::2] + ws[:, 1::2])
+    if kind == kf.ACT_Q8K:
+        # the mins operand: per 256 columns the eight per-32 sums as floor(s / 64), then s mod 64
+        xa = kf.act_xa(act, rows, n).cpu().numpy().astype(np.float64)
+        s32w = (ws[:, ::2] + ws[:, 1::2]).astype(np.int64).reshape(rows, n // 256, 8)
+        assert np.array_equal(xa[:, :, :8], s32w // 64) and np.array_equal(xa[:, :, 8:], s32w % 64)
 
 
 def test_quant_act_hard_rounding_ties(cuda):
