@@ -111,6 +111,8 @@ def time_launches(fn, iters):
 
 PREFILL = [("gate_up", 4096, 14336), ("down", 14336, 4096)]
 SMALL_BATCH = [8, 16, 32, 64]
+# the q4_K rows also cover the range where kf_hip_matmul's cost model moves from the few-row product to the tile GEMM
+SMALL_BATCH_Q4_K = SMALL_BATCH + [96, 128, 192, 256]
 
 
 def gemm_section(dev, m=2048, ty=None):
@@ -187,7 +189,7 @@ def small_batch_q4_k_section(dev):
         w = torch.from_numpy(make_weights(ty, n, n_out)).to(dev)
         ws = [w] + [w.clone() for _ in range(max(1, -(-2 * MALL_BYTES // w.numel())))]
         res = {}
-        for m in SMALL_BATCH:
+        for m in SMALL_BATCH_Q4_K:
             x = torch.from_numpy(kf.synth_normal(1, 1.0, m * n).reshape(m, n)).to(dev)
             act = kf.alloc_act(m, n, dev)
             y = torch.empty((m, n_out), device=dev)
@@ -203,16 +205,18 @@ def small_batch_q4_k_section(dev):
     return out
 
 
-def moe_section(dev, seed=0):
+def moe_section(dev, seed=0, rows=16):
     """the routed expert layer (kf_hip_moe_ffn) for 8 Q4_K experts of gate/up 4096->14336 and down
     14336->4096, 16 tokens, top-2 uniform without replacement. GB/s over the weight bytes of the touched experts (each
-    read once per call) plus the fp32 activations in and out; two copies of the expert set alternate (1.6 GB)."""
+    read once per call) plus the fp32 activations in and out; two copies of the expert set alternate (1.6 GB).
+    With rows = 512 (1024 routed pairs, the grouped tile GEMM): also TOPS = 2 * pairs * 3 * n_ff * n_embd / time, the
+    whole layer (quantize, group, gather, both products, gated activation, combine) against the int8 peak."""
     import numpy as np
     import torch
 
     import kungfu_amd as kf
 
-    ty, n_exp, n_embd, n_ff, rows, n_used = kf.TYPE_Q4_K, 8, 4096, 14336, 16, 2
+    ty, n_exp, n_embd, n_ff, n_used = kf.TYPE_Q4_K, 8, 4096, 14336, 2
     mats = []
     for i, (n_out, n_in) in enumerate([(n_ff, n_embd), (n_ff, n_embd), (n_embd, n_ff)]):
         w = torch.from_numpy(make_weights(ty, n_in, n_exp * n_out, seed=10 + i)).to(dev)
@@ -228,13 +232,53 @@ def moe_section(dev, seed=0):
     def call(i):
         kf.moe_ffn(ty, mats[0][i % 2], mats[1][i % 2], mats[2][i % 2], n_exp, n_embd, n_ff, x, s_, w_, out, scratch)
 
-    us = time_launches(call, 20)
+    us = time_launches(call, 20 if rows <= 64 else 5)
     touched = len(np.unique(sel))
     wbytes = touched * (2 * n_ff * kf.row_bytes(ty, n_embd) + n_embd * kf.row_bytes(ty, n_ff))
     nbytes = wbytes + 4 * rows * n_embd * 2
     del mats
-    return {"us": round(us, 2), "GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
-            "touched_experts": touched, "weight_bytes": wbytes, "tokens": rows, "top_k": n_used}
+    rec = {"us": round(us, 2), "GBs": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+           "touched_experts": touched, "weight_bytes": wbytes, "tokens": rows, "top_k": n_used}
+    if rows * n_used > 64:
+        tops = 2.0 * rows * n_used * 3 * n_ff * n_embd / us / 1e6
+        rec.update(TOPS=round(tops, 1), tops_frac=round(tops / INT8_PEAK_TOPS, 4), path="grouped tile GEMM")
+    return rec
+
+
+def moe_prefill_section(dev):
+    return moe_section(dev, rows=512)
+
+
+def layer_with_producers_section(shapes, dev):
+    """The decode layer step with its activation producers, batch 1, Q4_K: rms_norm_q8 -> QKV, quant_act of the
+    attention output -> O, rms_norm_q8 -> gate+up, gated_act_q8 of the gate+up output -> down (every product's
+    activations made inside the step, the cost Op::MatMul pays at M=1). GB/s over the same algorithmic bytes as the
+    headline step."""
+    import torch
+
+    import kungfu_amd as kf
+
+    by = {s.name: s for s in shapes}
+    x = torch.from_numpy(kf.synth_normal(6, 1.0, 4096).reshape(1, 4096)).to(dev)
+    wn = torch.from_numpy(kf.synth_normal(7, 1.0, 4096)).to(dev)
+    attn = torch.from_numpy(kf.synth_normal(8, 1.0, 4096).reshape(1, 4096)).to(dev)
+    n_ff = 14336
+
+    def step(i):
+        kf.rms_norm_q8(x, by["qkv"].act, kf.ACT_Q8K, wn, None, 1e-5)
+        by["qkv"].gemv(i)
+        kf.quant_act(attn, by["o"].act, kf.ACT_Q8K)
+        by["o"].gemv(i)
+        kf.rms_norm_q8(x, by["gate_up"].act, kf.ACT_Q8K, wn, None, 1e-5)
+        by["gate_up"].gemv(i)
+        gu = by["gate_up"].y
+        kf.gated_act_q8(gu[:, :n_ff], gu[:, n_ff:], by["down"].act, kf.ACT_Q8K, 1, n_ff, 2 * n_ff)
+        by["down"].gemv(i)
+
+    us = time_launches(step, 50)
+    nb = sum(s.bytes for s in shapes)
+    return {"us": round(us, 2), "GBs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+            "launches": 8}
 
 
 def fused_section(dev):
@@ -376,24 +420,45 @@ def read_traffic():
     return None
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(shapes, budget_s):
-    """The CPU backend's product (oracle restatement of ops::matmul_slice, OpenMP over output rows) on the same
-    weights and input: whole layer passes until budget_s of wall time is spent."""
+    """The CPU backend's product (oracle restatement of ops::matmul_slice, OpenMP over output rows, as rayon's par_iter
+    over rows) on the same weights and input: whole layer passes until budget_s of wall time is spent; then the same
+    for its integer path (ops::matmul_i8: the activations quantized once per call, dot_i8 per row). Threads: every
+    logical core the process may run on, capped by OMP_NUM_THREADS where the host sets it (a GPU box's CPU share)."""
     import oracle
 
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1)
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    env = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    threads = min(avail, env) if env > 0 else avail
     oracle.lib()
-    total_bytes, passes, t0 = 0, 0, time.perf_counter()
-    while True:
-        for sh in shapes:
-            oracle.matmul_slice(sh.ty, sh.host_w, sh.n, sh.n_out, sh.host_x, threads=threads)
-            total_bytes += sh.bytes
-        passes += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    return {"value": round(total_bytes / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{passes} full layer passes (5 Q4_K GEMVs at M=1) of oracle matmul_slice in {el:.1f} s"}
+
+    def run(fn):
+        total_bytes, passes, t0 = 0, 0, time.perf_counter()
+        while True:
+            for sh in shapes:
+                fn(sh.ty, sh.host_w, sh.n, sh.n_out, sh.host_x, threads=threads)
+                total_bytes += sh.bytes
+            passes += 1
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                return total_bytes / el / 1e9, passes, el
+
+    v, passes, el = run(oracle.matmul_slice)
+    vi, passes_i, el_i = run(oracle.matmul_i8)
+    return {"value": round(v, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{passes} full layer passes (5 Q4_K GEMVs at M=1) of oracle matmul_slice in {el:.1f} s",
+            "dot_i8_value": round(vi, 3), "dot_i8_sample": f"{passes_i} layer passes of oracle matmul_i8 in {el_i:.1f} s",
+            "nproc": os.cpu_count(), "affinity_cores": avail, "cpu_model": cpu_model()}
 
 
 def main():
@@ -403,7 +468,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "small_q4_k", "moe", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "small_q4_k", "moe", "moe_prefill", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -417,7 +482,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "small_q4_k": small_batch_q4_k_section, "moe": moe_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "small_q4_k": small_batch_q4_k_section, "moe": moe_section, "moe_prefill": moe_prefill_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -494,6 +559,8 @@ def main():
     out["small_batch_q8_0"] = small_batch_section(dev)
     out["small_batch_q4_k"] = small_batch_q4_k_section(dev)
     out["moe_q4_k"] = moe_section(dev)
+    out["moe_q4_k_prefill"] = moe_prefill_section(dev)
+    out["layer_with_producers"] = layer_with_producers_section(shapes, dev)
     out["fused_producers"] = fused_section(dev)
     out["k_quants"] = kquant_section(dev)
     out["grouped"] = group_section(dev)

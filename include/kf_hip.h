@@ -188,6 +188,16 @@ int kf_hip_moe_group(const int32_t* slots, int total, int n_slots, int32_t* orde
 int kf_hip_moe_gemv(uint32_t ty, const void* w, const void* w_up, int64_t expert_bytes, int64_t row_bytes, const void* act, int act_rows, int n,
                     int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int n_used, int per_slot, float* y, void* stream);
 
+/* Grouped tile GEMM of routed pairs (q4_K experts, n a multiple of 256): `act` holds `pairs` activation rows in group
+ * order (the pairs of slot s are rows offsets[s]..offsets[s + 1], device offsets from kf_hip_moe_group); slot s
+ * multiplies its expert w + s * expert_bytes ([n_out][row_bytes]) or, with w2 non-null, output columns below n_split
+ * from w + s * expert_bytes and columns n_split.. from w2 + s * expert_bytes (gate and up as one product). Output row p
+ * of the group order is written to y row out_rows[p] (device, nullable: row p); y is [*][n_out]. Rows of act past
+ * offsets[n_slots] are not read. Replaces kf8_gemm_moe (crates/kf-backend-cuda/src/kernels/kf8.cu:400-416) without the
+ * KF8 unpack; kf_hip_moe_ffn takes it past 64 routed pairs, as expert_gemm_chunks (exec.rs:2196-2237). */
+int kf_hip_moe_gemm(uint32_t ty, const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, int n_split, const void* act,
+                    int pairs, int n, int n_out, const int32_t* offsets, int n_slots, const int32_t* out_rows, float* y, void* stream);
+
 /* out[r][o] = sum over j of wts[rj] * scale * part[rj][o] for the row's pairs with slots[rj] >= 0, in j order, plus
  * host[r][o] (nullable). Replaces moe_combine (moe.cu:153-164). */
 int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used, int n_embd,
@@ -198,7 +208,9 @@ int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots
 size_t kf_hip_moe_scratch_bytes(int rows, int n_used, int n_embd, int n_ff, int n_slots);
 
 /* The routed expert layer with silu gating: quantize x, group the pairs, fused gate/up product, quantize the hidden
- * rows, down product, weighted combine. gate and up are [n_slots][n_ff][row of n_embd], down [n_slots][n_embd][row
+ * rows, down product, weighted combine. Past 64 routed pairs of q4_K experts (n_embd and n_ff multiples of 256) the
+ * products run as the grouped tile GEMM (kf_hip_moe_gemm) on the pairs' activation rows gathered in group order, with
+ * the hidden rows quantized by kf_hip_gated_act_q8; otherwise as the grouped few-row products (kf_hip_moe_gemv). gate and up are [n_slots][n_ff][row of n_embd], down [n_slots][n_embd][row
  * of n_ff], all of type ty. out [rows][n_embd]. A pair whose slot is outside [0, n_slots) contributes nothing (the
  * grouping skips it and so does the combine). Replaces expert_launches (crates/kf-backend-cuda/src/exec.rs:2378-2386)
  * for int8-capable experts resident on the device. */

@@ -81,6 +81,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_moe_group": ([P, I, I, P, P, P], I),
         "kf_hip_moe_gemv": ([U, P, P, L64, L64, P, I, I, I, P, P, I, I, I, P, P], I),
         "kf_hip_moe_combine": ([P, P, P, P, P, I, I, I, ctypes.c_float, P], I),
+        "kf_hip_moe_gemm": ([U, P, P, L64, L64, I, P, I, I, I, P, I, P, P, P], I),
         "kf_hip_moe_scratch_bytes": ([I, I, I, I, I], S),
         "kf_hip_moe_ffn": ([U, P, P, P, I, I, I, P, I, P, P, I, ctypes.c_float, P, S, P, P], I),
         "kf_hip_backend_new": ([I], P),
@@ -281,6 +282,13 @@ def moe_gemv(ty: int, w, act, act_rows: int, n: int, n_out: int, order, offsets,
 
 def moe_combine(part, wts, slots, out, rows: int, n_used: int, n_embd: int, scale: float = 1.0, host=None, stream=None) -> None:
     check(lib().kf_hip_moe_combine(_ptr(part), _ptr(wts), _ptr(slots), _ptr(host), _ptr(out), rows, n_used, n_embd, scale, _stream(stream)))
+
+
+def moe_gemm(ty: int, w, act, pairs: int, n: int, n_out: int, offsets, n_slots: int, y, expert_bytes: int, w2=None, n_split: int = 0,
+             out_rows=None, stream=None) -> None:
+    """The grouped tile GEMM (kf_hip_moe_gemm): act holds `pairs` activation rows in group order."""
+    check(lib().kf_hip_moe_gemm(ty, _ptr(w), _ptr(w2), expert_bytes, row_bytes(ty, n), n_split, _ptr(act), pairs, n, n_out, _ptr(offsets),
+                                n_slots, _ptr(out_rows), _ptr(y), _stream(stream)))
 
 
 def moe_scratch_bytes(rows: int, n_used: int, n_embd: int, n_ff: int, n_slots: int) -> int:

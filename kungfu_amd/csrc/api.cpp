@@ -43,6 +43,11 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
                           int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used, int per_slot,
                           const float* bias, const float* res, float* y, hipStream_t s);
 hipError_t kf_launch_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, hipStream_t s);
+hipError_t kf_launch_moe_gather_act(const void* src, int src_rows, void* dst, int pairs, const int32_t* order, const int32_t* offsets,
+                                    int n_slots, int n_used, int n, hipStream_t s);
+hipError_t kf_launch_gemm_q4k_moe(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, int n_split, const void* act,
+                                  int pairs, int n_slots, const int32_t* offsets, const int32_t* out_rows, float* y, int N, int K,
+                                  hipStream_t s);
 hipError_t kf_launch_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used,
                                  int n_embd, float scale, int n_slots, hipStream_t s);
 
@@ -399,6 +404,23 @@ int kf_hip_moe_gemv(uint32_t ty, const void* w, const void* w_up, int64_t expert
     return e == hipSuccess ? KF_OK : hip_fail(e, "moe product launch");
 }
 
+int kf_hip_moe_gemm(uint32_t ty, const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, int n_split, const void* act,
+                    int pairs, int n, int n_out, const int32_t* offsets, int n_slots, const int32_t* out_rows, float* y, void* stream) {
+    const int rc = check_product(ty, w, row_bytes, act, y, pairs, n, n_out);
+    if (rc != KF_OK) return rc;
+    if (ty != KF_TYPE_Q4_K) return fail(KF_E_UNSUPPORTED, "the grouped GEMM runs q4_K experts (type %u)", ty);
+    if (n % 256 != 0) return fail(KF_E_INVALID, "%d columns, the grouped GEMM needs a multiple of 256", n);
+    if (!offsets || n_slots < 1) return fail(KF_E_INVALID, "null offsets or %d slots", n_slots);
+    const int mat_rows = w2 ? n_split : n_out;
+    if (w2 && (n_split < 1 || n_split >= n_out || n_split % 256 != 0 || !aligned(w2, 16)))
+        return fail(KF_E_INVALID, "split at column %d of %d (a multiple of 256 inside the output) or unaligned second matrix", n_split, n_out);
+    if (expert_bytes < (int64_t)mat_rows * row_bytes || expert_bytes % 16 != 0)
+        return fail(KF_E_INVALID, "expert stride %lld for %d rows of %lld bytes (16-byte multiple)", (long long)expert_bytes, mat_rows, (long long)row_bytes);
+    const hipError_t e = kf_launch_gemm_q4k_moe(w, w2, expert_bytes, row_bytes, w2 ? n_split : 0, act, pairs, n_slots, offsets, out_rows, y,
+                                                n_out, n, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "grouped GEMM launch");
+}
+
 int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used, int n_embd,
                        float scale, void* stream) {
     if (rows < 0 || n_used < 1 || n_embd < 0) return fail(KF_E_INVALID, "%d rows, %d used, %d columns", rows, n_used, n_embd);
@@ -409,9 +431,10 @@ int kf_hip_moe_combine(const float* part, const float* wts, const int32_t* slots
 }
 
 namespace {
-// Scratch of one MoE layer: x activations | order | offsets | hidden f32 | hidden activations | pair outputs
+// Scratch of one MoE layer: x activations | order | offsets | hidden f32 | hidden activations | pair outputs, and for
+// the grouped GEMM the pairs' activation rows in group order; hidden holds [pairs][2 n_ff] (gate | up for the GEMM)
 struct MoeScratch {
-    size_t xact, order, offsets, hidden, hact, part, total;
+    size_t xact, order, offsets, hidden, hact, part, xg, total;
 };
 MoeScratch moe_scratch(int rows, int n_used, int n_embd, int n_ff, int n_slots) {
     MoeScratch m{};
@@ -424,14 +447,21 @@ MoeScratch moe_scratch(int rows, int n_used, int n_embd, int n_ff, int n_slots) 
     m.offsets = at;
     at += kf_align_up(((size_t)n_slots + 1) * 4, 256);
     m.hidden = at;
-    at += kf_align_up(pairs * n_ff * 4, 256);
+    at += kf_align_up(pairs * n_ff * 2 * 4, 256);
     m.hact = at;
     at += kf_align_up(kf_act_layout(pairs, (size_t)n_ff).total, 256);
     m.part = at;
     at += kf_align_up(pairs * n_embd * 4, 256);
+    m.xg = at;
+    at += kf_align_up(kf_act_layout(pairs, (size_t)n_embd).total, 256);
     m.total = at;
     return m;
 }
+
+// Routed pairs past which the q4_K expert products run as the grouped tile GEMM (each expert's weights read once per
+// 128 pairs) instead of the few-row product (once per 16); the reference switches to its tensor-core GEMM past
+// MOE_MATVEC_ROWS = 64 pairs (crates/kf-backend-cuda/src/exec.rs:2196)
+constexpr int KF_MOE_GEMM_PAIRS = 64;
 }  // namespace
 
 size_t kf_hip_moe_scratch_bytes(int rows, int n_used, int n_embd, int n_ff, int n_slots) {
@@ -464,6 +494,21 @@ int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* do
     const int pairs = rows * n_used;
     int rc = kf_hip_quant_act(x, xact, rows, n_embd, kind_of(ty), stream);
     if (rc == KF_OK) rc = kf_hip_moe_group(sel, pairs, n_slots, order, offsets, stream);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    if (rc == KF_OK && ty == KF_TYPE_Q4_K && pairs > KF_MOE_GEMM_PAIRS && n_embd % 256 == 0 && n_ff % 256 == 0) {
+        // many pairs: the grouped GEMM (the reference's expert_gemm_chunks, exec.rs:2196-2237). The pairs' activation
+        // rows in group order; gate and up as one product of 2 n_ff columns; the gated activation quantized; down
+        // written to each pair's row; the weighted combine
+        void* xg = base + m.xg;
+        hipError_t e = kf_launch_moe_gather_act(xact, rows, xg, pairs, order, offsets, n_slots, n_used, n_embd, st);
+        if (e != hipSuccess) return hip_fail(e, "moe gather launch");
+        rc = kf_hip_moe_gemm(ty, gate, up, eb_gu, rb_in, n_ff, xg, pairs, n_embd, 2 * n_ff, offsets, n_slots, nullptr, hidden, stream);
+        if (rc == KF_OK) rc = kf_hip_gated_act_q8(hidden, hidden + n_ff, pairs, n_ff, 2 * n_ff, KF_GLU_SILU, kind_of(ty), hact, stream);
+        if (rc == KF_OK) rc = kf_hip_moe_gemm(ty, down, nullptr, eb_dn, rb_ff, 0, hact, pairs, n_ff, n_embd, offsets, n_slots, order, part, stream);
+        if (rc != KF_OK) return rc;
+        e = kf_launch_moe_combine(part, wts, sel, nullptr, out, rows, n_used, n_embd, scale, n_slots, st);
+        return e == hipSuccess ? KF_OK : hip_fail(e, "moe_combine launch");
+    }
     if (rc == KF_OK)
         rc = kf_hip_moe_gemv(ty, gate, up, eb_gu, rb_in, xact, rows, n_embd, n_ff, order, offsets, n_slots, n_used, 0, hidden, stream);
     if (rc == KF_OK) rc = kf_hip_quant_act(hidden, hact, pairs, n_ff, kind_of(ty), stream);

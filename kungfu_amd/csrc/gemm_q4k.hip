@@ -99,11 +99,23 @@ constexpr int G4_NW = G4_BN * 144 / 1024;       // weights (64 16-byte pieces ea
 static_assert(G4_BN * 144 % 1024 == 0 && G4_NA % G4_WAVES == 0 && G4_BN * 9 <= 2304, "whole DMA instructions");
 static_assert(2 * G4_STAGE + 3 * G4_REC <= 160 * 1024, "two stages and three records fit the LDS");
 
+// The grouped (MoE) form: the activation rows are routed pairs in group order (pairs of slot s are rows
+// offsets[s]..offsets[s + 1]), slot s multiplies its own expert matrix (w + s expert_bytes; with w2, output columns from
+// n_split on come from w2 + s expert_bytes, row n - n_split), and output row p goes to y row out_rows[p] (or p)
+struct G4Moe {
+    const int32_t* offsets;
+    const int32_t* out_rows;
+    const uint8_t* w2;
+    int64_t expert_bytes;
+    int n_slots, n_split;
+};
+
+template <bool MOE>
 __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
                                                                   const int8_t* __restrict__ xq, const _Float16* __restrict__ xa,
                                                                   const float* __restrict__ xd32, const float* __restrict__ bias,
                                                                   const float* __restrict__ res, float* __restrict__ y, int M, int N,
-                                                                  int K) {
+                                                                  int K, G4Moe moe) {
     __shared__ __align__(16) uint8_t buf0[G4_STAGE];
     __shared__ __align__(16) uint8_t buf1[G4_STAGE];
     __shared__ __align__(16) uint8_t recs[3 * G4_REC];  // records of super-blocks sb % 3
@@ -112,16 +124,38 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
     const int half = lane >> 5, r32 = lane & 31;
     int tm, tn;
     g4_tile((N + G4_BN - 1) / G4_BN, (M + G4_BM - 1) / G4_BM, tm, tn);
-    const int m0 = tm * G4_BM, n0 = tn * G4_BN;
+    int m0 = tm * G4_BM, n0 = tn * G4_BN;
     const int kg = K >> 5;
     const int nsb = K >> 8;
+    int m_end = M;  // rows of the block's slot end here
+    const uint8_t* wt = w + (int64_t)n0 * row_bytes;
+    int n_end = N;  // columns of the block's matrix end here (as output columns)
+    if (MOE) {
+        // M counts the grid's row tiles over all slots (an upper bound): tile tm is the slot's tile tm - (the tiles of
+        // the slots before it); past the last slot's tiles the block has nothing to do
+        int s = 0, t0 = 0;
+        for (; s < moe.n_slots; s++) {
+            const int rows = moe.offsets[s + 1] - moe.offsets[s], t = (rows + G4_BM - 1) / G4_BM;
+            if (tm < t0 + t) break;
+            t0 += t;
+        }
+        if (s == moe.n_slots) return;  // whole block, before any barrier
+        m0 = moe.offsets[s] + (tm - t0) * G4_BM;
+        m_end = moe.offsets[s + 1];
+        if (moe.w2 && n0 >= moe.n_split) {
+            wt = moe.w2 + s * moe.expert_bytes + (int64_t)(n0 - moe.n_split) * row_bytes;
+        } else {
+            wt = w + s * moe.expert_bytes + (int64_t)n0 * row_bytes;
+            if (moe.w2) n_end = moe.n_split;
+        }
+    }
 
     // DMA sources: buffer resources over the tile's first rows to the end of the matrix; rows past M or N read as
     // zeros (the hardware range check), and their outputs are not stored
-    const auto rw = kf_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
-    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
-    const auto rs = kf_rsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(M - m0) * nsb * 32);
-    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    const auto rw = kf_rsrc(wt, (uint64_t)(n_end - n0) * row_bytes);
+    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(m_end - m0) * K);
+    const auto rs = kf_rsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(m_end - m0) * nsb * 32);
+    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(m_end - m0) * kg * 4);
     // Every DMA instruction reads whole rows: 4 activation rows of 256 bytes, or 64 consecutive 16-byte pieces of the
     // weight rows' 144-byte super-blocks (about seven rows), so each 128-byte line a stage needs crosses from L2 once
     // per instruction. Activation instruction i (rows 4 i..) is wave i % 8's; lane l takes chunk (l % 16) ^ (row % 8)
@@ -305,10 +339,17 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
         for (int i = 0; i < G4_TM; i++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int m = m0 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
-                if (m >= M) continue;
-                const int64_t o = (int64_t)m * N + n;
-                y[o] = acc[i][r] + bn + (res ? res[o] : 0.0f);
+                // row m0 + 32 i + (r % 4) + 8 (r / 4) + 4 half: a wave-uniform row base and the lane's offset
+                const int mb = m0 + i * 32 + (r & 3) + 8 * (r >> 2);
+                if (mb + 4 * half >= m_end) continue;
+                if (MOE && moe.out_rows) {
+                    const int64_t o = (int64_t)moe.out_rows[mb + 4 * half] * N + n;
+                    y[o] = acc[i][r] + bn + (res ? res[o] : 0.0f);
+                    continue;
+                }
+                const int64_t ob = (int64_t)mb * N;
+                const int lo = 4 * half * N + n;
+                y[ob + lo] = acc[i][r] + bn + (res ? res[ob + lo] : 0.0f);
             }
     }
 }
@@ -322,8 +363,27 @@ hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act,
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
     const char* base = static_cast<const char*>(act);
     dim3 grid(((N + G4_BN - 1) / G4_BN) * ((M + G4_BM - 1) / G4_BM));
-    gemm_q4k_kernel<<<grid, G4_THREADS, 0, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
-                                                 reinterpret_cast<const _Float16*>(base + o.xa), reinterpret_cast<const float*>(base + o.d32),
-                                                 bias, res, y, M, N, K);
+    gemm_q4k_kernel<false><<<grid, G4_THREADS, 0, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
+                                                        reinterpret_cast<const _Float16*>(base + o.xa),
+                                                        reinterpret_cast<const float*>(base + o.d32), bias, res, y, M, N, K, G4Moe{});
+    return hipGetLastError();
+}
+
+// Grouped (MoE) form: `act` holds `pairs` activation rows in group order (slot s: rows offsets[s]..offsets[s + 1],
+// device offsets), slot s multiplies w + s expert_bytes (N output columns; with w2, columns n_split.. from w2), output
+// row p goes to y row out_rows[p] (nullable: p). Validated by the caller: K a multiple of 256, n_split a multiple of 256.
+hipError_t kf_launch_gemm_q4k_moe(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, int n_split, const void* act,
+                                  int pairs, int n_slots, const int32_t* offsets, const int32_t* out_rows, float* y, int N, int K,
+                                  hipStream_t s) {
+    const kf_act_offsets o = kf_act_layout((size_t)pairs, (size_t)K);
+    const char* base = static_cast<const char*>(act);
+    // row tiles over all slots: each slot adds at most one partial tile
+    const int mt = (pairs + G4_BM - 1) / G4_BM + n_slots;
+    dim3 grid(((N + G4_BN - 1) / G4_BN) * mt);
+    const G4Moe moe{offsets, out_rows, static_cast<const uint8_t*>(w2), expert_bytes, n_slots, n_split};
+    gemm_q4k_kernel<true><<<grid, G4_THREADS, 0, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
+                                                       reinterpret_cast<const _Float16*>(base + o.xa),
+                                                       reinterpret_cast<const float*>(base + o.d32), nullptr, nullptr, y, mt * G4_BM, N, K,
+                                                       moe);
     return hipGetLastError();
 }

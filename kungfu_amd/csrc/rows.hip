@@ -467,6 +467,37 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
               : rows_dispatch<KF_TYPE_Q8_0, false>(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, bias, res, y, s);
 }
 
+// The quantized activation rows of the routed pairs in group order, for the grouped GEMM: row p of dst is row
+// order[p] / n_used (the pair's token) of src, for the pairs moe_group placed (p < offsets[n_slots]). Copies the sections
+// the q4_K GEMM reads: q, the per-32 scales and the mins operands (xa). One block a pair row.
+__global__ void __launch_bounds__(256) moe_gather_act_kernel(const int8_t* __restrict__ sq, const float* __restrict__ sd32,
+                                                             const uint4* __restrict__ sxa, int8_t* __restrict__ dq,
+                                                             float* __restrict__ dd32, uint4* __restrict__ dxa,
+                                                             const int32_t* __restrict__ order, const int32_t* __restrict__ offsets,
+                                                             int n_slots, int n_used, int n) {
+    const int p = blockIdx.x;
+    if (p >= offsets[n_slots]) return;
+    const int64_t t = order[p] / n_used;
+    const uint4* src = reinterpret_cast<const uint4*>(sq + t * n);
+    uint4* dst = reinterpret_cast<uint4*>(dq + (int64_t)p * n);
+    for (int i = threadIdx.x; i < n / 16; i += blockDim.x) dst[i] = src[i];
+    for (int i = threadIdx.x; i < n / 32; i += blockDim.x) dd32[(int64_t)p * (n / 32) + i] = sd32[t * (n / 32) + i];
+    for (int i = threadIdx.x; i < n / 256 * 2; i += blockDim.x) dxa[(int64_t)p * (n / 256) * 2 + i] = sxa[t * (n / 256) * 2 + i];
+}
+
+hipError_t kf_launch_moe_gather_act(const void* src, int src_rows, void* dst, int pairs, const int32_t* order, const int32_t* offsets,
+                                    int n_slots, int n_used, int n, hipStream_t s) {
+    if (pairs == 0) return hipSuccess;
+    const kf_act_offsets so = kf_act_layout((size_t)src_rows, (size_t)n), dso = kf_act_layout((size_t)pairs, (size_t)n);
+    const char* sb = static_cast<const char*>(src);
+    char* db = static_cast<char*>(dst);
+    moe_gather_act_kernel<<<pairs, 256, 0, s>>>(reinterpret_cast<const int8_t*>(sb + so.q), reinterpret_cast<const float*>(sb + so.d32),
+                                                reinterpret_cast<const uint4*>(sb + so.xa), reinterpret_cast<int8_t*>(db + dso.q),
+                                                reinterpret_cast<float*>(db + dso.d32), reinterpret_cast<uint4*>(db + dso.xa), order, offsets,
+                                                n_slots, n_used, n);
+    return hipGetLastError();
+}
+
 hipError_t kf_launch_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, hipStream_t s) {
     moe_group_kernel<<<1, 256, (size_t)n_slots * sizeof(int), s>>>(slots, total, n_slots, order, offsets);
     return hipGetLastError();

@@ -102,8 +102,18 @@ def test_moe_gemv_matches_per_pair_products(cuda, ty, glu):
         _close(got[p], want.astype(np.float32))
 
 
+# routed pairs past which kf_hip_moe_ffn runs q4_K experts as the grouped tile GEMM (the reference's MOE_MATVEC_ROWS,
+# crates/kf-backend-cuda/src/exec.rs:2196)
+MOE_GEMM_PAIRS = 64
+
+
+def _takes_gemm(ty, rows, n_used, n_embd, n_ff):
+    return ty == kf.TYPE_Q4_K and rows * n_used > MOE_GEMM_PAIRS and n_embd % 256 == 0 and n_ff % 256 == 0
+
+
 def _moe_layer(cuda, ty, n_exp, n_embd, n_ff, rows, n_used, seed, drop=0.0):
-    """kf_hip_moe_ffn on seeded inputs, and the same layer run stage by stage through the C ABI."""
+    """kf_hip_moe_ffn on seeded inputs, and the same layer run stage by stage through the C ABI (the few-row products,
+    or past 64 q4_K pairs the grouped GEMM on the pairs' activation rows in group order)."""
     import torch
 
     gate = _experts(ty, n_exp, n_ff, n_embd, seed)
@@ -115,24 +125,50 @@ def _moe_layer(cuda, ty, n_exp, n_embd, n_ff, rows, n_used, seed, drop=0.0):
     scratch = torch.empty(kf.moe_scratch_bytes(rows, n_used, n_embd, n_ff, n_exp), dtype=torch.uint8, device=cuda)
     out = torch.full((rows, n_embd), float("nan"), device=cuda)
     kf.moe_ffn(ty, g_, u_, d_, n_exp, n_embd, n_ff, x_, s_, w_, out, scratch)
-    # the stages: group, fused gate/up, quantized hidden rows, grouped down, combine
+    # the stages: group, gate/up, quantized hidden rows, down, combine
     pairs = rows * n_used
     order = torch.empty(pairs, dtype=torch.int32, device=cuda)
     offsets = torch.empty(n_exp + 1, dtype=torch.int32, device=cuda)
     kf.moe_group(s_, pairs, n_exp, order, offsets)
-    act = kf.alloc_act(rows, n_embd, cuda)
-    kf.quant_act(x_, act, kf.act_kind(ty))
-    hidden = torch.zeros((pairs, n_ff), device=cuda)
-    kf.moe_gemv(ty, g_, act, rows, n_embd, n_ff, order, offsets, n_exp, n_used, False, hidden, w_up=u_)
-    hact = kf.alloc_act(pairs, n_ff, cuda)
-    kf.quant_act(hidden, hact, kf.act_kind(ty))
     part = torch.zeros((pairs, n_embd), device=cuda)
-    kf.moe_gemv(ty, d_, hact, pairs, n_ff, n_embd, order, offsets, n_exp, n_used, True, part)
+    stages = {}
+    if _takes_gemm(ty, rows, n_used, n_embd, n_ff):
+        torch.cuda.synchronize()
+        routed = int(offsets[-1].item())
+        order_h = order.cpu().numpy()[:routed]
+        # the pairs' rows in group order, quantized (the same rows the layer gathers)
+        xg = kf.alloc_act(pairs, n_embd, cuda)
+        xrows = np.zeros((pairs, n_embd), np.float32)
+        xrows[:routed] = x[order_h // n_used]
+        kf.quant_act(_t(xrows, cuda), xg, kf.act_kind(ty))
+        gu = torch.zeros((pairs, 2 * n_ff), device=cuda)
+        eb_gu, eb_dn = n_ff * kf.row_bytes(ty, n_embd), n_embd * kf.row_bytes(ty, n_ff)
+        kf.moe_gemm(ty, g_, xg, pairs, n_embd, 2 * n_ff, offsets, n_exp, gu, eb_gu, w2=u_, n_split=n_ff)
+        hact = kf.alloc_act(pairs, n_ff, cuda)
+        kf.gated_act_q8(gu, gu[:, n_ff:], hact, kf.act_kind(ty), pairs, n_ff, 2 * n_ff)
+        kf.moe_gemm(ty, d_, hact, pairs, n_ff, n_embd, offsets, n_exp, part, eb_dn, out_rows=order)
+        torch.cuda.synchronize()
+        q, d16, s16 = (t.cpu().numpy() for t in kf.act_views(hact, pairs, n_ff)[:3])
+        stages.update(order=order_h, gu=gu.cpu().numpy(), hq=q, hd16=d16, hs16=s16)
+    else:
+        act = kf.alloc_act(rows, n_embd, cuda)
+        kf.quant_act(x_, act, kf.act_kind(ty))
+        hidden = torch.zeros((pairs, n_ff), device=cuda)
+        kf.moe_gemv(ty, g_, act, rows, n_embd, n_ff, order, offsets, n_exp, n_used, False, hidden, w_up=u_)
+        hact = kf.alloc_act(pairs, n_ff, cuda)
+        kf.quant_act(hidden, hact, kf.act_kind(ty))
+        kf.moe_gemv(ty, d_, hact, pairs, n_ff, n_embd, order, offsets, n_exp, n_used, True, part)
+        stages["hidden"] = hidden.cpu().numpy()
     staged = torch.full((rows, n_embd), float("nan"), device=cuda)
     kf.moe_combine(part, w_, s_, staged, rows, n_used, n_embd)
     torch.cuda.synchronize()
-    stages = {"hidden": hidden.cpu().numpy(), "part": part.cpu().numpy(), "out": staged.cpu().numpy()}
+    stages.update(part=part.cpu().numpy(), out=staged.cpu().numpy())
     return (gate, up, down, x, sel, wts), out.cpu().numpy(), stages
+
+
+def _silu_mul(g, u):
+    g = g.astype(np.float64)
+    return (g / (1 + np.exp(-g))) * u
 
 
 def _check_layer(got, stages, args, ty, n_exp, n_embd, n_ff, rows_checked):
@@ -142,10 +178,15 @@ def _check_layer(got, stages, args, ty, n_exp, n_embd, n_ff, rows_checked):
     own int8-vs-float bound (experts.rs:181-217: 2e-2 of the mean magnitude). The layer is not held to 1e-3 against
     the CPU as a whole: the hidden row is quantized again between the two products, and a last-bit difference in a
     float sum (the GPU adds in another order) can move one hidden value across a rounding boundary, which shifts
-    every output of the row by d * w."""
+    every output of the row by d * w. On the grouped-GEMM path the gate and up products are checked apart, the
+    quantized hidden row against the CPU quantizer of silu(gate) * up on the GPU's products (bit for bit, as the CPU
+    backend's gated activation), and down on the GPU's quantized hidden row through the integer dot product."""
     gate, up, down, x, sel, wts = args
     n_used = sel.shape[1]
     assert np.array_equal(got, stages["out"])
+    gemm = "gu" in stages
+    if gemm:
+        where = {int(p): i for i, p in enumerate(stages["order"])}
     for r in range(rows_checked):
         want = np.zeros(n_embd, np.float64)
         for j in range(n_used):
@@ -154,9 +195,20 @@ def _check_layer(got, stages, args, ty, n_exp, n_embd, n_ff, rows_checked):
                 continue
             g = oracle.matmul_i8(ty, gate[e * n_ff : (e + 1) * n_ff], n_embd, n_ff, x[r])[0]
             u = oracle.matmul_i8(ty, up[e * n_ff : (e + 1) * n_ff], n_embd, n_ff, x[r])[0]
-            h = (g.astype(np.float64) / (1 + np.exp(-g.astype(np.float64)))) * u
-            _close(stages["hidden"][p], h.astype(np.float32))
-            y = oracle.matmul_i8(ty, down[e * n_embd : (e + 1) * n_embd], n_ff, n_embd, stages["hidden"][p])[0]
+            if gemm:
+                i = where[p]
+                gg, gu_ = stages["gu"][i, :n_ff], stages["gu"][i, n_ff:]
+                _close(gg, g)
+                _close(gu_, u)
+                h = oracle.gated(kf.GLU_SILU, gg[None], gu_[None], 1, n_ff, n_ff)
+                wq, wd, ws = oracle.quantize_activations(oracle.act_kind(ty), h)
+                assert np.array_equal(stages["hq"][i], wq[0]) and np.array_equal(stages["hs16"][i], ws[0])
+                assert np.array_equal(stages["hd16"][i].view(np.uint32), wd[0].view(np.uint32))
+                dn = down[e * n_embd : (e + 1) * n_embd]
+                y = np.array([oracle.dot_i8(ty, dn[o], wq, wd, ws)[0] for o in range(n_embd)], np.float32)
+            else:
+                _close(stages["hidden"][p], _silu_mul(g, u).astype(np.float32))
+                y = oracle.matmul_i8(ty, down[e * n_embd : (e + 1) * n_embd], n_ff, n_embd, stages["hidden"][p])[0]
             _close(stages["part"][p], y)
             want += float(wts[r, j]) * stages["part"][p].astype(np.float64)
         _close(got[r], want.astype(np.float32), rtol=1e-5, atol=1e-6)
@@ -229,6 +281,22 @@ def test_moe_ffn_128_experts_top_8(cuda, rows):
     n_exp, n_embd, n_ff, n_used = 128, 256, 512, 8
     args, got, stages = _moe_layer(cuda, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows, n_used, 60 + rows)
     _check_layer(got, stages, args, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows)
+
+
+@pytest.mark.parametrize("rows,n_exp", [(512, 8), (100, 3)])
+def test_moe_ffn_grouped_gemm_top_2(cuda, rows, n_exp):
+    """Past 64 routed pairs the q4_K layer runs on the grouped tile GEMM: 512 tokens top-2 over eight experts (about
+    128 pairs an expert, one or two row tiles each), and 100 tokens over three (two tiles, the second partial), with
+    some pairs unused; sampled tokens against the CPU backend stage by stage and the float path."""
+    n_embd, n_ff, n_used = 1024, 1536, 2
+    args, got, stages = _moe_layer(cuda, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows, n_used, 70 + n_exp, drop=0.05)
+    assert "gu" in stages
+    _check_layer(got, stages, args, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, 6)
+    dead = (args[4] < 0).all(axis=1)
+    assert not got[dead].any()
+    # every token against the float path at the same bound
+    flt = oracle.moe_ffn(kf.TYPE_Q4_K, *args[:3], n_exp, n_embd, n_ff, args[3], args[4], args[5])
+    assert np.abs(got - flt).max() <= 2e-2 * max(np.abs(flt).mean(), 1e-6)
 
 
 def test_moe_ffn_config_c5_first_tokens(cuda):
