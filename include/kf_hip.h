@@ -131,7 +131,9 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
 
 /* The whole Op::MatMul of one weight: quantize x into `act` (device scratch of kf_hip_act_bytes(rows, n_in)) and run
  * the product the row count and shape select (q4_K: the few-row product or the tile GEMM, whichever a cost model
- * fitted on MI355X favours). Replaces matmul_launch (exec.rs:2061-2093). */
+ * fitted on MI355X favours). Replaces matmul_launch (exec.rs:2061-2093). One row of q8_0 / q4_K (n_in <= 4096, x
+ * and the weights 16-byte aligned) runs as one launch: the GEMV quantizes x itself, to the same integers, and `act`
+ * is left unwritten (environment KF_MATMUL_NO_FUSE: two launches, as for other shapes). */
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream);
 
@@ -165,7 +167,8 @@ int kf_hip_gemv_group(uint32_t ty, const void* w, int64_t row_bytes, const void*
                       int nseg, void* stream);
 
 /* kf_hip_matmul for a group: quantize x once, then the grouped product (each member's product chosen by the row
- * count as kf_hip_matmul chooses it). Replaces matmul_group_launch (exec.rs:1283-1346). */
+ * count as kf_hip_matmul chooses it); one row of q8_0 / q4_K is one launch that quantizes x itself, as in
+ * kf_hip_matmul. Replaces matmul_group_launch (exec.rs:1283-1346). */
 int kf_hip_matmul_group(uint32_t ty, const void* w, int n_in, const float* x, int rows, void* act, float* y, const int64_t* segs, int nseg,
                         void* stream);
 

@@ -31,6 +31,8 @@ hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const 
                            const float* bias, const float* res, float* y, int n, int n_out, int maxit, const KfSegs* segs, hipStream_t s);
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
                                 int32_t* out, hipStream_t s);
+hipError_t kf_launch_gemv1_fused(uint32_t ty, const void* w, int64_t row_bytes, const float* x, const float* bias, const float* res, float* y,
+                                 int n, int n_out, const KfSegs* segs, hipStream_t s);
 int kf_gemv_max_n();
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s);
@@ -106,6 +108,9 @@ int gemv_maxit() {
     const int v = e ? atoi(e) : 0;
     return v < 0 ? 0 : v;
 }
+
+// KF_MATMUL_NO_FUSE set: one-row matmuls quantize into `act` and run the GEMV as two launches (a comparison knob)
+bool no_fusion() { return getenv("KF_MATMUL_NO_FUSE") != nullptr; }
 
 int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float* bias, const float* res, float* y, int rows, int n_in,
             int n_out, void* stream);
@@ -245,6 +250,12 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
     const int64_t rb = (int64_t)(n_in / block) * bytes;
     const int rc = check_product(ty, w, rb, act, y, rows, n_in, n_out);
     if (rc != KF_OK) return rc;
+    if (rows == 1 && x && !no_fusion()) {
+        // one launch: the GEMV quantizes its activation row itself
+        const hipError_t e = kf_launch_gemv1_fused(ty, w, rb, x, bias, res, y, n_in, n_out, nullptr, static_cast<hipStream_t>(stream));
+        if (e == hipSuccess) return KF_OK;
+        if (e != hipErrorNotSupported) return hip_fail(e, "fused gemv launch");
+    }
     const int q = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
     if (q != KF_OK) return q;
     return product(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
@@ -320,20 +331,26 @@ int unpack_segs(const void* w, float* y, const int64_t* segs, int nseg, std::vec
     return KF_OK;
 }
 
+// The kernels' member table of a group
+KfSegs seg_table(const std::vector<Member>& ms) {
+    KfSegs sg{};
+    sg.n = (int)ms.size();
+    for (size_t i = 0; i < ms.size(); i++) {
+        sg.start[i] = ms[i].start;
+        sg.w[i] = ms[i].w;
+        sg.y[i] = ms[i].y;
+        sg.bias[i] = ms[i].bias;
+        sg.res[i] = ms[i].res;
+    }
+    return sg;
+}
+
 // The grouped product over quantized activations: one GEMV launch over the stacked rows for one activation row of
 // q8_0 / q4_K, otherwise each member's product against the shared activations
 int group_product(uint32_t ty, const std::vector<Member>& ms, int64_t rb, const void* act, int rows, int n, int total, bool select,
                   void* stream) {
     if (rows == 1 && (ty == KF_TYPE_Q8_0 || ty == KF_TYPE_Q4_K) && n <= kf_gemv_max_n()) {
-        KfSegs sg{};
-        sg.n = (int)ms.size();
-        for (size_t i = 0; i < ms.size(); i++) {
-            sg.start[i] = ms[i].start;
-            sg.w[i] = ms[i].w;
-            sg.y[i] = ms[i].y;
-            sg.bias[i] = ms[i].bias;
-            sg.res[i] = ms[i].res;
-        }
+        const KfSegs sg = seg_table(ms);
         const kf_act_offsets o = kf_act_layout(1, (size_t)n);
         const char* base = static_cast<const char*>(act);
         const hipError_t e = kf_launch_gemv1(ty, ms[0].w, rb, reinterpret_cast<const int8_t*>(base + o.q), reinterpret_cast<const int32_t*>(base + o.s32),
@@ -376,6 +393,13 @@ int kf_hip_matmul_group(uint32_t ty, const void* w, int n_in, const float* x, in
     if (rc != KF_OK) return rc;
     rc = check_product(ty, w, rb, act, y, rows, n_in, total);
     if (rc != KF_OK) return rc;
+    if (rows == 1 && x && !no_fusion()) {
+        // one launch over the stacked rows, quantizing the activation row itself
+        const KfSegs sg = seg_table(ms);
+        const hipError_t e = kf_launch_gemv1_fused(ty, ms[0].w, rb, x, nullptr, nullptr, ms[0].y, n_in, total, &sg, static_cast<hipStream_t>(stream));
+        if (e == hipSuccess) return KF_OK;
+        if (e != hipErrorNotSupported) return hip_fail(e, "fused grouped gemv launch");
+    }
     rc = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
     if (rc != KF_OK) return rc;
     return group_product(ty, ms, rb, act, rows, n_in, total, true, stream);

@@ -18,6 +18,7 @@
 
 #include "kf_blocks.h"
 #include "kf_host.h"
+#include "kf_qa.h"
 
 #include <algorithm>
 
@@ -164,6 +165,61 @@ __device__ __forceinline__ void gv_stage_store(uint8_t* smem, size_t sums_at, si
     }
 }
 
+// The fused variants (QX > 0) quantize the f32 activation row themselves, in place of a quant_act launch before the
+// product: wave w owns the 256-column chunks w, w + GV_WAVES, ... (QX of them, n <= QX * GV_WAVES * 256). Its loads
+// are issued before the weight requests, so quantizing waits on them alone; the integers, scales and sums are
+// kf_qa_quant's, the same as the quant_act kernel writes, parked in the layout the staged variants fill.
+template <int QX>
+struct GvXf {
+    float4 v[QX > 0 ? QX : 1];
+};
+
+template <int QX>
+__device__ __forceinline__ void gv_xf_load(GvXf<QX>& r, const float* __restrict__ x, int n, int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < QX; i++) {
+        // unpredicated: a lane past the row's end reloads the row's last four columns, which it does not quantize
+        const int c0 = (wave + GV_WAVES * i) * 256 + 4 * lane;
+        r.v[i] = *reinterpret_cast<const float4*>(x + min(c0, n - 4));
+    }
+}
+
+template <uint32_t TY, int QX>
+__device__ __forceinline__ void gv_xf_quant(uint8_t* smem, size_t sums_at, size_t scales_at, const GvXf<QX>& r, int n, int wave, int lane) {
+    constexpr int kind = TY == KF_TYPE_Q4_K ? KF_ACT_Q8K : KF_ACT_Q8_0;
+#pragma unroll
+    for (int i = 0; i < QX; i++) {
+        const int ch = wave + GV_WAVES * i;
+        if (ch * 256 >= n) break;  // wave-uniform
+        const int c0 = ch * 256 + 4 * lane;
+        const bool in = c0 < n;
+        float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (in) {
+            v[0] = r.v[i].x;
+            v[1] = r.v[i].y;
+            v[2] = r.v[i].z;
+            v[3] = r.v[i].w;
+        }
+        const KfQa q = kf_qa_quant(v, c0, in, kind);
+        if (in) {
+            const int c = c0 >> 4;  // the 16-column piece, placed as the staged variants place it
+            int dst;
+            if constexpr (TY == KF_TYPE_Q4_K) {
+                const int sb = c >> 4, jj = (c >> 2) & 3, k = c & 3;
+                dst = (((sb >> 4) * 4 + k) << 6) + ((sb & 15) << 2) + jj;
+            } else {
+                const int b = c >> 1, k = c & 1;
+                dst = (((b >> 6) * 2 + k) << 6) + (b & 63);
+            }
+            *reinterpret_cast<uint32_t*>(smem + (size_t)dst * 16 + (c0 & 15)) = q.packed;
+            if ((lane & 7) == 0) {
+                if constexpr (TY == KF_TYPE_Q4_K) reinterpret_cast<int32_t*>(smem + sums_at)[c0 >> 5] = q.sum32;
+                reinterpret_cast<float*>(smem + scales_at)[c0 >> 5] = q.d;
+            }
+        }
+    }
+}
+
 // Per-lane constants of the weight pieces: lane l moves the 16-byte pieces l, l+64 and l+128 of a step
 struct GvLane {
     int lane;
@@ -232,7 +288,8 @@ template <uint32_t TY, int SPW, int WPR, int MAXIT>
 __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                           const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                           const float* __restrict__ bias, const float* __restrict__ res,
-                                                          float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg) {
+                                                          float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
+                                                          const float* __restrict__) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
@@ -368,7 +425,8 @@ template <uint32_t TY, int SPW, int WPR, int MAXIT>
 __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                               const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                               const float* __restrict__ bias, const float* __restrict__ res,
-                                                              float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg) {
+                                                              float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
+                                                              const float* __restrict__) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
@@ -485,11 +543,12 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
 // multiplied, the loads of rows i+1 and i+2 are in flight, so the arithmetic of a wave overlaps its own weight stream
 // (a wave that computes only after all its loads land holds its slot while the memory pipe idles). The activation
 // row reaches LDS by DMA before any weight is requested.
-template <uint32_t TY, int WPR, int D>
+template <uint32_t TY, int WPR, int D, int QX = 0>
 __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                                const float* __restrict__ bias, const float* __restrict__ res,
-                                                               float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg) {
+                                                               float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
+                                                               const float* __restrict__ xf) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;
@@ -508,8 +567,13 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
 
     // the activation row is staged by the first waves only (256 pieces of 16 bytes and 128 sums and scales a wave,
     // all loads issued before the first wait), which then request their own weights; the other waves request theirs
-    // at once, so most waves start streaming without waiting on the activation row
-    {
+    // at once, so most waves start streaming without waiting on the activation row. Fused: every wave loads its f32
+    // chunks first and quantizes them once its first rows' weights are requested
+    GvXf<QX> xr;
+    if constexpr (QX > 0) {
+        gv_xf_load<QX>(xr, xf, n, wave, lane);
+        __builtin_amdgcn_sched_barrier(0);
+    } else {
         const int nchunks = n >> 4, n32 = n >> 5;
         const int nsw = (nchunks + 255) / 256;
         if (!(KF_GV_ABLATE & 1) && wave < nsw) {
@@ -595,6 +659,10 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     uint4 ring[D][GV_PIECES];
 #pragma unroll
     for (int k = 0; k < D; k++) gv_load_step<TY>(ring[k], row_ptr(k), len, ln);
+    if constexpr (QX > 0) {
+        __builtin_amdgcn_sched_barrier(0);
+        gv_xf_quant<TY, QX>(smem, L.sums, L.scales, xr, n, wave, lane);
+    }
     // the activation stores are LDS writes of this block only: waiting on lgkmcnt and a bare barrier order them
     // (__syncthreads would add a release fence that waits on the weight loads as well)
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
@@ -719,7 +787,8 @@ int cu_count() {
     return n;
 }
 
-typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int, const KfSegs);
+typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int, const KfSegs,
+                         const float*);
 
 // Most blocks of one kernel resident per CU at a dynamic LDS size, cached per (kernel, LDS)
 int resident_blocks(GvKernel k, size_t smem) {
@@ -740,35 +809,53 @@ int resident_blocks(GvKernel k, size_t smem) {
     return v;
 }
 
+// The fused variants of one (type, waves a row) for QX f32 chunks a wave (1, 2, 4 or 8): always the pipelined kernel,
+// whose weights travel through registers, so the compiler waits on the activation loads alone (with the one-shot
+// kernel's LDS DMA in flight it waits on everything before the quantization)
+template <uint32_t TY, int WPR>
+GvKernel gv_fused_pipe(int qx) {
+    switch (qx) {
+        case 1: return gemv_pipe_kernel<TY, WPR, KF_GV_DEPTH, 1>;
+        case 2: return gemv_pipe_kernel<TY, WPR, KF_GV_DEPTH, 2>;
+    }
+    return nullptr;
+}
+
+// xf non-null: the fused variants, quantizing the f32 row xf themselves (qx chunks a wave); hipErrorNotSupported when
+// neither fits (the caller then quantizes first)
 template <uint32_t TY, int SPW, int WPR>
 hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
-                       const float* res, float* y, int n, int n_out, int maxit_env, const KfSegs& sg, hipStream_t s) {
+                       const float* res, float* y, int n, int n_out, int maxit_env, const KfSegs& sg, hipStream_t s, const float* xf = nullptr,
+                       int qx = 0) {
     constexpr int RPB = GV_WAVES / WPR;
     const int groups = (n_out + RPB - 1) / RPB;
+    const bool fused = xf != nullptr;
     // row iterations per block: enough blocks that the chip is full, each block's waves holding the loads of all
     // their rows at once
     const int want = maxit_env > 0 ? maxit_env : KF_GV_MAXIT;
     // the DMA variant needs 16-byte aligned rows and activation pieces
-    const bool dma = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 && (reinterpret_cast<uintptr_t>(xq) & 15) == 0 &&
-                     !getenv("KF_GEMV_NO_DMA");
+    const bool dma = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
+                     (reinterpret_cast<uintptr_t>(fused ? static_cast<const void*>(xf) : xq) & 15) == 0 && !getenv("KF_GEMV_NO_DMA");
+    if (fused && (SPW != 1 || !dma)) return hipErrorNotSupported;
     // one row a wave (WPR == 1) and every block resident at once: one-shot waves, each fetching its row straight into
     // LDS (nothing to pipeline: the whole matrix is requested at launch)
-    if (SPW == 1 && WPR == 1 && dma && maxit_env == 0 && !getenv("KF_GEMV_NO_ONESHOT")) {
+    if (!fused && SPW == 1 && WPR == 1 && dma && maxit_env == 0 && !getenv("KF_GEMV_NO_ONESHOT")) {
         const size_t smem = gd_lds(TY, n, 1, WPR, 1, 1).total;
         GvKernel k = gemv_dma_kernel<TY, 1, WPR, 1>;
         if (groups <= cu_count() * resident_blocks(k, smem) && smem <= 65536) {
-            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1, sg);
+            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1, sg, xf);
             return hipGetLastError();
         }
     }
     // the pipelined persistent variant: a resident grid, every wave walking its rows two in flight
-    if (SPW == 1 && dma && !getenv("KF_GEMV_NO_PIPE")) {
+    if (SPW == 1 && dma && (fused || !getenv("KF_GEMV_NO_PIPE"))) {
         static const int depth = [] {
             const char* e = getenv("KF_GEMV_DEPTH");
             const int v = e ? atoi(e) : 0;
             return v >= 2 && v <= 4 ? v : KF_GV_DEPTH;
         }();
-        GvKernel k = depth == 4 ? gemv_pipe_kernel<TY, WPR, 4> : depth == 3 ? gemv_pipe_kernel<TY, WPR, 3> : gemv_pipe_kernel<TY, WPR, 2>;
+        GvKernel k = fused ? gv_fused_pipe<TY, WPR>(qx)
+                           : depth == 4 ? gemv_pipe_kernel<TY, WPR, 4> : depth == 3 ? gemv_pipe_kernel<TY, WPR, 3> : gemv_pipe_kernel<TY, WPR, 2>;
         const size_t base_lds = gd_lds(TY, n, 0, WPR, 1, 1).total;
         // two blocks (16 waves) per CU measured best on MI355X (3.9-4.1 TB/s at 33 MB against 3.2-3.5 with every
         // resident slot filled, where waves contend for the memory pipe); KF_GEMV_BPC overrides it
@@ -778,21 +865,22 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         if (grid > groups) grid = groups;
         const int iters = (groups + grid - 1) / grid;
         const size_t smem = gd_lds(TY, n, iters, WPR, 1, 1).total;
-        if (smem <= 65536) {
-            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg);
+        if (k && smem <= 65536) {
+            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, xf);
             return hipGetLastError();
         }
     }
+    if (fused) return hipErrorNotSupported;
 #define KF_GV_IT(M)                                                                                                      \
     if (want <= M) {                                                                                                     \
         const int grid = (groups + M - 1) / M;                                                                           \
         const int iters = (groups + grid - 1) / grid;                                                                    \
         if (dma && gd_lds(TY, n, iters, WPR, M, SPW).total <= 65536) {                                                   \
             const size_t smem = gd_lds(TY, n, iters, WPR, M, SPW).total;                                                 \
-            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg); \
+            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr); \
         } else {                                                                                                         \
             const size_t smem = gv_lds(TY, n, iters, WPR).total;                                                         \
-            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg); \
+            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr); \
         }                                                                                                                \
         return hipGetLastError();                                                                                        \
     }
@@ -845,6 +933,42 @@ hipError_t kf_launch_gemv1(uint32_t ty, const void* wv, int64_t row_bytes, const
     KF_GV(KF_TYPE_Q8_0, 2, 8)
 #undef KF_GV
     return hipErrorInvalidValue;
+}
+
+// Largest row width the fused single-row GEMV quantizes itself: two 256-column chunks a wave. Every block quantizes
+// the whole row (its waves multiply whole rows), so the quantization's VALU work is repeated in all 512 blocks; at two
+// chunks a wave it hides under the first weight requests (4096 columns: 1.0 us saved against quant_act + GEMV), at
+// seven (14336 columns) it measured 5.5 us slower than the two launches.
+int kf_gemv_fused_max_n() { return 2 * GV_WAVES * 256; }
+
+// The single-row GEMV quantizing its f32 activation row x itself (one launch in place of quant_act + GEMV; the same
+// integers and scales, so the same outputs bit for bit). hipErrorNotSupported when no fused variant fits (n above
+// kf_gemv_fused_max_n, rows or x not 16-byte aligned, a type other than q8_0 / q4_K): the caller quantizes first.
+hipError_t kf_launch_gemv1_fused(uint32_t ty, const void* wv, int64_t row_bytes, const float* x, const float* bias, const float* res, float* y,
+                                 int n, int n_out, const KfSegs* segs, hipStream_t s) {
+    if (n_out == 0) return hipSuccess;
+    if (n > kf_gemv_fused_max_n() || n % 4 != 0 || (ty != KF_TYPE_Q4_K && ty != KF_TYPE_Q8_0)) return hipErrorNotSupported;
+    KfSegs sg{};
+    if (segs) sg = *segs;
+    const uint8_t* w = static_cast<const uint8_t*>(wv);
+    const int steps = ty == KF_TYPE_Q4_K ? (n / 256 + 15) / 16 : (n / 32 + 63) / 64;
+    const int wpr = gv_wpr(steps);
+    const int spw = (steps + wpr - 1) / wpr;
+    const int per_wave = ((n + 255) / 256 + GV_WAVES - 1) / GV_WAVES;
+    const int qx = per_wave <= 1 ? 1 : 2;
+#define KF_GVF(TY, WPR)                                                                                                    \
+    if (ty == TY && spw == 1 && wpr == WPR)                                                                               \
+        return launch_gemv<TY, 1, WPR>(w, row_bytes, nullptr, nullptr, nullptr, bias, res, y, n, n_out, 0, sg, s, x, qx);
+    KF_GVF(KF_TYPE_Q4_K, 1)
+    KF_GVF(KF_TYPE_Q4_K, 2)
+    KF_GVF(KF_TYPE_Q4_K, 4)
+    KF_GVF(KF_TYPE_Q4_K, 8)
+    KF_GVF(KF_TYPE_Q8_0, 1)
+    KF_GVF(KF_TYPE_Q8_0, 2)
+    KF_GVF(KF_TYPE_Q8_0, 4)
+    KF_GVF(KF_TYPE_Q8_0, 8)
+#undef KF_GVF
+    return hipErrorNotSupported;
 }
 
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,

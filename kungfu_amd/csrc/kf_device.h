@@ -37,6 +37,57 @@ __device__ __forceinline__ float kf_dpp(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
 }
 
+template <int CTRL>
+__device__ __forceinline__ int kf_dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, false);
+}
+
+// Lane `lane`'s value of a float, as a wave-uniform value (v_readlane_b32)
+__device__ __forceinline__ float kf_readlane_f(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Lane i's value combined with lane i ^ 16 / i ^ 32 (gfx950 v_permlane16_swap / v_permlane32_swap: the two results
+// hold each lane's own row or half and the partner's, in some order, so a commutative op of the pair is the same
+// on every lane)
+template <typename Op>
+__device__ __forceinline__ uint32_t kf_xor16(uint32_t v, Op op) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return op(r[0], r[1]);
+}
+template <typename Op>
+__device__ __forceinline__ uint32_t kf_xor32(uint32_t v, Op op) {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return op(r[0], r[1]);
+}
+
+// Maximum of a float over the 64 lanes, on every lane: DPP within each row of 16, then the permlane swaps (VALU
+// only, no LDS traffic)
+__device__ __forceinline__ float kf_wave_max_all(float v) {
+    v = fmaxf(v, kf_dpp<0xb1>(v));   // xor 1
+    v = fmaxf(v, kf_dpp<0x4e>(v));   // xor 2
+    v = fmaxf(v, kf_dpp<0x141>(v));  // half-row mirror: lane i and 7 - i
+    v = fmaxf(v, kf_dpp<0x140>(v));  // row mirror: lane i and 15 - i
+    auto fmax_u = [](uint32_t x, uint32_t y) {
+        return __builtin_bit_cast(uint32_t, fmaxf(__builtin_bit_cast(float, x), __builtin_bit_cast(float, y)));
+    };
+    uint32_t u = kf_xor16(__builtin_bit_cast(uint32_t, v), fmax_u);
+    u = kf_xor32(u, fmax_u);
+    return __builtin_bit_cast(float, u);
+}
+
+// Minimum of an int over the 64 lanes, on every lane
+__device__ __forceinline__ int kf_wave_min_all_i(int v) {
+    v = min(v, kf_dpp_i<0xb1>(v));
+    v = min(v, kf_dpp_i<0x4e>(v));
+    v = min(v, kf_dpp_i<0x141>(v));
+    v = min(v, kf_dpp_i<0x140>(v));
+    auto min_u = [](uint32_t x, uint32_t y) { return (uint32_t)min((int)x, (int)y); };
+    uint32_t u = kf_xor16((uint32_t)v, min_u);
+    u = kf_xor32(u, min_u);
+    return (int)u;
+}
+
 // Sum over the 64 lanes of a wave through DPP within each row of 16 lanes and four lane reads across the rows; the
 // result is uniform (held in a scalar register). Full-rate VALU work instead of LDS permutes.
 __device__ __forceinline__ float kf_wave_sum_dpp(float v) {

@@ -1,17 +1,10 @@
-// Activation quantizer: rows of f32 activations into the int8 scratch the products consume.
-//
-// Restates crates/kf-quant/src/lib.rs:81-140 (quantize_activations) on the GPU, in place of the reference's
-// quant_act (crates/kf-backend-cuda/src/kernels/fused.cu:12-21, kf_quant_span common.cuh:231-309):
-//   kind 3 (Q8_0): per 32 columns d = amax/127, q = round-half-away(v / d) with 1/d taken from the unrounded d,
-//                  d stored f16-rounded
-//   kind 4 (Q8K):  per 256 columns, the first value of largest magnitude `mx`, iscale = -127/mx,
-//                  q = min(round-half-even(iscale * v), 127), d = 1/iscale
-// A wave of 64 lanes covers 256 columns, four consecutive columns a lane, so a Q8K block is one wave and a Q8_0 block
-// eight lanes. The integer results are bit-exact with the CPU reference.
-#include "kf_device.h"
+// Activation quantizer: rows of f32 activations into the int8 scratch the products consume, in place of the
+// reference's quant_act (crates/kf-backend-cuda/src/kernels/fused.cu:12-21, kf_quant_span common.cuh:231-309). The
+// per-lane arithmetic (crates/kf-quant/src/lib.rs:81-140) is kf_qa_quant; the integer results are bit-exact with the
+// CPU reference.
+#include "kf_qa.h"
 
-// The reference rounds the f32 product v * id: with contraction, roundf's expansion (trunc, then p - trunc(p)) becomes
-// fma(v, id, -trunc(p)), which sees the unrounded product and turns ties such as 58.4999999 -> 58.5 into 58.
+// The producers' own f32 arithmetic (rms_norm, the gated activation) is written unfused, as the CPU rounds it.
 #pragma clang fp contract(off)
 
 namespace {
@@ -20,82 +13,28 @@ constexpr int QA_THREADS = 256;
 constexpr int QA_SPAN = QA_THREADS * 4;  // columns one block covers
 
 // Quantizes the four columns c0.. of one row held by this thread (v, zeros past n) and writes q, the per-16 and
-// per-32 scales and integer sums. Every thread of the wave calls it (the reductions are wave-wide).
+// per-32 scales and integer sums, and (Q8K) the mins operand of the q4_K GEMM. Every thread of the wave calls it.
 __device__ __forceinline__ void qa_emit(const float (&v)[4], int c0, bool in, int n, int kind, int row, int8_t* __restrict__ q,
                                         float* __restrict__ d16, int32_t* __restrict__ s16, float* __restrict__ d32,
                                         int32_t* __restrict__ s32, _Float16* __restrict__ xa) {
     const int lane = threadIdx.x & 63;
-    int qi[4];
-    float d;
-    if (kind == KF_ACT_Q8_0) {
-        float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        // eight lanes make a block of 32
-        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-        amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
-        const float dd = amax / 127.0f;
-        const float id = dd != 0.0f ? 1.0f / dd : 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; j++) qi[j] = (int)roundf(v[j] * id);
-        d = kf_round_f16(dd);
-    } else {
-        // first index of the largest magnitude: lexicographic max of (|v|, -index) over the wave
-        float a = -1.0f, mx = 0.0f;
-        int idx = 0x7fffffff;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const float aj = in ? fabsf(v[j]) : -1.0f;
-            if (aj > a) {
-                a = aj;
-                idx = c0 + j;
-                mx = v[j];
-            }
-        }
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float oa = __shfl_xor(a, o, 64);
-            const int oi = __shfl_xor(idx, o, 64);
-            const float om = __shfl_xor(mx, o, 64);
-            if (oa > a || (oa == a && oi < idx)) {
-                a = oa;
-                idx = oi;
-                mx = om;
-            }
-        }
-        if (a > 0.0f) {
-            const float iscale = -127.0f / mx;
-            d = 1.0f / iscale;
-#pragma unroll
-            for (int j = 0; j < 4; j++) qi[j] = min((int)rintf(iscale * v[j]), 127);
-        } else {
-            d = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) qi[j] = 0;
-        }
-    }
-    // four lanes make a group of 16, eight a group of 32
-    int sum16 = qi[0] + qi[1] + qi[2] + qi[3];
-    sum16 += __shfl_xor(sum16, 1, 64);
-    sum16 += __shfl_xor(sum16, 2, 64);
-    const int sum32 = sum16 + __shfl_xor(sum16, 4, 64);
+    const KfQa r = kf_qa_quant(v, c0, in, kind);
     if (!in) return;
-    const uint32_t packed = (uint32_t)(qi[0] & 0xff) | ((uint32_t)(qi[1] & 0xff) << 8) | ((uint32_t)(qi[2] & 0xff) << 16) |
-                            ((uint32_t)(qi[3] & 0xff) << 24);
-    *reinterpret_cast<uint32_t*>(q + (size_t)row * n + c0) = packed;
+    *reinterpret_cast<uint32_t*>(q + (size_t)row * n + c0) = r.packed;
     if ((lane & 3) == 0) {
         const size_t g = (size_t)row * (n >> 4) + (c0 >> 4);
-        d16[g] = d;
-        s16[g] = sum16;
+        d16[g] = r.d;
+        s16[g] = r.sum16;
     }
     if ((lane & 7) == 0) {
         const size_t g = (size_t)row * (n >> 5) + (c0 >> 5);
-        d32[g] = d;
-        s32[g] = sum32;
+        d32[g] = r.d;
+        s32[g] = r.sum32;
         if (kind == KF_ACT_Q8K) {
             // the mins operand of the q4_K GEMM: sum32 = 64 hi + lo
             _Float16* xr = xa + ((size_t)row * ((n + 255) >> 8) + (c0 >> 8)) * 16 + ((c0 >> 5) & 7);
-            xr[0] = (_Float16)(float)(sum32 >> 6);
-            xr[8] = (_Float16)(float)(sum32 & 63);
+            xr[0] = (_Float16)(float)(r.sum32 >> 6);
+            xr[8] = (_Float16)(float)(r.sum32 & 63);
         }
     }
 }

@@ -80,7 +80,9 @@ def test_group_one_row_single_launch(cuda, ty, n, sizes):
 
 
 @pytest.mark.parametrize("ty,rows,n,sizes", [
-    (kf.TYPE_Q4_K, 1, 1024, (64, 96, 32)),
+    (kf.TYPE_Q4_K, 1, 1024, (64, 96, 32)),       # one row: one launch that quantizes x itself
+    (kf.TYPE_Q8_0, 1, 4096, (256, 256)),
+    (kf.TYPE_Q4_K, 1, 14336, (96, 40)),
     (kf.TYPE_Q4_K, 3, 1024, (64, 96)),           # the multi-row product per member
     (kf.TYPE_Q8_0, 64, 4096, (256, 128)),        # the int8 GEMM per member
     (kf.TYPE_Q4_K, 200, 1024, (256, 128)),       # the q4_K GEMM per member

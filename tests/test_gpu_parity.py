@@ -242,9 +242,46 @@ def test_gemv_launch_variants(cuda, monkeypatch, dma, maxit, ty, n, n_out):
     x = kf.synth_normal(32, 1.0, n).reshape(1, n)
     act = kf.alloc_act(1, n, cuda)
     y = torch.empty((1, n_out), device=cuda)
-    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    kf.quant_act(_tensor(x, cuda), act, kf.act_kind(ty))
+    kf.gemv(ty, _tensor(w, cuda), act, y, 1, n, n_out)
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+@pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 256, 40), (kf.TYPE_Q4_K, 1280, 300), (kf.TYPE_Q4_K, 4096, 1030),
+                                        (kf.TYPE_Q4_K, 2304, 777), (kf.TYPE_Q4_K, 14336, 64),
+                                        (kf.TYPE_Q8_0, 32, 7), (kf.TYPE_Q8_0, 1056, 300), (kf.TYPE_Q8_0, 4096, 777),
+                                        (kf.TYPE_Q8_0, 2080, 45), (kf.TYPE_Q8_0, 4128, 9)])
+def test_matmul_one_row_fused_equals_two_launches(cuda, monkeypatch, ty, n, n_out):
+    """kf_hip_matmul at one row quantizes inside the GEMV (one launch; up to 4096 columns, past that the two launches):
+    the same integers and scales as quant_act, so its outputs equal quant_act + kf_hip_gemv bit for bit, with bias and
+    residual, on a row with an all-zero block, ties and a negative maximum; and the CPU backend's within the f32 bar."""
+    import torch
+
+    rng = np.random.default_rng(n + n_out)
+    w = _weights(ty, n_out, n, seed=41)
+    x = (rng.standard_normal((1, n)) * rng.uniform(0.01, 20)).astype(np.float32)
+    x[0, : min(n, 256)] = 0.0
+    if n >= 512:
+        x[0, 256:288] = 1.5
+        x[0, 300] = -np.abs(x[0, 256:512]).max() * 1.25
+    bias = kf.synth_normal(42, 1.0, n_out)
+    res = kf.synth_normal(43, 1.0, n_out).reshape(1, n_out)
+    wt, xt, bt, rt = (_tensor(a, cuda) for a in (w, x, bias, res))
+    act = kf.alloc_act(1, n, cuda)
+    y1 = torch.full((1, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, wt, xt, act, y1, n_out, bias=bt, res=rt)
+    y2 = torch.full((1, n_out), float("nan"), device=cuda)
+    kf.quant_act(xt, act, kf.act_kind(ty))
+    kf.gemv(ty, wt, act, y2, 1, n, n_out, bias=bt, res=rt)
+    monkeypatch.setenv("KF_MATMUL_NO_FUSE", "1")
+    y3 = torch.full((1, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, wt, xt, act, y3, n_out, bias=bt, res=rt)
+    torch.cuda.synchronize()
+    got = y1.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), y2.cpu().numpy().view(np.uint32))
+    assert np.array_equal(got.view(np.uint32), y3.cpu().numpy().view(np.uint32))
+    _close(got, oracle.matmul_slice(ty, w, n, n_out, x, bias) + res)
 
 
 GEMM_SHAPES = [(2, 128, 64), (9, 1024, 1000), (130, 512, 200), (256, 4096, 384), (64, 14336, 96), (8, 14336, 520),
