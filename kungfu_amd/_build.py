@@ -23,6 +23,9 @@ HOST_SOURCES = ["api.cpp", "host_quant.cpp", "gguf.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-ffp-contract=fast-honor-pragmas"]
+# per-source additions: the int8 GEMMs take the matrix-core results in ordinary vector registers (no copies out of
+# the accumulation registers before the float rescale that follows every MFMA)
+SOURCE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def hipcc() -> str:
@@ -34,7 +37,7 @@ def hipcc() -> str:
 
 def _compile(src: str, obj: str, device: bool) -> None:
     cmd = [hipcc(), "-c", src, "-o", obj] + COMMON
-    cmd += (["-x", "hip"] + DEVICE_FLAGS) if device else ["-D__HIP_PLATFORM_AMD__"]
+    cmd += (["-x", "hip"] + DEVICE_FLAGS + SOURCE_FLAGS.get(os.path.basename(src), [])) if device else ["-D__HIP_PLATFORM_AMD__"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -28,6 +28,7 @@
 #include "kf_device.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 namespace {
@@ -300,7 +301,17 @@ __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __r
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     uint8_t* lw = smem + wave * SK_WAVE_LDS;
-    const int n0 = blockIdx.x * SK_ROWS, m0 = blockIdx.y * MR;
+    // XCD-aware order (a 1-D grid of gx weight tiles x gy row blocks): the hardware deals blocks to the 8 XCDs in
+    // turn (block b to XCD b % 8), so XCD x takes a contiguous range of (tile, row block) pairs with a tile's row
+    // blocks next to each other: they run together on one XCD and its L2 serves the tile's weights to all of them
+    int tn, tm;
+    {
+        const int gy = (M + MR - 1) / MR, T = (int)gridDim.x, b = (int)blockIdx.x;
+        const int t = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);
+        tn = t / gy;
+        tm = t - tn * gy;
+    }
+    const int n0 = tn * SK_ROWS, m0 = tm * MR;
     const int q = lane >> 4, c = lane & 15;  // operand k-quarter and row/column
     const int kg = K >> 5;
     const int chunks = kg / SK_G;  // K % 256 == 0: whole chunks
@@ -614,6 +625,225 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
         }
 }
 
+// ------------------------------------------------------------------------------------------------ 49..64 rows
+// gemm_q8_0_small_kernel holds a wave's activation operands in registers, so it carries 16 rows (32 spill); past 16
+// rows each further 16-row block streams the weights again. Here a wave holds all 64 (MR_ROWS) rows of its K chunk
+// in LDS instead: per chunk of 4 groups (128 columns) it DMAs the rows' 128 int8 bytes, their 4 scales (group-major)
+// and its weight rows' 136 bytes into one of three buffers, two chunks ahead of the one it multiplies, so a weight
+// byte is read once for all the rows. Rows of a buffer are 128 bytes with 16-byte slot s of row r holding piece
+// s ^ (r % 8), so the MFMA operand reads (16 rows, 8 bytes each) spread over the banks; rows past M and N read as
+// zeros (buffer range check) and are not stored. The block's W waves split K (chunk c to wave c % W) and meet in a
+// fixed-order tree. Per output and group: one int8 MFMA lane result, d_x d_w (exact: both are f16 values) and one
+// FMA, as the small kernel. What bounds it: every block re-reads all M x K activation bytes, M / 16 times its weight
+// bytes, so it beats four 16-row passes only where it measured so (see the launcher).
+constexpr int MR_ROWS = 64, MR_TM = MR_ROWS / 16;
+constexpr int MR_G = 4;                                   // groups per chunk
+constexpr int MR_ACT = MR_ROWS * MR_G * 32;               // 8192 bytes of activations a chunk
+constexpr int MR_ABUF = MR_ACT + MR_ROWS * MR_G * 4;      // + the scales: 9216
+constexpr int MR_WCH = MR_G * KF_Q8_0_BYTES;              // 136 weight bytes a row and chunk
+
+
+// The kernel below issues its LDS DMA through inline assembly. The compiler's own waits for DMA written LDS are
+// conservative (a read of one buffer waited for the DMA into another, serializing the chunks); here every wait is
+// explicit: loads complete in issue order and the loop waits for exact vmcnt counts. The descriptor is the raw buffer
+// kf_rsrc builds: base, stride 0, num_records bytes (reads past it return zeros), word 3 0x00020000.
+typedef int mr_v4i __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ mr_v4i mr_rsrc(const void* base, uint64_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return mr_v4i{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)n, 0x00020000};
+}
+
+__device__ __forceinline__ uint32_t mr_lds_addr(const void* p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// buffer_load_dwordx4 / _dword ... lds: lane l writes the 16 (4) bytes at voff + soff of the buffer to lds + 16 l (4 l)
+__device__ __forceinline__ void mr_dma16(mr_v4i r, int voff, int soff, const void* lds) {
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+                 "s"(mr_lds_addr(lds))
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void mr_dma4(mr_v4i r, int voff, int soff, const void* lds) {
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
+                 "s"(mr_lds_addr(lds))
+                 : "memory", "m0");
+}
+
+template <int TN, int W>
+__global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                              const float* __restrict__ xd32, const float* __restrict__ bias,
+                                                              const float* __restrict__ res, float* __restrict__ y, int M, int N, int K) {
+    constexpr int ROWS = 16 * TN;                  // weight rows of the block (every wave: all of them, its own K chunks)
+    constexpr int WB = ROWS * MR_WCH;              // weight bytes a chunk, rows MR_WCH apart in the buffer
+    constexpr int WI = (WB / 4 + 63) / 64;         // dword DMA instructions for them
+    constexpr int BUF = MR_ABUF + WI * 256;        // one chunk: activations, scales, weights
+    constexpr int NI = MR_ROWS / 8 + MR_G + WI;    // memory instructions a chunk
+    static_assert(2 * NI <= 63, "two chunks in flight fit the vmcnt counter");
+    static_assert(BUF >= MR_TM * TN * 4 * 64 * 4, "a wave's buffer holds its partial tile for the tree");
+    __shared__ __align__(16) uint8_t abuf0[W * BUF];
+    __shared__ __align__(16) uint8_t abuf1[W * BUF];
+    __shared__ __align__(16) uint8_t abuf2[W * BUF];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int c = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * ROWS;
+    const int kg = K >> 5;
+    const int chunks = K / (32 * MR_G);
+    uint8_t* const ab[3] = {abuf0 + wave * BUF, abuf1 + wave * BUF, abuf2 + wave * BUF};
+
+    // activation DMA sources: instruction i (rows 8 i..) lane l: row 8 i + l / 8, piece (l % 8) ^ (row % 8); scales:
+    // lane l row l, 16 bytes
+    const mr_v4i rx = mr_rsrc(xq, (uint64_t)M * K);
+    const mr_v4i rd = mr_rsrc(xd32, (uint64_t)M * kg * 4);
+    const int xr = lane >> 3, xs = lane & 7;
+    const int va = xr * K + 16 * (xs ^ (xr & 7));  // + 8 i K for instruction i (row 8 i + xr: same row % 8)
+    const int vd = lane * kg * 4;  // scales: instruction g moves group g of the 64 rows (lane l: row l), [group][row]
+    // weight DMA: instruction i lane l moves the dword at byte e = 256 i + 4 l of the chunk's [ROWS][136] block: row
+    // e / 136, offset e % 136 (rows past N read as zeros: the resource ends at the matrix's last row)
+    const mr_v4i rw = mr_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)max(N - n0, 0) * row_bytes);
+    int vw[WI];
+#pragma unroll
+    for (int i = 0; i < WI; i++) {
+        const int e = min(256 * i + 4 * lane, WB - 4);
+        const int r = e / MR_WCH;
+        vw[i] = r * (int)row_bytes + (e - r * MR_WCH);
+    }
+
+    // every wave issues the same number of memory instructions per chunk slot (a slot past its last chunk reloads the
+    // last one), so the vmcnt counts below are exact
+    const int last = chunks - 1;
+    auto issue = [&](auto kb, int ch) __attribute__((always_inline)) {
+        constexpr int B = decltype(kb)::value;
+        const int cc = min(ch, last);
+#pragma unroll
+        for (int i = 0; i < MR_ROWS / 8; i++) mr_dma16(rx, va + 8 * i * K, cc * (32 * MR_G), ab[B] + 1024 * i);
+#pragma unroll
+        for (int g = 0; g < MR_G; g++) mr_dma4(rd, vd, (cc * MR_G + g) * 4, ab[B] + MR_ACT + 256 * g);
+#pragma unroll
+        for (int i = 0; i < WI; i++) mr_dma4(rw, vw[i], cc * MR_WCH, ab[B] + MR_ABUF + 256 * i);
+    };
+
+    v4f acc[MR_TM][TN];
+#pragma unroll
+    for (int t = 0; t < MR_TM; t++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[t][j] = v4f{};
+
+    // one chunk out of activation buffer B and the parked weights
+    auto compute = [&](auto kb) __attribute__((always_inline)) {
+        constexpr int B = decltype(kb)::value;
+        const uint8_t* a_b = ab[B];
+#pragma unroll
+        for (int g = 0; g < MR_G; g++) {
+            long b[TN];
+            float dw[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint8_t* wp = a_b + MR_ABUF + (16 * j + c) * MR_WCH + g * KF_Q8_0_BYTES;
+                const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
+                b[j] = (long)bv.x | ((long)bv.y << 32);
+                dw[j] = (float)*reinterpret_cast<const _Float16*>(wp);
+            }
+#pragma unroll
+            for (int t = 0; t < MR_TM; t++) {
+                const int r = 16 * t + c;
+                const int sl = (2 * g + (q >> 1)) ^ (r & 7);
+                const long a = *reinterpret_cast<const long*>(a_b + r * (32 * MR_G) + 16 * sl + 8 * (q & 1));
+                // the output lane holds activation rows 16 t + 4 q + k: their four scales of group g, one read
+                const v4f dx = *reinterpret_cast<const v4f*>(a_b + MR_ACT + 256 * g + 4 * (16 * t + 4 * q));
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    const v4i_ ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b[j], v4i_{}, 0, 0, 0);
+                    // d_x d_w I: the f32 products the reference forms (d_x and d_w are f16 values, so d_x d_w is exact)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[t][j][k] = fmaf((float)ci[k], dx[k] * dw[j], acc[t][j][k]);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);  // keep the groups apart: bounded registers
+        }
+    };
+
+    // the wave's chunks wave, wave + W, ...: slot i uses buffer i % 3, and chunk i + 2 is requested before chunk i is
+    // multiplied. Loads complete in issue order, so waiting until the two later chunks' 2 NI instructions are the only
+    // ones outstanding lands chunk i (DMA into LDS, which the compiler's register waits do not track). Nothing in the
+    // loop writes LDS, so the compiler adds no waits of its own for the DMA in flight.
+    const int mine = chunks > wave ? (chunks - wave + W - 1) / W : 0;
+    auto step = [&](auto kb, int i) __attribute__((always_inline)) {
+        constexpr int B = decltype(kb)::value;
+        constexpr int B2 = (B + 2) % 3;
+        issue(std::integral_constant<int, B2>{}, wave + (i + 2) * W);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(2 * NI));
+        compute(kb);
+    };
+    if (mine > 0) {
+        issue(std::integral_constant<int, 0>{}, wave);
+        issue(std::integral_constant<int, 1>{}, wave + W);
+        step(std::integral_constant<int, 0>{}, 0);
+        for (int i = 1; i < mine; i += 3) {
+            step(std::integral_constant<int, 1>{}, i);
+            if (i + 1 >= mine) break;
+            step(std::integral_constant<int, 2>{}, i + 1);
+            if (i + 2 >= mine) break;
+            step(std::integral_constant<int, 0>{}, i + 2);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));  // the reloads past the last chunk land before the buffers are reused
+
+    // fixed-order tree over the waves (W a power of two): the upper half stores its tile, the lower half adds
+    if (W > 1) {
+        __syncthreads();
+        for (int half = W / 2; half >= 1; half >>= 1) {
+            if (wave >= half && wave < 2 * half) {
+                float* p = reinterpret_cast<float*>(abuf0 + (wave - half) * BUF) + lane;
+#pragma unroll
+                for (int t = 0; t < MR_TM; t++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) p[((t * TN + j) * 4 + k) * 64] = acc[t][j][k];
+            }
+            __syncthreads();
+            if (wave < half) {
+                const float* p = reinterpret_cast<const float*>(abuf0 + wave * BUF) + lane;
+#pragma unroll
+                for (int t = 0; t < MR_TM; t++)
+#pragma unroll
+                    for (int j = 0; j < TN; j++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) acc[t][j][k] += p[((t * TN + j) * 4 + k) * 64];
+            }
+            __syncthreads();
+        }
+    }
+    if (wave != 0) return;
+    // 16 x 16 accumulator layout: lane l holds weight row l % 16 of tile j, register k activation row 4 (l / 16) + k
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        const int n = n0 + 16 * j + c;
+        if (n >= N) continue;
+        const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+        for (int t = 0; t < MR_TM; t++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const int m = 16 * t + 4 * q + k;
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[t][j][k] + bn + (res ? res[o] : 0.0f);
+            }
+    }
+}
+
+template <int TN, int W>
+hipError_t gemm_mr_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
+                          float* y, int M, int N, int K, hipStream_t s) {
+    gemm_q8_0_mr_kernel<TN, W><<<(N + 16 * TN - 1) / (16 * TN), 64 * W, 0, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    return hipGetLastError();
+}
+
 template <int WM, int WN, int TM, int TN>
 hipError_t gemm_q8_0_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
                                 float* y, int M, int N, int K, hipStream_t s) {
@@ -643,7 +873,8 @@ hipError_t gemm_small_launch(const uint8_t* w, int64_t row_bytes, const int8_t* 
     auto* fn = gemm_q8_0_small_kernel<MR, TN>;
     const hipError_t e = kf_raise_lds(reinterpret_cast<const void*>(fn), 8 * SkGeo<TN>::WAVE_LDS);
     if (e != hipSuccess) return e;
-    fn<<<dim3((N + SkGeo<TN>::ROWS - 1) / SkGeo<TN>::ROWS, (M + MR - 1) / MR), 64 * W, W * SkGeo<TN>::WAVE_LDS, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    fn<<<dim3(((N + SkGeo<TN>::ROWS - 1) / SkGeo<TN>::ROWS) * ((M + MR - 1) / MR)), 64 * W, W * SkGeo<TN>::WAVE_LDS, s>>>(w, row_bytes, xq, xd32, bias, res,
+                                                                                                                 y, M, N, K);
     return hipGetLastError();
 }
 
@@ -688,7 +919,17 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
     const auto* wb = static_cast<const uint8_t*>(w);
     // the small-batch kernel reads whole 16-byte pieces of rows, which needs 16-byte aligned rows (K % 256 == 0)
-    if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31)) {
+    if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31) && !getenv("KF_GEMM_TILE")) {
+        if (M > 48 && M <= MR_ROWS && K % (32 * MR_G) == 0 && !getenv("KF_GEMM_NO_MR")) {
+            // 49..64 rows in one weight pass where it measured faster than four 16-row blocks (MI355X, Llama-3-8B
+            // shapes at 64 rows: O 18.4 against 21.6 us, down 48.3 against 57.0, gate 49.8 against 55.2; QKV and
+            // 17..48 rows: no gain). One 16-row weight tile a block, 4 waves splitting K for N <= 4096 (too few tiles
+            // otherwise), one wave for wide outputs. KF_GEMM_MR=11 / 14 forces a variant (a comparison knob)
+            const char* fe = getenv("KF_GEMM_MR");
+            const int v = fe ? atoi(fe) : N >= 8192 ? 11 : N <= 4096 ? 14 : 0;
+            if (v == 11) return gemm_mr_launch<1, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+            if (v == 14) return gemm_mr_launch<1, 4>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+        }
         if (M <= 64) {  // M / 16 row blocks
             // one 16-column tile a wave when that still gives at most one block per CU (a block holds a CU), else two
             static const int tn = [] {  // KF_GEMM_SMALL_TN: a tuning knob

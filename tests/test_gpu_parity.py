@@ -500,3 +500,25 @@ def test_matmul_q8_0_small_batch_llama_shapes(cuda, shape, rows):
     got = y.cpu().numpy()
     assert np.isfinite(got).all()
     _close(got[:, cols], want)
+
+
+@pytest.mark.parametrize("variant", ["11", "14"])
+@pytest.mark.parametrize("rows,n,n_out", [(49, 256, 40), (53, 4096, 300), (64, 1280, 520), (57, 14336, 96), (64, 768, 4100)])
+def test_gemm_q8_0_all_rows_one_pass_variants(cuda, monkeypatch, variant, rows, n, n_out):
+    """49..64 Q8_0 rows in one weight pass (activation rows staged in LDS per K chunk), both (waves) variants: ragged
+    row counts, a single chunk, K split over waves with a chunk count that is not a multiple of the waves, a last
+    weight tile past n_out, against the CPU backend."""
+    import torch
+
+    monkeypatch.setenv("KF_GEMM_MR", variant)
+    rng = np.random.default_rng(rows * 7 + n_out)
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n)
+    x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
+    bias = kf.synth_normal(5, 1.0, n_out)
+    res = kf.synth_normal(6, 1.0, rows * n_out).reshape(rows, n_out)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8_0)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q8_0, _tensor(w, cuda), act, y, rows, n, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res)
