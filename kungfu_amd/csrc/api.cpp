@@ -31,6 +31,9 @@ hipError_t kf_launch_gemv1(uint32_t ty, const void* w, int64_t row_bytes, const 
                            const float* bias, const float* res, float* y, int n, int n_out, int maxit, const KfSegs* segs, hipStream_t s);
 hipError_t kf_launch_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out,
                                 int32_t* out, hipStream_t s);
+bool kf_rows_mma_1_ok(uint32_t ty, const void* w, int64_t row_bytes, int n, int n_out, int rows);
+hipError_t kf_launch_rows_mma_1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n,
+                                int n_out, int rows, const float* bias, const float* res, float* y, hipStream_t s);
 hipError_t kf_launch_gemv1_fused(uint32_t ty, const void* w, int64_t row_bytes, const float* x, const float* bias, const float* res, float* y,
                                  int n, int n_out, const KfSegs* segs, hipStream_t s);
 int kf_gemv_max_n();
@@ -204,7 +207,15 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
     const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
     if (rc != KF_OK) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    // q5_K / q6_K: their own product, all rows (eight activation rows a weight pass)
+    // q5_K / q6_K: several rows on the matrix cores (16 activation rows a weight pass), one row (or a layout the
+    // matrix-core form does not take: q6_K rows with an odd number of super-blocks) on their own per-lane product
+    if ((ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) && rows > 1 && !getenv("KF_ROWS_VALU") && kf_rows_mma_1_ok(ty, w, row_bytes, n, n_out, rows)) {
+        const kf_act_offsets o = kf_act_layout((size_t)rows, (size_t)n);
+        const char* base = static_cast<const char*>(act);
+        const hipError_t e = kf_launch_rows_mma_1(ty, w, row_bytes, reinterpret_cast<const int8_t*>(base + o.q), reinterpret_cast<const int32_t*>(base + o.s32),
+                                                  reinterpret_cast<const float*>(base + o.d32), n, n_out, rows, bias, res, y, s);
+        return e == hipSuccess ? KF_OK : hip_fail(e, "q5_K/q6_K multi-row product launch");
+    }
     if (ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) {
         const hipError_t e = kf_launch_gemv_k(ty, w, row_bytes, act, bias, res, y, rows, n, n_out, s);
         return e == hipSuccess ? KF_OK : hip_fail(e, "q5_K/q6_K product launch");

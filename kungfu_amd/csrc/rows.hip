@@ -26,7 +26,8 @@ hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_byte
                               const float* xd32, int n, int n_out, const int32_t* order, const int32_t* offsets, int n_slots, int pairs, int n_used,
                               int per_slot, int avg_rows, const float* bias, const float* res, float* y, hipStream_t s);
 bool kf_rows_mma_ok(int n, int n_out, int slots, bool glu, int avg_rows);
-hipError_t kf_launch_rows_mma_1(const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n, int n_out,
+bool kf_rows_mma_1_ok(uint32_t ty, const void* w, int64_t row_bytes, int n, int n_out, int rows);
+hipError_t kf_launch_rows_mma_1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n, int n_out,
                                 int rows, const float* bias, const float* res, float* y, hipStream_t s);
 
 namespace {
@@ -455,8 +456,8 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
     const int avg_rows = offsets ? (per_slot ? act_rows : act_rows * n_used) / std::max(1, slots) : pairs;
     // one matrix (no slots, no fused up): K split over the waves of a block (rows_mma_1_kernel)
     if (ty == KF_TYPE_Q4_K && !valu && !offsets && !order && !w2 && per_slot == 1 && n_used == 1 &&
-        (int64_t)n_out * row_bytes < (1ll << 31) && (int64_t)act_rows * n < (1ll << 31))
-        return kf_launch_rows_mma_1(wb, row_bytes, xq, xs, xd, n, n_out, act_rows, bias, res, y, s);
+        kf_rows_mma_1_ok(ty, w, row_bytes, n, n_out, act_rows))
+        return kf_launch_rows_mma_1(KF_TYPE_Q4_K, wb, row_bytes, xq, xs, xd, n, n_out, act_rows, bias, res, y, s);
     if (ty == KF_TYPE_Q4_K && !valu && kf_rows_mma_ok(n, n_out, slots, w2 != nullptr, avg_rows))
         return kf_launch_rows_mma(wb, ub, expert_bytes, row_bytes, xq, xs, xd, n, n_out, order, offsets, n_slots, pairs, n_used, per_slot, avg_rows, bias,
                                   res, y, s);

@@ -62,16 +62,19 @@ __host__ __device__ inline RmLds rm_lds(int n, int rt) {
 
 constexpr int RM_TILE_BYTES = 16 * KF_Q4_K_BYTES;  // one super-block of a wave's 16 weight rows
 
-// One super-block of one weight operand row set: the lane's header and its four 8-byte nibble pieces
+// One super-block of one weight operand row set: the lane's header and its four 8-byte nibble pieces (q5_K: and the
+// high bits of its eight columns, qh bytes 8 q..)
 struct RmW {
     rm_v4u hd;
     rm_v2u q[4];
+    rm_v2u qh;
 };
 
 // S and mins of one super-block for the lane's weight row against the staged rows; a_at / x_at: the lane's A operand
 // and split-sum addresses of this super-block (group 0)
+template <bool Q5 = false>
 __device__ __forceinline__ void rm_block(const RmW& v, const uint8_t* a_at, int a_gstride, rm_v4h xo, int q, rm_v4i& S, rm_v4f& mins) {
-    const uint32_t m4 = 0x0f0f0f0fu;
+    const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
     S = rm_v4i{0, 0, 0, 0};
     uint32_t mq = 0;
 #pragma unroll
@@ -79,8 +82,15 @@ __device__ __forceinline__ void rm_block(const RmW& v, const uint8_t* a_at, int 
         uint32_t sc2, m2;
         kf_q4k_scales(v.hd.y, v.hd.z, v.hd.w, p, sc2, m2);
         if (p == q) mq = m2;
-        const long blo = (long)(v.q[p].x & m4) | ((long)(v.q[p].y & m4) << 32);
-        const long bhi = (long)((v.q[p].x >> 4) & m4) | ((long)((v.q[p].y >> 4) & m4) << 32);
+        uint32_t l0 = v.q[p].x & m4, l1 = v.q[p].y & m4, h0 = (v.q[p].x >> 4) & m4, h1 = (v.q[p].y >> 4) & m4;
+        if constexpr (Q5) {  // the fifth bit of group g is bit g of the column's qh byte (q5_k.rs:7-60)
+            l0 |= ((v.qh.x >> (2 * p)) & m1) << 4;
+            l1 |= ((v.qh.y >> (2 * p)) & m1) << 4;
+            h0 |= ((v.qh.x >> (2 * p + 1)) & m1) << 4;
+            h1 |= ((v.qh.y >> (2 * p + 1)) & m1) << 4;
+        }
+        const long blo = (long)l0 | ((long)l1 << 32);
+        const long bhi = (long)h0 | ((long)h1 << 32);
         const long a0 = *reinterpret_cast<const long*>(a_at + (2 * p) * a_gstride);
         const long a1 = *reinterpret_cast<const long*>(a_at + (2 * p + 1) * a_gstride);
         const rm_v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, blo, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
@@ -364,20 +374,38 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
 // activation rows per block would cost as much as the block's weights. Here a block's eight waves split K over
 // TILES tiles (KP = 8 / TILES waves a tile, each taking super-blocks kpart, kpart + KP, ...), and each wave fetches,
 // per super-block, its tile's weights and exactly the activation data it multiplies them with (16 rows x 256 int8
-// columns in MFMA order, their 32-column sums and scales) by DMA into one of its two LDS buffers: nine DMA
-// instructions a super-block for every wave. (Operand loads into registers instead made the compiler copy the loaded
-// registers at every loop pass, waiting for all loads in flight.) The KP partials of a tile are summed in LDS in
-// kpart order (deterministic). Rows run in chunks of 16.
-constexpr int RD_A = RM_TILE_BYTES, RD_S = RD_A + 8 * 16 * 32, RD_D = RD_S + 16 * 8 * 4, RD_BUF = RD_D + 16 * 4 + 64;  // 7104 bytes
+// columns in MFMA order, their 32-column sums and scales) by DMA into one of its two LDS buffers. (Operand loads into
+// registers instead made the compiler copy the loaded registers at every loop pass, waiting for all loads in flight.)
+// The KP partials of a tile are summed in LDS in kpart order (deterministic). Rows run in chunks of 16.
+// The same kernel runs q5_K and q6_K (replacing the per-lane dot form of gemv_k.hip for several rows):
+//   * q5_K: q4_K's arithmetic with 5-bit operands (the fifth bit from qh, q5_k.rs:7-60); 176-byte rows;
+//   * q6_K: the operand is q - 32 (in [-32, 31], an int8), so the super-block integer sum_s sc_s (dot_s - 32 bsum_s)
+//     of the reference (q6_k.rs) is sum_s sc_s dot'_s with no sums term; the int8 scales cover 16 columns, so each
+//     32-column group takes two MFMAs with the other 16 columns' operand bytes zeroed (lane quarters 0-1 hold columns
+//     0-15, quarters 2-3 columns 16-31). Its 210-byte blocks are 2-byte aligned: each row's super-block comes as the
+//     212-byte dword window [start & ~3, +212) (rows are 4-byte aligned when the row has an even number of
+//     super-blocks, which the launcher requires), read back at the window's 0- or 2-byte shift.
+template <uint32_t TY>
+struct RdGeo {
+    static constexpr int WROW = TY == KF_TYPE_Q4_K ? KF_Q4_K_BYTES : TY == KF_TYPE_Q5_K ? KF_Q5_K_BYTES : 212;  // LDS row
+    static constexpr int WB = (16 * WROW + 15) / 16 * 16;  // the tile's weights
+    static constexpr int A = WB, S = A + 8 * 16 * 32, D = S + 16 * 8 * 4, BUF = D + 16 * 4 + 64;
+    static constexpr bool DW = TY == KF_TYPE_Q6_K;         // dword DMA (2-byte aligned blocks) instead of 16-byte
+    static constexpr int UNITS = DW ? 16 * WROW / 4 : 16 * WROW / 16;  // DMA units of the tile's weights
+    static constexpr int WI = (UNITS + 63) / 64;           // weight DMA instructions a super-block
+    static constexpr int NI = WI + 4 + (TY == KF_TYPE_Q6_K ? 0 : 1) + 1;  // all DMA instructions a super-block
+};
 
-template <int TILES>
+template <uint32_t TY, int TILES>
 __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                 const int32_t* __restrict__ xs32, const float* __restrict__ xd32, int n, int n_out,
                                                                 int rows, const float* __restrict__ bias, const float* __restrict__ res,
                                                                 float* __restrict__ y) {
+    using G = RdGeo<TY>;
     constexpr int KP = RM_WAVES / TILES;
-    __shared__ __align__(16) uint8_t pk0[RM_WAVES * RD_BUF];
-    __shared__ __align__(16) uint8_t pk1[RM_WAVES * RD_BUF];
+    constexpr int SBB = TY == KF_TYPE_Q4_K ? KF_Q4_K_BYTES : TY == KF_TYPE_Q5_K ? KF_Q5_K_BYTES : KF_Q6_K_BYTES;
+    __shared__ __align__(16) uint8_t pk0[RM_WAVES * G::BUF];
+    __shared__ __align__(16) uint8_t pk1[RM_WAVES * G::BUF];
     __shared__ __align__(16) rm_v4f part[RM_WAVES * 64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -391,11 +419,13 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
     // last row: the hardware range check on the per-lane offset returns zeros for rows past n_out
     const int trow = min(orow, (n_out - 1) & ~15);
     const auto rw = kf_rsrc(w + (int64_t)trow * row_bytes, (uint64_t)(n_out - trow) * row_bytes);
-    int vpk[3];
+    // weight DMA unit u = 64 i + lane: row u / per, unit u % per of the row's super-block (clamped duplicates)
+    int vpk[G::WI];
 #pragma unroll
-    for (int i = 0; i < 3; i++) {
-        const int s2 = min(64 * i + lane, 143);
-        vpk[i] = (s2 / 9) * (int)row_bytes + 16 * (s2 % 9);
+    for (int i = 0; i < G::WI; i++) {
+        constexpr int per = G::DW ? G::WROW / 4 : G::WROW / 16;
+        const int u = min(64 * i + lane, G::UNITS - 1);
+        vpk[i] = (u / per) * (int)row_bytes + (G::DW ? 4 : 16) * (u % per);
     }
 
     for (int c0 = 0; c0 < rows; c0 += 16) {
@@ -413,43 +443,96 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
         const int vd = min(lane & 15, R - 1) * nsum * 4;
         auto park = [&](int j, uint8_t* buf) {
             const int sb = kpart + KP * j;
-            const int so = sb * KF_Q4_K_BYTES;
-            uint8_t* b = buf + wave * RD_BUF;
-            kf_bdma16(rw, vpk[0], so, b);
-            kf_bdma16(rw, vpk[1], so, b + 1024);
-            if (lane < 16) kf_bdma16(rw, vpk[2], so, b + 2048);
+            uint8_t* b = buf + wave * G::BUF;
+            if constexpr (G::DW) {
+                const int so = (sb * SBB) & ~3;  // the window's start (rows 4-byte aligned)
 #pragma unroll
-            for (int i = 0; i < 4; i++) kf_bdma16(rx, va[i], sb * KF_Q4_K_BLOCK, b + RD_A + 1024 * i);
-            if (lane < 32) kf_bdma16(rs, vs, sb * 32, b + RD_S);
-            if (lane < 16) kf_bdma4(rd, vd, sb * 32, b + RD_D);
+                for (int i = 0; i < G::WI; i++)
+                    if (G::UNITS % 64 == 0 || i + 1 < G::WI || lane < G::UNITS % 64) kf_bdma4(rw, vpk[i], so, b + 256 * i);
+            } else {
+                const int so = sb * SBB;
+#pragma unroll
+                for (int i = 0; i < G::WI; i++)
+                    if (G::UNITS % 64 == 0 || i + 1 < G::WI || lane < G::UNITS % 64) kf_bdma16(rw, vpk[i], so, b + 1024 * i);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; i++) kf_bdma16(rx, va[i], sb * KF_Q4_K_BLOCK, b + G::A + 1024 * i);
+            if constexpr (TY != KF_TYPE_Q6_K)
+                if (lane < 32) kf_bdma16(rs, vs, sb * 32, b + G::S);
+            if (lane < 16) kf_bdma4(rd, vd, sb * 32, b + G::D);
         };
-        constexpr int NI = 9;  // DMA instructions a super-block, every wave
         rm_v4f acc = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
         if (items > 0) park(0, pk0);
         if (items > 1) park(1, pk1);
         auto step = [&](uint8_t* buf, int j) {
             if (j + 1 < items)
-                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
+                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(G::NI));
             else
                 __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-            const uint8_t* b = buf + wave * RD_BUF;
-            RmW v;
-            v.hd = *reinterpret_cast<const rm_v4u*>(b + c * KF_Q4_K_BYTES);
+            const uint8_t* b = buf + wave * G::BUF;
+            const rm_v4f dx = *reinterpret_cast<const rm_v4f*>(b + G::D + 16 * q);
+            const uint8_t* a_at = b + G::A + c * 32 + 8 * q;
+            if constexpr (TY == KF_TYPE_Q6_K) {
+                const int sb = kpart + KP * j;
+                const uint8_t* wr = b + c * G::WROW + ((sb * SBB) & 3);  // the lane's row of the super-block
+                typedef uint32_t v2a2 __attribute__((ext_vector_type(2), aligned(2)));
+                typedef uint32_t v4a2 __attribute__((ext_vector_type(4), aligned(2)));
+                const v4a2 scv = *reinterpret_cast<const v4a2*>(wr + 192);  // the row's sixteen int8 scales
+                const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+                rm_v4i S = rm_v4i{0, 0, 0, 0};
+                const uint32_t m4 = 0x0f0f0f0fu, m3 = 0x03030303u, hb = 0x80808080u, k32 = 0x20202020u;
 #pragma unroll
-            for (int p = 0; p < 4; p++) v.q[p] = *reinterpret_cast<const rm_v2u*>(b + c * KF_Q4_K_BYTES + 16 + 32 * p + 8 * q);
-            const int2 bs = *reinterpret_cast<const int2*>(b + RD_S + (c * 8 + 2 * q) * 4);
-            const rm_v4f dx = *reinterpret_cast<const rm_v4f*>(b + RD_D + 16 * q);
-            rm_v4h xo;
-            xo[0] = (_Float16)(float)(bs.x >> 6);
-            xo[1] = (_Float16)(float)(bs.x & 63);
-            xo[2] = (_Float16)(float)(bs.y >> 6);
-            xo[3] = (_Float16)(float)(bs.y & 63);
-            rm_v4i S;
-            rm_v4f mins;
-            rm_block(v, b + RD_A + c * 32 + 8 * q, 16 * 32, xo, q, S, mins);
-            const float d = kf_h2f(v.hd.x & 0xffffu), dm = kf_h2f(v.hd.x >> 16);
+                for (int h = 0; h < 2; h++) {
+                    const v2a2 la = *reinterpret_cast<const v2a2*>(wr + 64 * h + 8 * q);
+                    const v2a2 lb = *reinterpret_cast<const v2a2*>(wr + 64 * h + 32 + 8 * q);
+                    const v2a2 qh = *reinterpret_cast<const v2a2*>(wr + 128 + 32 * h + 8 * q);
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], fmaf(-dm, mins[e], d * (float)S[e]), acc[e]);
+                    for (int gg = 0; gg < 4; gg++) {
+                        const v2a2 src = (gg & 1) ? lb : la;
+                        uint32_t wv[2];
+#pragma unroll
+                        for (int e = 0; e < 2; e++) {
+                            const uint32_t lo = (gg >> 1) ? (src[e] >> 4) & m4 : src[e] & m4;
+                            const uint32_t v = lo | (((qh[e] >> (2 * gg)) & m3) << 4);  // q in [0, 63] per byte
+                            wv[e] = ((v | hb) - k32) ^ hb;                            // q - 32 per byte, no borrows
+                        }
+                        const long bw = (long)wv[0] | ((long)wv[1] << 32);
+                        const long b0 = q < 2 ? bw : 0, b1 = q < 2 ? 0 : bw;  // columns 0-15, then 16-31
+                        const long a = *reinterpret_cast<const long*>(a_at + (4 * h + gg) * (16 * 32));
+                        const rm_v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
+                        const rm_v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
+                        // scales 8 h + 2 gg and 8 h + 2 gg + 1 (ggml's q6_K order: 16 columns a scale)
+                        const int si = 8 * h + 2 * gg;
+                        const int s0 = (int)(int8_t)(uint8_t)(scw[si >> 2] >> (8 * (si & 3)));
+                        const int s1 = (int)(int8_t)(uint8_t)(scw[(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
+                        // |dot| <= 32 * 128 * 16 and |sc| <= 128: 24-bit multiplies are exact
+#pragma unroll
+                        for (int e = 0; e < 4; e++) S[e] += __mul24(s0, i0[e]) + __mul24(s1, i1[e]);
+                    }
+                }
+                const float d = kf_h2f(*reinterpret_cast<const uint16_t*>(wr + 208));
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], d * (float)S[e], acc[e]);
+            } else {
+                constexpr int QS = TY == KF_TYPE_Q5_K ? 48 : 16;  // the nibbles' offset in the block
+                RmW v;
+                v.hd = *reinterpret_cast<const rm_v4u*>(b + c * G::WROW);
+#pragma unroll
+                for (int p = 0; p < 4; p++) v.q[p] = *reinterpret_cast<const rm_v2u*>(b + c * G::WROW + QS + 32 * p + 8 * q);
+                if constexpr (TY == KF_TYPE_Q5_K) v.qh = *reinterpret_cast<const rm_v2u*>(b + c * G::WROW + 16 + 8 * q);
+                const int2 bs = *reinterpret_cast<const int2*>(b + G::S + (c * 8 + 2 * q) * 4);
+                rm_v4h xo;
+                xo[0] = (_Float16)(float)(bs.x >> 6);
+                xo[1] = (_Float16)(float)(bs.x & 63);
+                xo[2] = (_Float16)(float)(bs.y >> 6);
+                xo[3] = (_Float16)(float)(bs.y & 63);
+                rm_v4i S;
+                rm_v4f mins;
+                rm_block<TY == KF_TYPE_Q5_K>(v, a_at, 16 * 32, xo, q, S, mins);
+                const float d = kf_h2f(v.hd.x & 0xffffu), dm = kf_h2f(v.hd.x >> 16);
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], fmaf(-dm, mins[e], d * (float)S[e]), acc[e]);
+            }
             if (j + 2 < items) {
                 __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));  // this buffer's reads are done
                 park(j + 2, buf);
@@ -515,11 +598,21 @@ hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_byte
 #undef KF_RM
 }
 
-// Host launcher of the one-slot q4_K few-row product (rows_mma_1_kernel), validated by the caller: n a multiple of
-// 256, the matrix below 2 GB. Tiles per block chosen so the grid has about one block per CU or more.
-hipError_t kf_launch_rows_mma_1(const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n, int n_out,
-                                int rows, const float* bias, const float* res, float* y, hipStream_t s) {
-    if ((int64_t)n_out * row_bytes >= (1ll << 31) || (int64_t)rows * n >= (1ll << 31)) return hipErrorInvalidValue;
+// Whether the one-slot matrix-core product takes a q4_K / q5_K / q6_K weight: row offsets travel as 32-bit values (the
+// matrix and the activation rows below 2 GB), 16-byte aligned weights, and for q6_K 4-byte aligned rows (an even
+// number of super-blocks a row)
+bool kf_rows_mma_1_ok(uint32_t ty, const void* w, int64_t row_bytes, int n, int n_out, int rows) {
+    if (n % KF_Q4_K_BLOCK != 0 || (int64_t)n_out * row_bytes >= (1ll << 31) || (int64_t)rows * n >= (1ll << 31)) return false;
+    if ((reinterpret_cast<uintptr_t>(w) & 15) != 0) return false;
+    if (ty == KF_TYPE_Q6_K) return row_bytes % 4 == 0;
+    return (ty == KF_TYPE_Q4_K || ty == KF_TYPE_Q5_K) && row_bytes % 16 == 0;
+}
+
+// Host launcher of the one-slot few-row product (rows_mma_1_kernel) for q4_K, q5_K and q6_K weights, validated by the
+// caller (kf_rows_mma_1_ok). Tiles per block chosen so the grid has about one block per CU or more.
+hipError_t kf_launch_rows_mma_1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n,
+                                int n_out, int rows, const float* bias, const float* res, float* y, hipStream_t s) {
+    if (!kf_rows_mma_1_ok(ty, w, row_bytes, n, n_out, rows)) return hipErrorInvalidValue;
     const int tiles = (n_out + 15) / 16;
     static const int forced = [] {  // KF_RM1_TILES: a tuning knob (1, 2, 4 or 8 tiles a block)
         const char* e = getenv("KF_RM1_TILES");
@@ -539,15 +632,20 @@ hipError_t kf_launch_rows_mma_1(const void* w, int64_t row_bytes, const int8_t* 
             }
     }
     const auto* wb = static_cast<const uint8_t*>(w);
-#define KF_R1(T)                                                                                                   \
+#define KF_R1(TY, T)                                                                                               \
     {                                                                                                              \
-        rows_mma_1_kernel<T><<<(tiles + T - 1) / T, RM_THREADS, 0, s>>>(wb, row_bytes, xq, xs32, xd32, n, n_out, rows, bias, res, y); \
+        rows_mma_1_kernel<TY, T><<<(tiles + T - 1) / T, RM_THREADS, 0, s>>>(wb, row_bytes, xq, xs32, xd32, n, n_out, rows, bias, res, y); \
         return hipGetLastError();                                                                                  \
     }
-    if (tpb == 8) KF_R1(8)
-    if (tpb == 4) KF_R1(4)
-    if (tpb == 2) KF_R1(2)
-    KF_R1(1)
+#define KF_R1_T(TY)          \
+    if (tpb == 8) KF_R1(TY, 8) \
+    if (tpb == 4) KF_R1(TY, 4) \
+    if (tpb == 2) KF_R1(TY, 2) \
+    KF_R1(TY, 1)
+    if (ty == KF_TYPE_Q6_K) { KF_R1_T(KF_TYPE_Q6_K) }
+    if (ty == KF_TYPE_Q5_K) { KF_R1_T(KF_TYPE_Q5_K) }
+    KF_R1_T(KF_TYPE_Q4_K)
+#undef KF_R1_T
 #undef KF_R1
 }
 

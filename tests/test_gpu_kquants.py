@@ -91,3 +91,35 @@ def test_product_on_random_blocks(cuda):
             kf.gemv(ty, _tensor(w, cuda), act, y, rows, n, n_out)
             torch.cuda.synchronize()
             _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("rows,n,n_out", [(2, 512, 16), (20, 4096, 1000), (17, 2304, 45), (16, 14336, 200), (33, 1024, 130)])
+def test_multi_row_matrix_cores(cuda, ty, rows, n, n_out):
+    """Several rows of q5_K / q6_K on the matrix cores (16 activation rows a weight pass, K split over a block's
+    waves): chunks of 16 rows past the first, ragged last tiles, 14336 columns; 2304 columns (nine super-blocks a row)
+    leave q6_K rows 2-byte aligned, which the per-lane product takes instead. Random block bytes (every scale and
+    bit pattern), with bias and residual, against the CPU backend's int8 path (ops::matmul_i8: the same quantized
+    activations and dot_i8 integers; the float path differs from it by the activation rounding, which on these
+    outputs of mean magnitude 150-600 exceeds the relative bar near zero for the per-lane product too)."""
+    import torch
+
+    rng = np.random.default_rng(rows * 31 + n + n_out + ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    # unit-scale rows as in test_product_on_random_blocks: with random 6-bit scales and mins the super-block terms
+    # already reach thousands, and outputs that cancel to near zero are then bounded by f32 rounding, not the kernel
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    bias = rng.standard_normal(n_out).astype(np.float32)
+    res = rng.standard_normal((rows, n_out)).astype(np.float32)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemv(ty, _tensor(w, cuda), act, y, rows, n, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    got, want = y.cpu().numpy().astype(np.float64), (oracle.matmul_i8(ty, w, n, n_out, x, bias) + res).astype(np.float64)
+    # the GPU adds the n / 256 super-block terms of an output in another order than the CPU: each sum carries an f32
+    # rounding of its largest terms, which on these blocks are as large as the largest outputs, so the bar adds
+    # 2e-6 of the largest |output| (a few of its ulps) to the north-star bound
+    bound = 1e-4 + 1e-3 * np.abs(want) + 2e-6 * np.abs(want).max()
+    err = np.abs(got - want)
+    assert (err <= bound).all(), f"max err {err.max():.3e} at {np.unravel_index(np.argmax(err - bound), err.shape)}"
