@@ -643,35 +643,9 @@ constexpr int MR_ABUF = MR_ACT + MR_ROWS * MR_G * 4;      // + the scales: 9216
 constexpr int MR_WCH = MR_G * KF_Q8_0_BYTES;              // 136 weight bytes a row and chunk
 
 
-// The kernel below issues its LDS DMA through inline assembly. The compiler's own waits for DMA written LDS are
-// conservative (a read of one buffer waited for the DMA into another, serializing the chunks); here every wait is
-// explicit: loads complete in issue order and the loop waits for exact vmcnt counts. The descriptor is the raw buffer
-// kf_rsrc builds: base, stride 0, num_records bytes (reads past it return zeros), word 3 0x00020000.
-typedef int mr_v4i __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ mr_v4i mr_rsrc(const void* base, uint64_t bytes) {
-    const uint64_t a = reinterpret_cast<uint64_t>(base);
-    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
-    return mr_v4i{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)n, 0x00020000};
-}
-
-__device__ __forceinline__ uint32_t mr_lds_addr(const void* p) {
-    return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)p;
-}
-
-// buffer_load_dwordx4 / _dword ... lds: lane l writes the 16 (4) bytes at voff + soff of the buffer to lds + 16 l (4 l)
-__device__ __forceinline__ void mr_dma16(mr_v4i r, int voff, int soff, const void* lds) {
-    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
-                 "s"(mr_lds_addr(lds))
-                 : "memory", "m0");
-}
-
-__device__ __forceinline__ void mr_dma4(mr_v4i r, int voff, int soff, const void* lds) {
-    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff),
-                 "s"(mr_lds_addr(lds))
-                 : "memory", "m0");
-}
-
+// The kernel below issues its LDS DMA through inline assembly (kf_adma16 / kf_adma4): the compiler's own waits for
+// DMA-written LDS were conservative here (a read of one buffer waited for the DMA into another, serializing the
+// chunks); every wait is explicit instead.
 template <int TN, int W>
 __global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                               const float* __restrict__ xd32, const float* __restrict__ bias,
@@ -696,14 +670,14 @@ __global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __r
 
     // activation DMA sources: instruction i (rows 8 i..) lane l: row 8 i + l / 8, piece (l % 8) ^ (row % 8); scales:
     // lane l row l, 16 bytes
-    const mr_v4i rx = mr_rsrc(xq, (uint64_t)M * K);
-    const mr_v4i rd = mr_rsrc(xd32, (uint64_t)M * kg * 4);
+    const kf_arsrc_t rx = kf_arsrc(xq, (uint64_t)M * K);
+    const kf_arsrc_t rd = kf_arsrc(xd32, (uint64_t)M * kg * 4);
     const int xr = lane >> 3, xs = lane & 7;
     const int va = xr * K + 16 * (xs ^ (xr & 7));  // + 8 i K for instruction i (row 8 i + xr: same row % 8)
     const int vd = lane * kg * 4;  // scales: instruction g moves group g of the 64 rows (lane l: row l), [group][row]
     // weight DMA: instruction i lane l moves the dword at byte e = 256 i + 4 l of the chunk's [ROWS][136] block: row
     // e / 136, offset e % 136 (rows past N read as zeros: the resource ends at the matrix's last row)
-    const mr_v4i rw = mr_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)max(N - n0, 0) * row_bytes);
+    const kf_arsrc_t rw = kf_arsrc(w + (int64_t)n0 * row_bytes, (uint64_t)max(N - n0, 0) * row_bytes);
     int vw[WI];
 #pragma unroll
     for (int i = 0; i < WI; i++) {
@@ -719,11 +693,11 @@ __global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __r
         constexpr int B = decltype(kb)::value;
         const int cc = min(ch, last);
 #pragma unroll
-        for (int i = 0; i < MR_ROWS / 8; i++) mr_dma16(rx, va + 8 * i * K, cc * (32 * MR_G), ab[B] + 1024 * i);
+        for (int i = 0; i < MR_ROWS / 8; i++) kf_adma16(rx, va + 8 * i * K, cc * (32 * MR_G), ab[B] + 1024 * i);
 #pragma unroll
-        for (int g = 0; g < MR_G; g++) mr_dma4(rd, vd, (cc * MR_G + g) * 4, ab[B] + MR_ACT + 256 * g);
+        for (int g = 0; g < MR_G; g++) kf_adma4(rd, vd, (cc * MR_G + g) * 4, ab[B] + MR_ACT + 256 * g);
 #pragma unroll
-        for (int i = 0; i < WI; i++) mr_dma4(rw, vw[i], cc * MR_WCH, ab[B] + MR_ABUF + 256 * i);
+        for (int i = 0; i < WI; i++) kf_adma4(rw, vw[i], cc * MR_WCH, ab[B] + MR_ABUF + 256 * i);
     };
 
     v4f acc[MR_TM][TN];

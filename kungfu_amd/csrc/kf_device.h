@@ -154,6 +154,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t kf_rsrc(const void* base, uint
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 
+// The same DMA issued through inline assembly, for kernels whose every wait on it is explicit. The compiler's own
+// waits for DMA-written LDS are conservative where it cannot tell the buffers apart (a read of one buffer waits for
+// the DMA into another, which serializes a prefetch ring); assembly it does not see gets none, so such a kernel waits
+// with exact vmcnt counts (loads complete in issue order) before it reads a buffer. The descriptor is the raw buffer
+// kf_rsrc builds: base, stride 0, num_records bytes (reads past it return zeros), word 3 0x00020000.
+typedef int kf_arsrc_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ kf_arsrc_t kf_arsrc(const void* base, uint64_t bytes) {
+    const uint64_t a = reinterpret_cast<uint64_t>(base);
+    const uint32_t n = bytes > 0xffffffffull ? 0xffffffffu : (uint32_t)bytes;
+    return kf_arsrc_t{(int)(uint32_t)a, (int)((uint32_t)(a >> 32) & 0xffffu), (int)n, 0x00020000};
+}
+
+__device__ __forceinline__ uint32_t kf_lds_addr(const void* p) {
+    return (uint32_t)(size_t)(const __attribute__((address_space(3))) uint8_t*)p;
+}
+
+// lane l writes the 16 (4) bytes at voff + soff of the buffer to lds + 16 l (4 l)
+__device__ __forceinline__ void kf_adma16(kf_arsrc_t r, int voff, int soff, const void* lds) {
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "s"(kf_lds_addr(lds))
+                 : "memory", "m0");
+}
+
+__device__ __forceinline__ void kf_adma4(kf_arsrc_t r, int voff, int soff, const void* lds) {
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dword %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "s"(kf_lds_addr(lds))
+                 : "memory", "m0");
+}
+
 // buffer_load_dwordx4 / _dword ... lds: lane l writes its 16 (4) bytes read at voff + soff to lds_base + 16 l (4 l).
 __device__ __forceinline__ void kf_bdma16(__amdgpu_buffer_rsrc_t r, int voff, int soff, void* lds_base) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (kf_lds_void*)lds_base, 16, voff, soff, 0, 0);

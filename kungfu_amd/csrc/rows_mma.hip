@@ -376,7 +376,8 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
 // per super-block, its tile's weights and exactly the activation data it multiplies them with (16 rows x 256 int8
 // columns in MFMA order, their 32-column sums and scales) by DMA into one of its two LDS buffers. (Operand loads into
 // registers instead made the compiler copy the loaded registers at every loop pass, waiting for all loads in flight.)
-// The KP partials of a tile are summed in LDS in kpart order (deterministic). Rows run in chunks of 16.
+// The KP partials of a tile are summed in LDS in kpart order (deterministic). Rows run in chunks of 16, up to four
+// chunks (64 rows) per pass over the weights: a super-block's weights stay while its chunks of staged rows pass.
 // The same kernel runs q5_K and q6_K (replacing the per-lane dot form of gemv_k.hip for several rows):
 //   * q5_K: q4_K's arithmetic with 5-bit operands (the fifth bit from qh, q5_k.rs:7-60); 176-byte rows;
 //   * q6_K: the operand is q - 32 (in [-32, 31], an int8), so the super-block integer sum_s sc_s (dot_s - 32 bsum_s)
@@ -388,15 +389,16 @@ hipError_t rows_mma_launch(const uint8_t* w, const uint8_t* w2, int64_t expert_b
 template <uint32_t TY>
 struct RdGeo {
     static constexpr int WROW = TY == KF_TYPE_Q4_K ? KF_Q4_K_BYTES : TY == KF_TYPE_Q5_K ? KF_Q5_K_BYTES : 212;  // LDS row
-    static constexpr int WB = (16 * WROW + 15) / 16 * 16;  // the tile's weights
-    static constexpr int A = WB, S = A + 8 * 16 * 32, D = S + 16 * 8 * 4, BUF = D + 16 * 4 + 64;
+    static constexpr int WB = (16 * WROW + 15) / 16 * 16;  // one weight buffer: the tile's super-block
+    static constexpr int A = 0, S = A + 8 * 16 * 32, D = S + 16 * 8 * 4, AB = D + 16 * 4 + 64;  // one activation buffer
     static constexpr bool DW = TY == KF_TYPE_Q6_K;         // dword DMA (2-byte aligned blocks) instead of 16-byte
     static constexpr int UNITS = DW ? 16 * WROW / 4 : 16 * WROW / 16;  // DMA units of the tile's weights
     static constexpr int WI = (UNITS + 63) / 64;           // weight DMA instructions a super-block
-    static constexpr int NI = WI + 4 + (TY == KF_TYPE_Q6_K ? 0 : 1) + 1;  // all DMA instructions a super-block
+    static constexpr int NA = 4 + (TY == KF_TYPE_Q6_K ? 0 : 1) + 1;  // activation DMA instructions a chunk
 };
 
-template <uint32_t TY, int TILES>
+// CM: row chunks of 16 a block carries through one pass over its weights (1 up to 16 rows; 4 above: 64 rows a pass)
+template <uint32_t TY, int TILES, int CM>
 __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                 const int32_t* __restrict__ xs32, const float* __restrict__ xd32, int n, int n_out,
                                                                 int rows, const float* __restrict__ bias, const float* __restrict__ res,
@@ -404,8 +406,11 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
     using G = RdGeo<TY>;
     constexpr int KP = RM_WAVES / TILES;
     constexpr int SBB = TY == KF_TYPE_Q4_K ? KF_Q4_K_BYTES : TY == KF_TYPE_Q5_K ? KF_Q5_K_BYTES : KF_Q6_K_BYTES;
-    __shared__ __align__(16) uint8_t pk0[RM_WAVES * G::BUF];
-    __shared__ __align__(16) uint8_t pk1[RM_WAVES * G::BUF];
+    // a wave's two weight buffers (super-blocks alternate) and two activation buffers (items alternate)
+    __shared__ __align__(16) uint8_t pw0[RM_WAVES * G::WB];
+    __shared__ __align__(16) uint8_t pw1[RM_WAVES * G::WB];
+    __shared__ __align__(16) uint8_t pa0[RM_WAVES * G::AB];
+    __shared__ __align__(16) uint8_t pa1[RM_WAVES * G::AB];
     __shared__ __align__(16) rm_v4f part[RM_WAVES * 64];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -413,12 +418,12 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
     const int c = lane & 15, q = lane >> 4;
     const int nsb = n / KF_Q4_K_BLOCK, nsum = n / 32;
     const int orow = (blockIdx.x * TILES + tl) * 16;  // the wave's tile
-    const int items = nsb > kpart ? (nsb - kpart + KP - 1) / KP : 0;
+    const int msb = nsb > kpart ? (nsb - kpart + KP - 1) / KP : 0;  // the wave's super-blocks
 
     // the resource starts at the wave's tile (the last tile's start for a wave past n_out) and ends at the matrix's
     // last row: the hardware range check on the per-lane offset returns zeros for rows past n_out
     const int trow = min(orow, (n_out - 1) & ~15);
-    const auto rw = kf_rsrc(w + (int64_t)trow * row_bytes, (uint64_t)(n_out - trow) * row_bytes);
+    const kf_arsrc_t rw = kf_arsrc(w + (int64_t)trow * row_bytes, (uint64_t)(n_out - trow) * row_bytes);
     // weight DMA unit u = 64 i + lane: row u / per, unit u % per of the row's super-block (clamped duplicates)
     int vpk[G::WI];
 #pragma unroll
@@ -428,138 +433,164 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_1_kernel(const uint8_t* _
         vpk[i] = (u / per) * (int)row_bytes + (G::DW ? 4 : 16) * (u % per);
     }
 
-    for (int c0 = 0; c0 < rows; c0 += 16) {
-        const int R = min(16, rows - c0);
-        // activation sources of the chunk (rows past R repeat row R - 1): A pieces (instruction i: groups 2 i, 2 i + 1;
-        // lane l: group 2 i + l / 32, row (l / 2) % 16, half l % 2), sums (lane l < 32: row l / 2, four sums from 4 (l % 2)),
-        // scales (lane l < 16: row l)
-        const auto rx = kf_rsrc(xq + (int64_t)c0 * n, (uint64_t)R * n);
-        const auto rs = kf_rsrc(xs32 + (int64_t)c0 * nsum, (uint64_t)R * nsum * 4);
-        const auto rd = kf_rsrc(xd32 + (int64_t)c0 * nsum, (uint64_t)R * nsum * 4);
-        int va[4];
+    // one super-block of the tile against one chunk of 16 staged rows: weights at wb, activations at ab
+    auto compute = [&](const uint8_t* wb, const uint8_t* ab, int sb, rm_v4f& acc) __attribute__((always_inline)) {
+        const rm_v4f dx = *reinterpret_cast<const rm_v4f*>(ab + G::D + 16 * q);
+        const uint8_t* a_at = ab + G::A + c * 32 + 8 * q;
+        if constexpr (TY == KF_TYPE_Q6_K) {
+            const uint8_t* wr = wb + c * G::WROW + ((sb * SBB) & 3);  // the lane's row of the super-block
+            typedef uint32_t v2a2 __attribute__((ext_vector_type(2), aligned(2)));
+            typedef uint32_t v4a2 __attribute__((ext_vector_type(4), aligned(2)));
+            const v4a2 scv = *reinterpret_cast<const v4a2*>(wr + 192);  // the row's sixteen int8 scales
+            const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+            rm_v4i S = rm_v4i{0, 0, 0, 0};
+            const uint32_t m4 = 0x0f0f0f0fu, m3 = 0x03030303u, hb = 0x80808080u, k32 = 0x20202020u;
 #pragma unroll
-        for (int i = 0; i < 4; i++) va[i] = min((lane >> 1) & 15, R - 1) * n + 32 * (2 * i + (lane >> 5)) + 16 * (lane & 1);
-        const int vs = min(lane >> 1 & 15, R - 1) * nsum * 4 + 16 * (lane & 1);
-        const int vd = min(lane & 15, R - 1) * nsum * 4;
-        auto park = [&](int j, uint8_t* buf) {
-            const int sb = kpart + KP * j;
-            uint8_t* b = buf + wave * G::BUF;
-            if constexpr (G::DW) {
-                const int so = (sb * SBB) & ~3;  // the window's start (rows 4-byte aligned)
+            for (int h = 0; h < 2; h++) {
+                const v2a2 la = *reinterpret_cast<const v2a2*>(wr + 64 * h + 8 * q);
+                const v2a2 lb = *reinterpret_cast<const v2a2*>(wr + 64 * h + 32 + 8 * q);
+                const v2a2 qh = *reinterpret_cast<const v2a2*>(wr + 128 + 32 * h + 8 * q);
 #pragma unroll
-                for (int i = 0; i < G::WI; i++)
-                    if (G::UNITS % 64 == 0 || i + 1 < G::WI || lane < G::UNITS % 64) kf_bdma4(rw, vpk[i], so, b + 256 * i);
-            } else {
-                const int so = sb * SBB;
+                for (int gg = 0; gg < 4; gg++) {
+                    const v2a2 src = (gg & 1) ? lb : la;
+                    uint32_t wv[2];
 #pragma unroll
-                for (int i = 0; i < G::WI; i++)
-                    if (G::UNITS % 64 == 0 || i + 1 < G::WI || lane < G::UNITS % 64) kf_bdma16(rw, vpk[i], so, b + 1024 * i);
+                    for (int e = 0; e < 2; e++) {
+                        const uint32_t lo = (gg >> 1) ? (src[e] >> 4) & m4 : src[e] & m4;
+                        const uint32_t v = lo | (((qh[e] >> (2 * gg)) & m3) << 4);  // q in [0, 63] per byte
+                        wv[e] = ((v | hb) - k32) ^ hb;                            // q - 32 per byte, no borrows
+                    }
+                    const long bw = (long)wv[0] | ((long)wv[1] << 32);
+                    const long b0 = q < 2 ? bw : 0, b1 = q < 2 ? 0 : bw;  // columns 0-15, then 16-31
+                    const long a = *reinterpret_cast<const long*>(a_at + (4 * h + gg) * (16 * 32));
+                    const rm_v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
+                    const rm_v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
+                    // scales 8 h + 2 gg and 8 h + 2 gg + 1 (ggml's q6_K order: 16 columns a scale)
+                    const int si = 8 * h + 2 * gg;
+                    const int s0 = (int)(int8_t)(uint8_t)(scw[si >> 2] >> (8 * (si & 3)));
+                    const int s1 = (int)(int8_t)(uint8_t)(scw[(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
+                    // |dot| <= 32 * 128 * 16 and |sc| <= 128: 24-bit multiplies are exact
+#pragma unroll
+                    for (int e = 0; e < 4; e++) S[e] += __mul24(s0, i0[e]) + __mul24(s1, i1[e]);
+                }
             }
+            const float d = kf_h2f(*reinterpret_cast<const uint16_t*>(wr + 208));
 #pragma unroll
-            for (int i = 0; i < 4; i++) kf_bdma16(rx, va[i], sb * KF_Q4_K_BLOCK, b + G::A + 1024 * i);
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], d * (float)S[e], acc[e]);
+        } else {
+            constexpr int QS = TY == KF_TYPE_Q5_K ? 48 : 16;  // the nibbles' offset in the block
+            RmW v;
+            v.hd = *reinterpret_cast<const rm_v4u*>(wb + c * G::WROW);
+#pragma unroll
+            for (int p = 0; p < 4; p++) v.q[p] = *reinterpret_cast<const rm_v2u*>(wb + c * G::WROW + QS + 32 * p + 8 * q);
+            if constexpr (TY == KF_TYPE_Q5_K) v.qh = *reinterpret_cast<const rm_v2u*>(wb + c * G::WROW + 16 + 8 * q);
+            const int2 bs = *reinterpret_cast<const int2*>(ab + G::S + (c * 8 + 2 * q) * 4);
+            rm_v4h xo;
+            xo[0] = (_Float16)(float)(bs.x >> 6);
+            xo[1] = (_Float16)(float)(bs.x & 63);
+            xo[2] = (_Float16)(float)(bs.y >> 6);
+            xo[3] = (_Float16)(float)(bs.y & 63);
+            rm_v4i S;
+            rm_v4f mins;
+            rm_block<TY == KF_TYPE_Q5_K>(v, a_at, 16 * 32, xo, q, S, mins);
+            const float d = kf_h2f(v.hd.x & 0xffffu), dm = kf_h2f(v.hd.x >> 16);
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], fmaf(-dm, mins[e], d * (float)S[e]), acc[e]);
+        }
+    };
+
+    // Rows in groups of up to 64; within a group the wave walks items j = (super-block i, chunk cc), j = i C + cc:
+    // a super-block's weights are fetched with its first chunk and stay while all C chunks of staged rows pass, so a
+    // weight byte is read once per 64 rows. Item j + 2 is requested once item j is multiplied. The DMA goes through
+    // kf_adma16 / kf_adma4 (the buffers are picked at run time, and the compiler's own waits would drain the ring):
+    // every wait below is explicit.
+    for (int g0 = 0; g0 < rows; g0 += 16 * CM) {
+        const int Rg = min(16 * CM, rows - g0);
+        const int C = (Rg + 15) / 16;
+        const int items = msb * C;
+        // activation sources of the group (rows past Rg repeat row Rg - 1): A pieces (instruction i: groups 2 i, 2 i + 1;
+        // lane l: group 2 i + l / 32, row 16 cc + (l / 2) % 16, half l % 2), sums (lane l < 32: row l / 2, four sums from
+        // 4 (l % 2)), scales (lane l < 16: row l)
+        const kf_arsrc_t rx = kf_arsrc(xq + (int64_t)g0 * n, (uint64_t)Rg * n);
+        const kf_arsrc_t rs = kf_arsrc(xs32 + (int64_t)g0 * nsum, (uint64_t)Rg * nsum * 4);
+        const kf_arsrc_t rd = kf_arsrc(xd32 + (int64_t)g0 * nsum, (uint64_t)Rg * nsum * 4);
+        auto park = [&](int j) {
+            const int i = j / C, cc = j - i * C;
+            const int sb = kpart + KP * i;
+            if (cc == 0) {
+                uint8_t* b = ((i & 1) ? pw1 : pw0) + wave * G::WB;
+                if constexpr (G::DW) {
+                    const int so = (sb * SBB) & ~3;  // the window's start (rows 4-byte aligned)
+#pragma unroll
+                    for (int k = 0; k < G::WI; k++)
+                        if (G::UNITS % 64 == 0 || k + 1 < G::WI || lane < G::UNITS % 64) kf_adma4(rw, vpk[k], so, b + 256 * k);
+                } else {
+                    const int so = sb * SBB;
+#pragma unroll
+                    for (int k = 0; k < G::WI; k++)
+                        if (G::UNITS % 64 == 0 || k + 1 < G::WI || lane < G::UNITS % 64) kf_adma16(rw, vpk[k], so, b + 1024 * k);
+                }
+            }
+            uint8_t* b = ((j & 1) ? pa1 : pa0) + wave * G::AB;
+            const int r16 = 16 * cc;
+            const int ra = min(r16 + ((lane >> 1) & 15), Rg - 1);
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                kf_adma16(rx, ra * n + 32 * (2 * k + (lane >> 5)) + 16 * (lane & 1), sb * KF_Q4_K_BLOCK, b + G::A + 1024 * k);
             if constexpr (TY != KF_TYPE_Q6_K)
-                if (lane < 32) kf_bdma16(rs, vs, sb * 32, b + G::S);
-            if (lane < 16) kf_bdma4(rd, vd, sb * 32, b + G::D);
+                if (lane < 32) kf_adma16(rs, ra * nsum * 4 + 16 * (lane & 1), sb * 32, b + G::S);
+            if (lane < 16) kf_adma4(rd, min(r16 + lane, Rg - 1) * nsum * 4, sb * 32, b + G::D);
         };
-        rm_v4f acc = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
-        if (items > 0) park(0, pk0);
-        if (items > 1) park(1, pk1);
-        auto step = [&](uint8_t* buf, int j) {
-            if (j + 1 < items)
-                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(G::NI));
-            else
-                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-            const uint8_t* b = buf + wave * G::BUF;
-            const rm_v4f dx = *reinterpret_cast<const rm_v4f*>(b + G::D + 16 * q);
-            const uint8_t* a_at = b + G::A + c * 32 + 8 * q;
-            if constexpr (TY == KF_TYPE_Q6_K) {
-                const int sb = kpart + KP * j;
-                const uint8_t* wr = b + c * G::WROW + ((sb * SBB) & 3);  // the lane's row of the super-block
-                typedef uint32_t v2a2 __attribute__((ext_vector_type(2), aligned(2)));
-                typedef uint32_t v4a2 __attribute__((ext_vector_type(4), aligned(2)));
-                const v4a2 scv = *reinterpret_cast<const v4a2*>(wr + 192);  // the row's sixteen int8 scales
-                const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
-                rm_v4i S = rm_v4i{0, 0, 0, 0};
-                const uint32_t m4 = 0x0f0f0f0fu, m3 = 0x03030303u, hb = 0x80808080u, k32 = 0x20202020u;
+        rm_v4f acc[CM];
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const v2a2 la = *reinterpret_cast<const v2a2*>(wr + 64 * h + 8 * q);
-                    const v2a2 lb = *reinterpret_cast<const v2a2*>(wr + 64 * h + 32 + 8 * q);
-                    const v2a2 qh = *reinterpret_cast<const v2a2*>(wr + 128 + 32 * h + 8 * q);
+        for (int k = 0; k < CM; k++) acc[k] = rm_v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if (items > 0) park(0);
+        if (items > 1) park(1);
+        for (int i = 0; i < msb; i++) {
+            const int sb = kpart + KP * i;
+            const uint8_t* wb = ((i & 1) ? pw1 : pw0) + wave * G::WB;
 #pragma unroll
-                    for (int gg = 0; gg < 4; gg++) {
-                        const v2a2 src = (gg & 1) ? lb : la;
-                        uint32_t wv[2];
-#pragma unroll
-                        for (int e = 0; e < 2; e++) {
-                            const uint32_t lo = (gg >> 1) ? (src[e] >> 4) & m4 : src[e] & m4;
-                            const uint32_t v = lo | (((qh[e] >> (2 * gg)) & m3) << 4);  // q in [0, 63] per byte
-                            wv[e] = ((v | hb) - k32) ^ hb;                            // q - 32 per byte, no borrows
-                        }
-                        const long bw = (long)wv[0] | ((long)wv[1] << 32);
-                        const long b0 = q < 2 ? bw : 0, b1 = q < 2 ? 0 : bw;  // columns 0-15, then 16-31
-                        const long a = *reinterpret_cast<const long*>(a_at + (4 * h + gg) * (16 * 32));
-                        const rm_v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b0, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
-                        const rm_v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b1, rm_v4i{0, 0, 0, 0}, 0, 0, 0);
-                        // scales 8 h + 2 gg and 8 h + 2 gg + 1 (ggml's q6_K order: 16 columns a scale)
-                        const int si = 8 * h + 2 * gg;
-                        const int s0 = (int)(int8_t)(uint8_t)(scw[si >> 2] >> (8 * (si & 3)));
-                        const int s1 = (int)(int8_t)(uint8_t)(scw[(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
-                        // |dot| <= 32 * 128 * 16 and |sc| <= 128: 24-bit multiplies are exact
-#pragma unroll
-                        for (int e = 0; e < 4; e++) S[e] += __mul24(s0, i0[e]) + __mul24(s1, i1[e]);
+            for (int cc = 0; cc < CM; cc++) {
+                if (cc < C) {
+                    const int j = i * C + cc;
+                    // loads complete in issue order: wait until only item j + 1's DMA is outstanding
+                    if (j + 1 >= items)
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+                    else if ((j + 1) % C == 0)
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(G::NA + G::WI));
+                    else
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(G::NA));
+                    compute(wb, ((j & 1) ? pa1 : pa0) + wave * G::AB, sb, acc[cc]);
+                    if (j + 2 < items) {
+                        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));  // this item's reads are done
+                        park(j + 2);
                     }
                 }
-                const float d = kf_h2f(*reinterpret_cast<const uint16_t*>(wr + 208));
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], d * (float)S[e], acc[e]);
-            } else {
-                constexpr int QS = TY == KF_TYPE_Q5_K ? 48 : 16;  // the nibbles' offset in the block
-                RmW v;
-                v.hd = *reinterpret_cast<const rm_v4u*>(b + c * G::WROW);
-#pragma unroll
-                for (int p = 0; p < 4; p++) v.q[p] = *reinterpret_cast<const rm_v2u*>(b + c * G::WROW + QS + 32 * p + 8 * q);
-                if constexpr (TY == KF_TYPE_Q5_K) v.qh = *reinterpret_cast<const rm_v2u*>(b + c * G::WROW + 16 + 8 * q);
-                const int2 bs = *reinterpret_cast<const int2*>(b + G::S + (c * 8 + 2 * q) * 4);
-                rm_v4h xo;
-                xo[0] = (_Float16)(float)(bs.x >> 6);
-                xo[1] = (_Float16)(float)(bs.x & 63);
-                xo[2] = (_Float16)(float)(bs.y >> 6);
-                xo[3] = (_Float16)(float)(bs.y & 63);
-                rm_v4i S;
-                rm_v4f mins;
-                rm_block<TY == KF_TYPE_Q5_K>(v, a_at, 16 * 32, xo, q, S, mins);
-                const float d = kf_h2f(v.hd.x & 0xffffu), dm = kf_h2f(v.hd.x >> 16);
-#pragma unroll
-                for (int e = 0; e < 4; e++) acc[e] = fmaf(dx[e], fmaf(-dm, mins[e], d * (float)S[e]), acc[e]);
             }
-            if (j + 2 < items) {
-                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));  // this buffer's reads are done
-                park(j + 2, buf);
-            }
-        };
-        for (int it = 0; it < items; it += 2) {
-            step(pk0, it);
-            if (it + 1 < items) step(pk1, it + 1);
         }
-        // the KP partials of each tile, in kpart order
-        part[wave * 64 + lane] = acc;
-        __syncthreads();
-        if (kpart == 0) {
-            rm_v4f t = part[(tl * KP) * 64 + lane];
+        // per chunk, the KP partials of each tile in kpart order
 #pragma unroll
-            for (int k = 1; k < KP; k++) t += part[(tl * KP + k) * 64 + lane];
-            const int o = orow + c;
+        for (int cc = 0; cc < CM; cc++) {
+            if (cc < C) {
+                part[wave * 64 + lane] = acc[cc];
+                __syncthreads();
+                if (kpart == 0) {
+                    rm_v4f t = part[(tl * KP) * 64 + lane];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = 4 * q + e;
-                if (m < R && o < n_out) {
-                    const int64_t at = (int64_t)(c0 + m) * n_out + o;
-                    y[at] = t[e] + (bias ? bias[o] : 0.0f) + (res ? res[at] : 0.0f);
+                    for (int k = 1; k < KP; k++) t += part[(tl * KP + k) * 64 + lane];
+                    const int o = orow + c;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int m = 16 * cc + 4 * q + e;
+                        if (m < Rg && o < n_out) {
+                            const int64_t at = (int64_t)(g0 + m) * n_out + o;
+                            y[at] = t[e] + (bias ? bias[o] : 0.0f) + (res ? res[at] : 0.0f);
+                        }
+                    }
                 }
+                __syncthreads();  // before the next chunk's partials
             }
         }
-        __syncthreads();  // before the next chunk reuses the partials and buffers
     }
 }
 
@@ -634,7 +665,10 @@ hipError_t kf_launch_rows_mma_1(uint32_t ty, const void* w, int64_t row_bytes, c
     const auto* wb = static_cast<const uint8_t*>(w);
 #define KF_R1(TY, T)                                                                                               \
     {                                                                                                              \
-        rows_mma_1_kernel<TY, T><<<(tiles + T - 1) / T, RM_THREADS, 0, s>>>(wb, row_bytes, xq, xs32, xd32, n, n_out, rows, bias, res, y); \
+        if (rows <= 16)                                                                                            \
+            rows_mma_1_kernel<TY, T, 1><<<(tiles + T - 1) / T, RM_THREADS, 0, s>>>(wb, row_bytes, xq, xs32, xd32, n, n_out, rows, bias, res, y); \
+        else                                                                                                       \
+            rows_mma_1_kernel<TY, T, 4><<<(tiles + T - 1) / T, RM_THREADS, 0, s>>>(wb, row_bytes, xq, xs32, xd32, n, n_out, rows, bias, res, y); \
         return hipGetLastError();                                                                                  \
     }
 #define KF_R1_T(TY)          \
