@@ -30,7 +30,8 @@ def _check_act(act, rows, n, kind, values):
 
 
 @pytest.mark.parametrize("kind", [kf.ACT_Q8_0, kf.ACT_Q8K])
-@pytest.mark.parametrize("rows,n,affine", [(1, 4096, True), (3, 256, False), (7, 14336, True), (33, 4096, False)])
+@pytest.mark.parametrize("rows,n,affine", [(1, 4096, True), (3, 256, False), (7, 14336, True), (33, 4096, False), (2, 20480, True),
+                                          (70, 4096, True), (70, 14336, False)])
 def test_rms_norm_q8_bit_exact(cuda, kind, rows, n, affine):
     rng = np.random.default_rng(rows * 7 + n + kind)
     x = (rng.standard_normal((rows, n)) * rng.uniform(0.01, 40, (rows, 1))).astype(np.float32)
