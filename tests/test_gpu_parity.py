@@ -477,6 +477,37 @@ def test_matmul_q4_k_cost_model_rows(cuda, rows):
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
 
 
+@pytest.mark.parametrize("rows", [96, 256])
+def test_matmul_q4_k_wide_k_few_row_and_gemm(cuda, rows):
+    """Wide K (down's 14336 columns, a small n_out): the cost model keeps the few-row product here (its weight pass
+    is cheap against a GEMM round of 56 super-blocks), which then carries 96 or 256 rows in 64-row passes. The
+    selected kf_hip_matmul must equal that product (kf_hip_gemv) bit for bit; the few-row product and the tile GEMM
+    (kf_hip_gemm_i8) each against the CPU backend's int8 path on every 7th row."""
+    import torch
+
+    ty, n, n_out = kf.TYPE_Q4_K, 14336, 40
+    w = _weights(ty, n_out, n, 95 + rows)
+    x = kf.synth_normal(96 + rows, 1.0, rows * n).reshape(rows, n)
+    wt, xt = _tensor(w, cuda), _tensor(x, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    outs = {}
+    for name in ("matmul", "gemv", "gemm"):
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        if name == "matmul":
+            kf.matmul(ty, wt, xt, act, y, n_out)
+        elif name == "gemv":
+            kf.gemv(ty, wt, act, y, rows, n, n_out)
+        else:
+            kf.gemm_i8(ty, wt, act, y, rows, n, n_out)
+        torch.cuda.synchronize()
+        outs[name] = y.cpu().numpy()
+    assert np.array_equal(outs["matmul"].view(np.uint32), outs["gemv"].view(np.uint32))
+    sample = np.arange(0, rows, 7)
+    want = oracle.matmul_i8(ty, w, n, n_out, x[sample])
+    _close(outs["gemv"][sample], want)
+    _close(outs["gemm"][sample], want)
+
+
 LLAMA_SHAPES = {"qkv": (4096, 6144), "o": (4096, 4096), "gate": (4096, 14336), "down": (14336, 4096)}
 
 
