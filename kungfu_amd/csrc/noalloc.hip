@@ -6,6 +6,7 @@
 // In host code the array's name is only a host-side stand-in, not a device address: every host use goes through the
 // device address that hipGetSymbolAddress returns, looked up once per device (with that device current) on the
 // device's first call and kept per device.
+#include "kf_host.h"
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -68,4 +69,35 @@ extern "C" int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n
     if (!act) return KF_E_HIP;
     // quant_act writes every byte of the scratch that the product reads, so nothing is cleared between calls
     return kf_hip_matmul(ty, w, n_in, n_out, x, rows, act, bias, res, y, stream);
+}
+
+// ------------------------------------------------------------------------------------------------ split-K scratch
+// The split-K products' partial tiles and tickets (kf_host.h): static, so nothing is allocated and the addresses never
+// change. Each device has its own copy, found with hipGetSymbolAddress once per device.
+static __device__ __align__(256) uint8_t split_scratch[KF_SPLIT_SLOTS * KF_SPLIT_SCRATCH];
+
+void* kf_split_scratch(hipStream_t s) {
+    static std::mutex mu;
+    static std::map<int, uint8_t*> base;                       // per device
+    static std::map<std::pair<int, hipStream_t>, int> slot;    // per (device, stream)
+    static std::map<int, int> used;                            // slots handed out per device
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> g(mu);
+    auto b = base.find(dev);
+    if (b == base.end()) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(split_scratch)) != hipSuccess || !p) {
+            (void)hipGetLastError();
+            return nullptr;
+        }
+        b = base.emplace(dev, static_cast<uint8_t*>(p)).first;
+    }
+    auto it = slot.find({dev, s});
+    if (it == slot.end()) {
+        int& u = used[dev];
+        if (u >= KF_SPLIT_SLOTS) return nullptr;
+        it = slot.emplace(std::make_pair(dev, s), u++).first;
+    }
+    return b->second + (size_t)it->second * KF_SPLIT_SCRATCH;
 }

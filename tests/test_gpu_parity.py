@@ -542,6 +542,7 @@ def test_gemm_q8_0_all_rows_one_pass_variants(cuda, monkeypatch, variant, rows, 
     import torch
 
     monkeypatch.setenv("KF_GEMM_MR", variant)
+    monkeypatch.setenv("KF_GEMM_SK", "0")  # the split-K form takes these rows first
     rng = np.random.default_rng(rows * 7 + n_out)
     w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n)
     x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
@@ -553,3 +554,43 @@ def test_gemm_q8_0_all_rows_one_pass_variants(cuda, monkeypatch, variant, rows, 
     kf.gemm_i8(kf.TYPE_Q8_0, _tensor(w, cuda), act, y, rows, n, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
     torch.cuda.synchronize()
     _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res)
+
+
+@pytest.mark.parametrize("rows,n,n_out,splits", [(17, 4096, 4096, None), (32, 4096, 300, None), (33, 14336, 4100, None),
+                                                 (33, 14336, 4100, 7), (64, 4096, 14336, None), (50, 384, 200, None),
+                                                 (64, 1024, 64, None), (24, 1024, 256, 8)])
+def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits):
+    """17..64 Q8_0 rows with K split across blocks (partials summed in split order by the last block of each tile),
+    forced on for every size (KF_GEMM_SK=1; by default it takes matrices above 4096 x 4096): ragged rows and output
+    tiles, split counts that do not divide the chunks (7 of 112; 8 of 8: one chunk a split), three calls in a row on
+    one stream (the tickets return to zero), bias and residual; against the CPU backend, bit-identical between calls
+    (deterministic), and within the f32 bar of the scratch-free products (KF_GEMM_SK=0)."""
+    import torch
+
+    monkeypatch.setenv("KF_GEMM_SK", "1")
+    if splits:
+        monkeypatch.setenv("KF_GEMM_SK_S", str(splits))
+
+    rng = np.random.default_rng(rows * 13 + n + n_out)
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n_out)
+    x = (rng.standard_normal((rows, n)) * 2).astype(np.float32)
+    bias = kf.synth_normal(7, 1.0, n_out)
+    res = kf.synth_normal(8, 1.0, rows * n_out).reshape(rows, n_out)
+    wt, bt, rt = _tensor(w, cuda), _tensor(bias, cuda), _tensor(res, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8_0)
+    outs = []
+    for _ in range(3):
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt, res=rt)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    want = oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res
+    _close(outs[0], want)
+    monkeypatch.setenv("KF_GEMM_SK", "0")
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt, res=rt)
+    torch.cuda.synchronize()
+    _close(outs[0], y.cpu().numpy())
