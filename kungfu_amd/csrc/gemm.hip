@@ -812,188 +812,257 @@ __global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __r
 }
 
 // ------------------------------------------------------------------------------------------------ split K
-// 17..64 rows with K split across blocks. A block of four waves owns 64 weight rows (16 a wave) and all TM x 16
-// activation rows, over its share of K: the activation chunk (TM x 16 rows x 128 columns and their group scales,
-// staged as in gemm_q8_0_mr_kernel) is DMA'd once per block and read by all four waves, so the activation bytes moved
-// are about M / 64 times the weight bytes instead of M / 16; the K split gives the grid about two blocks a CU even
-// where N / 64 tiles are few (N = 4096: 64 tiles, eight splits). Three stages ring, one barrier a chunk. Each block
-// writes its 64 x 64 partial tile to the scratch, and the last block of a tile to arrive (an atomic ticket per tile)
-// adds the partials in split order (deterministic whatever the arrival order), adds bias and residual, stores y and
-// resets the ticket; nothing waits on another block. All of the DMA goes through kf_adma16 / kf_adma4 with explicit
-// waits (the compiler would otherwise drain the ring before every LDS read).
-constexpr int SK2_G = 4;                                   // groups per chunk (128 columns)
-constexpr int SK2_ACT = 64 * SK2_G * 32;                   // activation bytes of a chunk (64 rows)
-constexpr int SK2_AB = SK2_ACT + SK2_G * 64 * 4;           // + the scales, group-major [group][row]
-constexpr int SK2_WCH = SK2_G * KF_Q8_0_BYTES;             // 136 weight bytes a row and chunk
-constexpr int SK2_WB = 16 * SK2_WCH;                       // a wave's 16 rows: 2176 bytes (544 dwords)
-constexpr int SK2_WI = (SK2_WB / 4 + 63) / 64;             // dword DMA instructions for them: 9
-constexpr int SK2_STAGE = SK2_AB + 4 * SK2_WB;
-constexpr int SK2_NI = 2 + 1 + SK2_WI;                     // DMA instructions a wave issues per chunk
-constexpr int SK2_TILE = 64 * 64;                          // floats of a partial tile
+// 17..64 rows with K split across blocks. A block of four waves owns 64 TN weight rows (16 TN a wave) and all TM x 16
+// activation rows, over its share of K in chunks of G groups: the activation chunk (TM x 16 rows x 32 G columns and
+// their group scales, 16-byte piece s of row r staged in slot s ^ (r % 2G) for bank-spread operand reads) is DMA'd
+// once per block and read by all four waves, so the activation bytes moved are about M / (64 TN) times the weight
+// bytes; the K split gives the grid about two blocks a CU even where the N / (64 TN) tiles are few. A row's 34 G
+// weight bytes of a chunk touch 2, 3 or 5 cache lines for G = 4, 8, 16: the L1's outstanding requests bound the
+// rate, so longer chunks move more bytes a request. NS stages ring (NS - 1 chunks in flight while one is
+// multiplied), one barrier a chunk.
+// Each block writes its partial tile to the scratch, and the last block of a tile to arrive (an atomic ticket per
+// tile) adds the partials in split order (deterministic whatever the arrival order), adds bias and residual, stores y
+// and resets the ticket; nothing waits on another block. All of the DMA goes through kf_adma16 / kf_adma4 with
+// explicit waits (the compiler would otherwise drain the ring before every LDS read).
+template <int TM, int TN, int G>
+struct SplitGeo {
+    static constexpr int R = 16 * TM;                      // activation rows staged
+    static constexpr int BR = 64 * TN;                     // weight rows of a block
+    static constexpr int RB = 32 * G;                      // bytes of an activation row of a chunk
+    static constexpr int P = 2 * G;                        // its 16-byte pieces
+    static constexpr int RI = 1024 / RB;                   // rows a 16-byte DMA instruction covers
+    static constexpr int ACT = R * RB;                     // activation bytes of a chunk
+    static constexpr int AB = ACT + G * R * 4;             // + the scales, group-major [group][row]
+    static constexpr int WCH = G * KF_Q8_0_BYTES;          // weight bytes a row and chunk
+    static constexpr int WB = 16 * TN * WCH;               // a wave's weight bytes of a chunk
+    static constexpr int WI = (WB / 4 + 63) / 64;          // dword DMA instructions for them
+    static constexpr int STAGE = AB + 4 * WB;
+    static constexpr int AI = R / (4 * RI);                // 16-byte activation DMA instructions a wave
+    static constexpr int DI = G / 4;                       // scale DMA instructions a wave (one group each)
+    static constexpr int NI = AI + DI + WI;                // DMA instructions a wave issues per chunk
+    static constexpr int TILE = 64 * BR;                   // floats of a partial tile (64 rows at most)
+    static_assert(R % (4 * RI) == 0 && G % 4 == 0, "whole instructions a wave");
+};
 
-template <int TM>
+// wait until at most `rem` chunks after the current one (NI instructions each) are still in flight (rem <= RMAX)
+template <int NI, int RMAX>
+__device__ __forceinline__ void sk_wait(int rem) {
+    if constexpr (RMAX == 0) {
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+    } else {
+        if (rem >= RMAX)
+            __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI * RMAX));
+        else
+            sk_wait<NI, RMAX - 1>(rem);
+    }
+}
+
+template <int TM, int TN, int G, int NS>
 __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                            const float* __restrict__ xd32, const float* __restrict__ bias,
                                                            const float* __restrict__ res, float* __restrict__ y, int M, int N, int K, int S,
                                                            int* __restrict__ tickets, float* __restrict__ part) {
-    __shared__ __align__(16) uint8_t st0[SK2_STAGE];
-    __shared__ __align__(16) uint8_t st1[SK2_STAGE];
-    __shared__ __align__(16) uint8_t st2[SK2_STAGE];
+    using Geo = SplitGeo<TM, TN, G>;
+    extern __shared__ __align__(16) uint8_t sk_ring[];     // NS stages of Geo::STAGE bytes
     __shared__ int last;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 15, q = lane >> 4;
     // the splits of a tile are consecutive blocks: they run together, and the last of them finishes the tile
     const int tile = blockIdx.x / S, sp = blockIdx.x - tile * S;
-    const int n0 = tile * 64;
+    const int n0 = tile * Geo::BR;
     const int kg = K >> 5;
-    const int chunks = K / (32 * SK2_G);
+    const int chunks = K / (32 * G);
     const int ch0 = (int)((int64_t)chunks * sp / S), ch1 = (int)((int64_t)chunks * (sp + 1) / S);
     const int nch = ch1 - ch0;
-    uint8_t* const stg[3] = {st0, st1, st2};
 
-    // activation DMA: the block's 8 row instructions (rows 8 i.., lane l: row 8 i + l / 8, piece (l % 8) ^ (row % 8))
-    // and 4 scale instructions (group g: lane l row l), instructions w, w + 4 and scale g = w for wave w
+    // activation DMA: RI-row instructions w + 4 i (lane l: row RI (w + 4 i) + l / P, piece (l % P) ^ (row % P)),
+    // and the scales of groups w + 4 i (lane l: row l, lanes past the staged rows idle)
     const kf_arsrc_t rx = kf_arsrc(xq, (uint64_t)M * K);
     const kf_arsrc_t rd = kf_arsrc(xd32, (uint64_t)M * kg * 4);
-    const int xr = lane >> 3, xs = lane & 7;
-    const int va0 = (8 * wave + xr) * K + 16 * (xs ^ (xr & 7));
-    const int va1 = (8 * (wave + 4) + xr) * K + 16 * (xs ^ (xr & 7));
-    const int vd = lane * kg * 4;
-    // weight DMA: the wave's 16 rows, dword e = 64 i + lane of the chunk's [16][136] block (rows past N read zeros)
-    const int wr0 = n0 + 16 * wave;
-    const kf_arsrc_t rw = kf_arsrc(w + (int64_t)min(wr0, N) * row_bytes, (uint64_t)max(N - wr0, 0) * row_bytes);
-    int vw[SK2_WI];
+    const int xr = lane / Geo::P, xs = lane % Geo::P;
+    int va[Geo::AI];
 #pragma unroll
-    for (int i = 0; i < SK2_WI; i++) {
-        const int e = min(256 * i + 4 * lane, SK2_WB - 4);
-        const int r = e / SK2_WCH;
-        vw[i] = r * (int)row_bytes + (e - r * SK2_WCH);
+    for (int i = 0; i < Geo::AI; i++) {
+        const int row = Geo::RI * (wave + 4 * i) + xr;
+        va[i] = row * K + 16 * (xs ^ (row % Geo::P));
+    }
+    const int vd = lane * kg * 4;
+    // weight DMA: the wave's 16 TN rows, dword e = 64 i + lane of the chunk's [16 TN][136] block (rows past N read
+    // zeros)
+    const int wr0 = n0 + 16 * TN * wave;
+    const kf_arsrc_t rw = kf_arsrc(w + (int64_t)min(wr0, N) * row_bytes, (uint64_t)max(N - wr0, 0) * row_bytes);
+    int vw[Geo::WI];
+#pragma unroll
+    for (int i = 0; i < Geo::WI; i++) {
+        const int e = min(256 * i + 4 * lane, Geo::WB - 4);
+        const int r = e / Geo::WCH;
+        vw[i] = r * (int)row_bytes + (e - r * Geo::WCH);
     }
     auto issue = [&](auto kb, int ch) __attribute__((always_inline)) {
-        uint8_t* b = stg[decltype(kb)::value];
-        const int cc = ch0 + min(ch, nch - 1);  // a slot past the split's last chunk reloads it: counts stay exact
-        kf_adma16(rx, va0, cc * (32 * SK2_G), b + 1024 * wave);
-        kf_adma16(rx, va1, cc * (32 * SK2_G), b + 1024 * (wave + 4));
-        kf_adma4(rd, vd, (cc * SK2_G + wave) * 4, b + SK2_ACT + 256 * wave);
-        uint8_t* wb = b + SK2_AB + wave * SK2_WB;
-        // the last instruction on the lanes that still hold bytes of the 16 rows (an instruction writes 256 bytes)
+        uint8_t* b = sk_ring + decltype(kb)::value * Geo::STAGE;
+        const int cc = ch0 + ch;
 #pragma unroll
-        for (int i = 0; i < SK2_WI; i++)
-            if ((SK2_WB / 4) % 64 == 0 || i + 1 < SK2_WI || lane < (SK2_WB / 4) % 64) kf_adma4(rw, vw[i], cc * SK2_WCH, wb + 256 * i);
+        for (int i = 0; i < Geo::AI; i++) kf_adma16(rx, va[i], cc * Geo::RB, b + 1024 * (wave + 4 * i));
+#pragma unroll
+        for (int i = 0; i < Geo::DI; i++)
+            if (Geo::R == 64 || lane < Geo::R) kf_adma4(rd, vd, (cc * G + wave + 4 * i) * 4, b + Geo::ACT + Geo::R * 4 * (wave + 4 * i));
+        uint8_t* wb = b + Geo::AB + wave * Geo::WB;
+        // the last instruction on the lanes that still hold bytes of the rows (an instruction writes 256 bytes)
+#pragma unroll
+        for (int i = 0; i < Geo::WI; i++)
+            if ((Geo::WB / 4) % 64 == 0 || i + 1 < Geo::WI || lane < (Geo::WB / 4) % 64) kf_adma4(rw, vw[i], cc * Geo::WCH, wb + 256 * i);
     };
 
-    v4f acc[TM];
+    v4f acc[TM][TN];
 #pragma unroll
-    for (int t = 0; t < TM; t++) acc[t] = v4f{};
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[t][j] = v4f{};
     auto compute = [&](auto kb) __attribute__((always_inline)) {
-        const uint8_t* b = stg[decltype(kb)::value];
-        const uint8_t* wr = b + SK2_AB + wave * SK2_WB + c * SK2_WCH;
+        const uint8_t* b = sk_ring + decltype(kb)::value * Geo::STAGE;
+        const uint8_t* wr = b + Geo::AB + wave * Geo::WB + c * Geo::WCH;
 #pragma unroll
-        for (int g = 0; g < SK2_G; g++) {
-            const uint8_t* wp = wr + g * KF_Q8_0_BYTES;
-            const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
-            const long bq = (long)bv.x | ((long)bv.y << 32);
-            const float dw = (float)*reinterpret_cast<const _Float16*>(wp);
+        for (int g = 0; g < G; g++) {
+            // the scales' outer product d_x d_w on the matrix cores (A and B hold them at k = 0, zeros elsewhere):
+            // both are f16 values, so the f32 products are exact, and the VALU keeps one conversion and one FMA
+            long bq[TN];
+            v4h sb[TN];
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                const uint8_t* wp = wr + 16 * j * Geo::WCH + g * KF_Q8_0_BYTES;
+                const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
+                bq[j] = (long)bv.x | ((long)bv.y << 32);
+                const _Float16 dw = *reinterpret_cast<const _Float16*>(wp);
+                sb[j] = v4h{};
+                sb[j][0] = q == 0 ? dw : (_Float16)0.0f;
+            }
 #pragma unroll
             for (int t = 0; t < TM; t++) {
                 const int r = 16 * t + c;
-                const int sl = (2 * g + (q >> 1)) ^ (r & 7);
-                const long a = *reinterpret_cast<const long*>(b + r * (32 * SK2_G) + 16 * sl + 8 * (q & 1));
-                const v4f dx = *reinterpret_cast<const v4f*>(b + SK2_ACT + 256 * g + 4 * (16 * t + 4 * q));
-                const v4i_ ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq, v4i_{}, 0, 0, 0);
-                // d_x d_w I: d_x and d_w are f16 values, so d_x d_w is exact
+                const int sl = (2 * g + (q >> 1)) ^ (r % Geo::P);
+                const long a = *reinterpret_cast<const long*>(b + r * Geo::RB + 16 * sl + 8 * (q & 1));
+                const _Float16 dx = (_Float16)*reinterpret_cast<const float*>(b + Geo::ACT + Geo::R * 4 * g + 4 * r);
+                v4h sa = v4h{};
+                sa[0] = q == 0 ? dx : (_Float16)0.0f;
 #pragma unroll
-                for (int k = 0; k < 4; k++) acc[t][k] = fmaf((float)ci[k], dx[k] * dw, acc[t][k]);
+                for (int j = 0; j < TN; j++) {
+                    const v4i_ ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[j], v4i_{}, 0, 0, 0);
+                    const v4f sc = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, sb[j], v4f{}, 0, 0, 0);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) acc[t][j][k] = fmaf((float)ci[k], sc[k], acc[t][j][k]);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // chunk i: wait for this wave's share of it (loads complete in issue order; chunk i + 1's NI instructions may stay
-    // in flight), the barrier makes every wave's share visible and frees the buffer chunk i + 2 lands in (chunk i - 1's)
+    // chunk i: wait for this wave's share of it (loads complete in issue order; the chunks after it, up to NS - 2,
+    // may stay in flight), the barrier makes every wave's share visible and frees the stage chunk i + NS - 1 lands in
+    // (chunk i - 1's)
     auto step = [&](auto kb, int i) __attribute__((always_inline)) {
         constexpr int B = decltype(kb)::value;
-        if (i + 1 < nch)
-            __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(SK2_NI));
-        else
-            __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        sk_wait<Geo::NI, NS - 2>(min(nch - 1 - i, NS - 2));
         __syncthreads();
-        if (i + 2 < nch) issue(std::integral_constant<int, (B + 2) % 3>{}, i + 2);
+        if (i + NS - 1 < nch) issue(std::integral_constant<int, (B + NS - 1) % NS>{}, i + NS - 1);
         compute(kb);
     };
-    if (nch > 0) {
-        issue(std::integral_constant<int, 0>{}, 0);
-        if (nch > 1) issue(std::integral_constant<int, 1>{}, 1);
-        for (int i = 0; i < nch; i += 3) {
-            step(std::integral_constant<int, 0>{}, i);
-            if (i + 1 >= nch) break;
-            step(std::integral_constant<int, 1>{}, i + 1);
+    static_assert(NS >= 2 && NS <= 4, "two to four stages");
+    issue(std::integral_constant<int, 0>{}, 0);  // nch >= 1: the launcher gives every split a chunk
+    if constexpr (NS > 2)
+        if (1 < nch) issue(std::integral_constant<int, 1>{}, 1);
+    if constexpr (NS > 3)
+        if (2 < nch) issue(std::integral_constant<int, 2>{}, 2);
+    for (int i = 0; i < nch; i += NS) {
+        step(std::integral_constant<int, 0>{}, i);
+        if (i + 1 >= nch) break;
+        step(std::integral_constant<int, 1>{}, i + 1);
+        if constexpr (NS > 2) {
             if (i + 2 >= nch) break;
             step(std::integral_constant<int, 2>{}, i + 2);
         }
+        if constexpr (NS > 3) {
+            if (i + 3 >= nch) break;
+            step(std::integral_constant<int, 3>{}, i + 3);
+        }
     }
-    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
 
-    // the partial tile: lane (c, q) of wave w holds rows 16 t + 4 q + k, column 16 w + c. Partials and tickets are
-    // read and written with system-scope relaxed atomics, which go through the caches to memory, so the blocks of a
-    // tile on different XCDs (each with its own L2) see each other's partials without an L2 write-back (a
-    // __threadfence here, one per block, cost more than the product). Every lane waits for its partial stores to
-    // complete before the barrier, and the ticket is taken after it.
-    float* pt = part + (size_t)blockIdx.x * SK2_TILE;
+    // the partial tile [row][BR columns]: lane (c, q) of wave w holds rows 16 t + 4 q + k, column 16 (TN w + j) + c.
+    // Partials and tickets are read and written with system-scope relaxed atomics, which go through the caches to
+    // memory, so the blocks of a tile on different XCDs (each with its own L2) see each other's partials without an L2
+    // write-back (a __threadfence here, one per block, cost more than the product). Every lane waits for its partial
+    // stores to complete before the barrier, and the ticket is taken after it.
+    float* pt = part + (size_t)blockIdx.x * Geo::TILE;
 #pragma unroll
     for (int t = 0; t < TM; t++)
 #pragma unroll
-        for (int k = 0; k < 4; k++)
-            __hip_atomic_store(pt + (16 * t + 4 * q + k) * 64 + 16 * wave + c, acc[t][k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                __hip_atomic_store(pt + (16 * t + 4 * q + k) * Geo::BR + 16 * (TN * wave + j) + c, acc[t][j][k], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
     __syncthreads();
     if (threadIdx.x == 0) last = __hip_atomic_fetch_add(&tickets[tile], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == S - 1;
     __syncthreads();
     if (!last) return;
-    // the thread's TM x 4 outputs (idx = threadIdx.x + 256 j), the S partials of all of them in flight per split:
-    // each load is a trip to memory, so the split loop waits S times, not S x TM x 4 times
-    const float* p0 = part + (size_t)tile * S * SK2_TILE;
-    float v[TM * 4];
+    // the thread's V outputs (idx = threadIdx.x + 256 u: row idx / BR, column idx % BR), the partials of all of them
+    // in flight per split: each load is a trip to memory, so the split loop (four splits a round) waits about S / 4
+    // times, not S V times
+    constexpr int V = TM * 16 * Geo::BR / 256;
+    constexpr int RPU = 256 / Geo::BR;                     // rows a step of u advances
+    const int col = threadIdx.x % Geo::BR, row0 = threadIdx.x / Geo::BR;
+    const float* p0 = part + (size_t)tile * S * Geo::TILE;
+    float v[V];
 #pragma unroll
-    for (int j = 0; j < TM * 4; j++) v[j] = 0.0f;
+    for (int u = 0; u < V; u++) v[u] = 0.0f;
+#pragma unroll 4
     for (int k = 0; k < S; k++) {
-        float u[TM * 4];
+        float x[V];
 #pragma unroll
-        for (int j = 0; j < TM * 4; j++)
-            u[j] = __hip_atomic_load(p0 + (size_t)k * SK2_TILE + threadIdx.x + 256 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        for (int u = 0; u < V; u++)
+            x[u] = __hip_atomic_load(p0 + (size_t)k * Geo::TILE + threadIdx.x + 256 * u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 #pragma unroll
-        for (int j = 0; j < TM * 4; j++) v[j] += u[j];
+        for (int u = 0; u < V; u++) v[u] += x[u];
     }
     // bias and residual with clamped (always valid) indices, so all of their loads are in flight together too
-    const int n = min(n0 + (int)(threadIdx.x & 63), N - 1);
+    const int n = min(n0 + col, N - 1);
     const float bn = bias ? bias[n] : 0.0f;
-    float r[TM * 4];
+    float r[V];
 #pragma unroll
-    for (int j = 0; j < TM * 4; j++) r[j] = res ? res[(int64_t)min((int)(threadIdx.x >> 6) + 4 * j, M - 1) * N + n] : 0.0f;
+    for (int u = 0; u < V; u++) r[u] = res ? res[(int64_t)min(row0 + RPU * u, M - 1) * N + n] : 0.0f;
 #pragma unroll
-    for (int j = 0; j < TM * 4; j++) {
-        const int m = (threadIdx.x >> 6) + 4 * j;
-        if (m < M && n0 + (int)(threadIdx.x & 63) < N) y[(int64_t)m * N + n] = v[j] + bn + r[j];
+    for (int u = 0; u < V; u++) {
+        const int m = row0 + RPU * u;
+        if (m < M && n0 + col < N) y[(int64_t)m * N + n] = v[u] + bn + r[u];
     }
     if (threadIdx.x == 0) __hip_atomic_store(&tickets[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
-// The split-K launch: S splits of K per 64-row weight tile, about two blocks a CU; hipErrorNotSupported when the
-// scratch cannot be had (graph capture before first use, a no-allocation call) or does not hold the partials
-template <int TM>
+// The split-K launch: S splits of K per weight tile, about BPC blocks a CU (as many as the stages' LDS lets a CU
+// hold, at most two), as many as the scratch holds; hipErrorNotSupported when the scratch cannot be had (a fifth
+// stream)
+template <int TM, int TN, int G, int NS>
 hipError_t gemm_sk_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
                           float* y, int M, int N, int K, hipStream_t s) {
-    const int tiles = (N + 63) / 64, chunks = K / (32 * SK2_G);
-    int S = std::max(1, 2 * kf_cu_count() / tiles);
+    using Geo = SplitGeo<TM, TN, G>;
+    constexpr int LDS = NS * Geo::STAGE;
+    constexpr int BPC = std::min(2, 160 * 1024 / (LDS + 256));
+    static_assert(BPC >= 1, "the stages fit one CU");
+    auto* fn = gemm_q8_0_sk_kernel<TM, TN, G, NS>;
+    const int tiles = (N + Geo::BR - 1) / Geo::BR, chunks = K / (32 * G);
+    int S = std::max(1, BPC * kf_cu_count() / tiles);
     S = std::min(S, std::max(1, chunks / 3));  // at least three chunks a split
     if (const char* e = getenv("KF_GEMM_SK_S")) S = std::max(1, std::min(atoi(e), chunks));  // a comparison knob
-    if (tiles > KF_SPLIT_TICKETS || (size_t)tiles * S * SK2_TILE * 4 > KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4)
-        return hipErrorNotSupported;
+    const size_t room = (KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4) / ((size_t)tiles * Geo::TILE * 4);
+    S = std::min<int>(S, (int)std::min<size_t>(room, 1 << 20));
+    if (tiles > KF_SPLIT_TICKETS || S < 1) return hipErrorNotSupported;
     char* scr = static_cast<char*>(kf_split_scratch(s));
     if (!scr) return hipErrorNotSupported;
+    const hipError_t le = kf_raise_lds(reinterpret_cast<const void*>(fn), LDS);
+    if (le != hipSuccess) return le;
     int* tickets = reinterpret_cast<int*>(scr);
     float* part = reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4);
-    gemm_q8_0_sk_kernel<TM><<<tiles * S, 256, 0, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K, S, tickets, part);
+    fn<<<tiles * S, 256, LDS, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K, S, tickets, part);
     return hipGetLastError();
 }
 
@@ -1087,8 +1156,24 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
         const char* ske = getenv("KF_GEMM_SK");
         const bool sk = ske ? atoi(ske) != 0 : (int64_t)N * K > (1ll << 24);
         if (M > 16 && M <= 64 && K % 128 == 0 && (K / 32) % 2 == 0 && sk) {
-            const hipError_t e = M <= 32 ? gemm_sk_launch<2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                                         : gemm_sk_launch<4>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+            const char* ve = getenv("KF_GEMM_SK_V");  // 10 G + NS (groups a chunk, ring stages): a tuning knob
+            const int var = ve ? atoi(ve) : 0;
+            // 8-group chunks in two stages where K allows (MI355X, Llama-3-8B shapes at 32 / 64 rows: gate 25.1 / 37.2
+            // against 26.0 / 38.3 us with 4-group chunks in three, down 24.5 / 37.4 against 25.3 / 39.3)
+            const int v = var ? var : K % 256 == 0 ? 82 : 43;
+            hipError_t e = hipErrorNotSupported;
+            if (K % (32 * (v / 10)) == 0) {
+                if (M <= 32)
+                    e = v == 83    ? gemm_sk_launch<2, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                        : v == 82  ? gemm_sk_launch<2, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                        : v == 162 ? gemm_sk_launch<2, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                                   : gemm_sk_launch<2, 1, 4, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+                else
+                    e = v == 83    ? gemm_sk_launch<4, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                        : v == 82  ? gemm_sk_launch<4, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                        : v == 162 ? gemm_sk_launch<4, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                                   : gemm_sk_launch<4, 1, 4, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+            }
             if (e != hipErrorNotSupported) return e;
         }
         if (M > 48 && M <= MR_ROWS && K % (32 * MR_G) == 0 && !getenv("KF_GEMM_NO_MR")) {

@@ -556,20 +556,26 @@ def test_gemm_q8_0_all_rows_one_pass_variants(cuda, monkeypatch, variant, rows, 
     _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res)
 
 
-@pytest.mark.parametrize("rows,n,n_out,splits", [(17, 4096, 4096, None), (32, 4096, 300, None), (33, 14336, 4100, None),
-                                                 (33, 14336, 4100, 7), (64, 4096, 14336, None), (50, 384, 200, None),
-                                                 (64, 1024, 64, None), (24, 1024, 256, 8)])
-def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits):
+@pytest.mark.parametrize("rows,n,n_out,splits,var", [(17, 4096, 4096, None, None), (32, 4096, 300, None, None),
+                                                     (33, 14336, 4100, None, None), (33, 14336, 4100, 7, None),
+                                                     (64, 4096, 14336, None, None), (50, 384, 200, None, None),
+                                                     (64, 1024, 64, None, None), (24, 1024, 256, 4, None),
+                                                     (40, 4096, 1000, None, 43), (64, 14336, 520, 5, 43),
+                                                     (20, 4096, 700, None, 83), (64, 2048, 300, None, 162)])
+def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
     """17..64 Q8_0 rows with K split across blocks (partials summed in split order by the last block of each tile),
     forced on for every size (KF_GEMM_SK=1; by default it takes matrices above 4096 x 4096): ragged rows and output
-    tiles, split counts that do not divide the chunks (7 of 112; 8 of 8: one chunk a split), three calls in a row on
-    one stream (the tickets return to zero), bias and residual; against the CPU backend, bit-identical between calls
-    (deterministic), and within the f32 bar of the scratch-free products (KF_GEMM_SK=0)."""
+    tiles, split counts that do not divide the chunks (7 of 56; 4 of 4: one chunk a split), the chunk forms (4, 8, 16
+    groups; two or three stages: KF_GEMM_SK_V), three calls in a row on one stream (the tickets return to zero), bias
+    and residual; against the CPU backend, bit-identical between calls (deterministic), and within the f32 bar of the
+    scratch-free products (KF_GEMM_SK=0)."""
     import torch
 
     monkeypatch.setenv("KF_GEMM_SK", "1")
     if splits:
         monkeypatch.setenv("KF_GEMM_SK_S", str(splits))
+    if var:
+        monkeypatch.setenv("KF_GEMM_SK_V", str(var))
 
     rng = np.random.default_rng(rows * 13 + n + n_out)
     w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n_out)
