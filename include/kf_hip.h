@@ -122,10 +122,13 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
  * dots, rescaled by the group's activation and weight scales. q4_K (Q8K-kind activations, n a multiple of 256): the
  * 6-bit scales split into two 3-bit halves folded into two int8 operand planes, so two int8 MFMA chains form the
  * exact super-block integer; the mins term by an exact f16 MFMA per super-block, and the float rescale once per 256
- * columns.
- * Replaces kf8_gemm_dense / Store::gemm (crates/kf-backend-cuda/src/kernels/kf8.cu:375-395, HAS_M for q4_K;
- * crates/kf-backend-cuda/src/kf8.rs:310-323) without the KF8 unpack pass (kf_unpack_i8, quant.cuh:585-601): the
- * native q8_0 / q4_K bytes are read directly. */
+ * columns. q5_K and q6_K (Q8K-kind activations, n a multiple of 256; q6_K: a multiple of 2048, so that its 210-byte
+ * super-block rows start 16-byte aligned): one int8 MFMA per 32-column group (q6_K: per 16-column scale) gives the
+ * exact int32 sub-block dots, the integer sub-scales are applied by multiply-adds into the exact super-block integer,
+ * q5_K's mins by an exact f16 MFMA; other shapes return KF_E_UNSUPPORTED (kf_hip_gemv takes them).
+ * Replaces kf8_gemm_dense / Store::gemm (crates/kf-backend-cuda/src/kernels/kf8.cu:375-395, HAS_M for q4_K / q5_K;
+ * crates/kf-backend-cuda/src/kf8.rs:310-323) without the KF8 unpack pass (kf_unpack_i8, quant.cuh:585-601, instantiated
+ * for q5_K / q6_K at quant_q5_K.cu:114 / quant_q6_K.cu:131): the native bytes are read directly. */
 int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                    int rows, int n, int n_out, void* stream);
 

@@ -41,6 +41,9 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
                                int N, int K, hipStream_t s);
 int kf_gemm_k_multiple();
 
+bool kf_gemm_kq_ok(uint32_t ty, const void* w, int64_t row_bytes, int K, int N);
+hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
+                             int M, int N, int K, hipStream_t s);
 hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                               int N, int K, hipStream_t s);
 int kf_rows_max_n(uint32_t ty);
@@ -247,7 +250,13 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
         const hipError_t e = kf_launch_gemm_q4k(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
         return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
     }
-    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0 and q4_K weights (type %u given; q5_K and q6_K go through kf_hip_gemv)", ty);
+    if (ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) {
+        if (!kf_gemm_kq_ok(ty, w, row_bytes, n, n_out))
+            return fail(KF_E_UNSUPPORTED, "the q5_K/q6_K GEMM needs 16-byte aligned weights and rows (q6_K: %d columns, a multiple of 2048) and a matrix below 2 GB; kf_hip_gemv takes any", n);
+        const hipError_t e = kf_launch_gemm_kq(ty, w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
+        return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
+    }
+    if (ty != KF_TYPE_Q8_0) return fail(KF_E_UNSUPPORTED, "the int8 GEMM runs q8_0, q4_K, q5_K and q6_K weights (type %u given)", ty);
     if (n % kf_gemm_k_multiple() != 0) return fail(KF_E_INVALID, "%d columns, the GEMM needs a multiple of %d", n, kf_gemm_k_multiple());
     const hipError_t e = kf_launch_gemm_q8_0(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
@@ -290,6 +299,23 @@ static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
     return t_gemm < t_rows;
 }
 
+// q5_K / q6_K: whether the tile GEMM beats the few-row product. The few-row product streams the weights once per 64
+// activation rows, about 1.05 (q5_K) / 1.55 (q6_K) us per MB and pass; a GEMM block computes a 64 x 256 tile over all
+// of K, about 3.45 / 5.6 us per super-block, and its grid runs in rounds of one block a CU (MI355X, Llama-3-8B gate and
+// down shapes at 32-2048 rows: the model picks the faster product at every measured point). KF_KQ_GEMM=0 / 1 forces
+// the choice (a comparison knob).
+static bool kq_gemm_pays(uint32_t ty, int rows, int n_in, int n_out, int64_t row_bytes) {
+    if (const char* e = getenv("KF_KQ_GEMM")) return atoi(e) != 0;
+    if (rows < 2) return false;
+    const bool q6 = ty == KF_TYPE_Q6_K;
+    const double mb = (double)n_out * row_bytes / 1e6;
+    const double t_rows = rows / 64.0 * mb * (q6 ? 1.55 : 1.05);
+    const int64_t blocks = (int64_t)((n_out + 255) / 256) * ((rows + 63) / 64);
+    const int cus = kf_cu_count();
+    const double t_gemm = (double)((blocks + cus - 1) / cus) * (n_in / 256) * (q6 ? 5.6 : 3.45);
+    return t_gemm < t_rows;
+}
+
 namespace {
 
 // The product of kf_hip_matmul once the activations are quantized
@@ -300,6 +326,8 @@ int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float
     if (rows > 1 && ty == KF_TYPE_Q8_0 && n_in % kf_gemm_k_multiple() == 0 && n_out > 0)
         return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     if (ty == KF_TYPE_Q4_K && n_out > 0 && q4k_gemm_pays(rows, n_in, n_out, rb))
+        return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+    if ((ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) && n_out > 0 && kq_gemm_pays(ty, rows, n_in, n_out, rb) && kf_gemm_kq_ok(ty, w, rb, n_in, n_out))
         return kf_hip_gemm_i8(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
     return kf_hip_gemv(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
 }

@@ -1,0 +1,301 @@
+// Prefill GEMM on native q5_K and q6_K bytes: y[m][n] = sum over super-blocks b of dx[m][b] * (d[n][b] * S_b[m][n]
+// - dmin[n][b] * mins_b[m][n]) (+ bias[n] + res[m][n]), with S_b the reference's exact super-block integer:
+//   * q5_K (crates/kf-quant/src/types/q5_k.rs): S_b = sum_g sc_g I_g over the eight 32-column groups, I_g the int32
+//     dot of the group's 5-bit values (the fifth bit from qh) with the int8 activations; mins_b = sum_g m_g bsum_g;
+//   * q6_K (crates/kf-quant/src/types/q6_k.rs): S_b = sum_s sc_s (dot_s - 32 bsum_s) over the sixteen 16-column
+//     sub-blocks with int8 scales, formed as sum_s sc_s dot'_s with the operand q - 32 (an int8); no mins term.
+// It replaces the reference's unpack + KF8 GEMM for these types (crates/kf-backend-cuda/src/kernels/quant.cuh:585-601,
+// KF_QUANT_KERNELS_I8 in quant_q5_K.cu:114 / quant_q6_K.cu:131, kf8.cu:116-369), reading the native bytes directly.
+//
+// Arithmetic: per group and 32 x 32 tile one v_mfma_i32_32x32x32_i8 gives I_g exactly (q6_K: two, each with the
+// other 16 columns' operand bytes zeroed, for the two scales of the group); S_b accumulates by 24-bit multiply-adds
+// with the integer sub-scales (every product below 2^23), mins_b by one exact v_mfma_f32_32x32x16_f16 against
+// quant_act's split sums (as the q4_K GEMM), and the float rescale runs once per super-block and output.
+//
+// Schedule: eight waves (two a SIMD), one block a CU, block tile 64 x 256: each wave a 64 x 32 tile (two 32 x 32
+// MFMA tiles down M, one weight column tile), so a wave's weight operands serve two MFMAs. One super-block (K = 256)
+// per stage, two stage buffers: activations [row 64][256] with the 16-byte chunk swizzle c ^ (row % 16), weights
+// [row 256][WROW] (q5_K: the 176-byte super-block; q6_K: the 224-byte 16-byte aligned window around the 210-byte
+// block, which needs rows that start 16-byte aligned: K a multiple of 2048), the stage's activation scales and (q5_K)
+// mins operands. Every DMA instruction reads whole 16-byte pieces of consecutive rows, issued through inline assembly
+// with explicit waits; rows past M or N read as zeros through the hardware range check. Blocks run in XCD order (each
+// XCD a contiguous range of tiles, M fastest), so the blocks in flight on an XCD share their weight tiles in its L2.
+#include "kf_blocks.h"
+#include "kf_device.h"
+#include "kf_host.h"
+
+#include <type_traits>
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+
+constexpr int KQ_WAVES = 8, KQ_THREADS = 64 * KQ_WAVES;
+constexpr int KQ_TM = 2;                       // 32-row tiles per wave (all of the block's rows)
+constexpr int KQ_BM = 32 * KQ_TM;              // 64
+constexpr int KQ_BN = 32 * KQ_WAVES;           // 256: one 32-column tile per wave
+
+template <uint32_t TY>
+struct KqGeo {
+    static constexpr bool Q6 = TY == KF_TYPE_Q6_K;
+    static constexpr int SBB = Q6 ? KF_Q6_K_BYTES : KF_Q5_K_BYTES;  // bytes of a super-block
+    static constexpr int WROW = Q6 ? 224 : KF_Q5_K_BYTES;            // LDS bytes of a weight row's super-block
+    static constexpr int PR = WROW / 16;                             // its 16-byte pieces
+    static constexpr int A = 0;                                      // activations [row 64][256]
+    static constexpr int W = A + KQ_BM * 256;                        // weights [row 256][WROW]
+    static constexpr int DX = W + KQ_BN * WROW;                      // activation scales [row 64] f32
+    static constexpr int XS = DX + KQ_BM * 4;                        // q5_K: mins operands [row 64][16] f16
+    static constexpr int STAGE = XS + (Q6 ? 0 : KQ_BM * 32);
+    static constexpr int NA = KQ_BM * 256 / 1024;                    // activation DMA instructions (4 rows each)
+    static constexpr int NW = (KQ_BN * PR + 63) / 64;                // weight DMA instructions (64 pieces each)
+    static_assert(NA % KQ_WAVES == 0, "whole activation instructions a wave");
+    static_assert(2 * STAGE <= 160 * 1024, "two stages fit the LDS");
+};
+
+// XCD-aware tile order: block b runs tile (b % 8) (T / 8) + b / 8 (tiles numbered M-fastest), so XCD x (blocks go to
+// the eight XCDs round-robin) works through a contiguous range of weight tiles against every activation panel.
+// Identity when T is not a multiple of eight.
+__device__ __forceinline__ void kq_tile(int nt, int mt, int& tm, int& tn) {
+    const int T = nt * mt, b = blockIdx.x;
+    const int t = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);
+    tn = t / mt;
+    tm = t - tn * mt;
+}
+
+template <uint32_t TY>
+__global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
+                                                                 const int8_t* __restrict__ xq, const _Float16* __restrict__ xa,
+                                                                 const float* __restrict__ xd32, const float* __restrict__ bias,
+                                                                 const float* __restrict__ res, float* __restrict__ y, int M, int N, int K) {
+    using G = KqGeo<TY>;
+    __shared__ __align__(16) uint8_t buf0[G::STAGE];
+    __shared__ __align__(16) uint8_t buf1[G::STAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = lane >> 5, r32 = lane & 31;
+    int tm, tn;
+    kq_tile((N + KQ_BN - 1) / KQ_BN, (M + KQ_BM - 1) / KQ_BM, tm, tn);
+    const int m0 = tm * KQ_BM, n0 = tn * KQ_BN;
+    const int kg = K >> 5;
+    const int nsb = K >> 8;
+
+    const kf_arsrc_t rw = kf_arsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
+    const kf_arsrc_t rx = kf_arsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
+    const kf_arsrc_t rs = kf_arsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(M - m0) * nsb * 32);
+    const kf_arsrc_t rd = kf_arsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    // activation instruction i (rows 4 i..) is wave i % 8's: lane l takes chunk (l % 16) ^ (row % 16) of row
+    // 4 i + l / 16 and writes it at position l % 16, so the MFMA operand reads below hit distinct banks
+    int va[G::NA / KQ_WAVES];
+#pragma unroll
+    for (int k = 0; k < G::NA / KQ_WAVES; k++) {
+        const int row = 4 * (wave + KQ_WAVES * k) + (lane >> 4);
+        va[k] = row * K + 16 * ((lane & 15) ^ (row & 15));
+    }
+    // weight piece q = 64 i + l of a stage: row q / PR, piece q % PR
+    auto wpiece = [&](int i) __attribute__((always_inline)) {
+        const int q = min(64 * i + lane, KQ_BN * G::PR - 1), row = q / G::PR;
+        return row * (int)row_bytes + 16 * (q - G::PR * row);
+    };
+    auto dma = [&](uint8_t* buf, int sb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < G::NA / KQ_WAVES; k++) kf_adma16(rx, va[k], sb * 256, buf + G::A + (wave + KQ_WAVES * k) * 1024);
+        const int wo = G::Q6 ? (sb * G::SBB) & ~15 : sb * G::SBB;
+#pragma unroll
+        for (int k = 0; k < (G::NW + KQ_WAVES - 1) / KQ_WAVES; k++) {
+            const int i = wave + KQ_WAVES * k;
+            if (i < G::NW) kf_adma16(rw, wpiece(i), wo, buf + G::W + i * 1024);
+        }
+        if (wave == 0) kf_adma4(rd, lane * kg * 4, sb * 32, buf + G::DX);
+        if (!G::Q6 && (wave == 1 || wave == 2))
+            kf_adma16(rs, ((wave - 1) * 32 + (lane >> 1)) * nsb * 32 + (lane & 1) * 16, sb * 32, buf + G::XS + (wave - 1) * 1024);
+    };
+
+    v16f acc[KQ_TM];
+#pragma unroll
+    for (int i = 0; i < KQ_TM; i++) acc[i] = v16f{};
+    const int wcol = (wave * 32 + r32) * G::WROW;  // the wave's weight row (tile column) for this lane
+    const int sw = r32 & 15;
+
+    // group g's activation operand of tile i: chunk 2 g + half of the lane's row, stored at (2 g + half) ^ (row % 16)
+    auto aop = [&](const uint8_t* cur, int g, int i) __attribute__((always_inline)) {
+        return *reinterpret_cast<const v4i*>(cur + G::A + (i * 32 + r32) * 256 + 16 * ((2 * g + half) ^ sw));
+    };
+
+    auto stage = [&](const uint8_t* cur, int sb) __attribute__((always_inline)) {
+        v16i S[KQ_TM];
+#pragma unroll
+        for (int i = 0; i < KQ_TM; i++) S[i] = v16i{};
+        float d, dm = 0.0f;
+        v8h mo;
+        if constexpr (!G::Q6) {
+            // q5_K: d, dmin, 12 bytes of 6-bit scales / mins, qh[32], qs[128]; the lane's 16 columns of group g are
+            // bytes 16 half.. of qs[32 (g / 2)..] (low nibbles: g even) with bit g of qh[16 half..]
+            const uint8_t* wr = cur + G::W + wcol;
+            const uint4 hd = *reinterpret_cast<const uint4*>(wr);
+            const uint4 qh = *reinterpret_cast<const uint4*>(wr + 16 + 16 * half);
+            const uint32_t qhv[4] = {qh.x, qh.y, qh.z, qh.w};
+            const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const uint4 raw = *reinterpret_cast<const uint4*>(wr + 48 + 32 * p + 16 * half);
+                const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
+                uint32_t sc2, m2;
+                kf_q4k_scales(hd.y, hd.z, hd.w, p, sc2, m2);
+                mo[2 * p] = (_Float16)(float)((half ? 1u : 64u) * (m2 & 0xffu));
+                mo[2 * p + 1] = (_Float16)(float)((half ? 1u : 64u) * (m2 >> 8));
+#pragma unroll
+                for (int gg = 0; gg < 2; gg++) {
+                    const int g = 2 * p + gg;
+                    v4i b;
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        b[e] = (int)(((gg ? v[e] >> 4 : v[e]) & m4) | (((qhv[e] >> g) & m1) << 4));  // 0..31
+                    const int sc = (int)(gg ? sc2 >> 8 : sc2 & 0xffu);
+#pragma unroll
+                    for (int i = 0; i < KQ_TM; i++) {
+                        const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop(cur, g, i), b, v16i{}, 0, 0, 0);
+#pragma unroll
+                        for (int r = 0; r < 16; r++) S[i][r] += __mul24(sc, I[r]);  // |sc I| < 2^22
+                    }
+                    // keep the groups apart: the running sums are materialized here (left free, the compiler
+                    // reassociates the integer adds across groups and holds every product), and no later group's
+                    // MFMAs are hoisted above this one's multiply-adds (16 registers per MFMA in flight)
+#pragma unroll
+                    for (int i = 0; i < KQ_TM; i++) __asm__ volatile("" : "+v"(S[i]));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            d = kf_h2f(hd.x & 0xffffu);
+            dm = kf_h2f(hd.x >> 16);
+        } else {
+            // q6_K: ql[128], qh[64], int8 scales[16], d; the super-block starts at the window's shift (sb * 210) % 16,
+            // 2-byte aligned. Group g = 4 h + gg (columns 128 h + 32 gg..): the lane's 16 columns l = 16 half.. take
+            // the low (gg < 2) or high nibbles of ql[64 h + 32 (gg % 2) + l] and bits 2 gg.. of qh[32 h + l]; scales
+            // 8 h + 2 gg (columns 0-15 of the group) and 8 h + 2 gg + 1 (16-31)
+            const uint8_t* wr = cur + G::W + wcol + ((sb * G::SBB) & 15);
+            const u32x4_a2 scv = *reinterpret_cast<const u32x4_a2*>(wr + 192);
+            const uint32_t scw[4] = {scv.x, scv.y, scv.z, scv.w};
+            const uint32_t m4 = 0x0f0f0f0fu, m3 = 0x03030303u, hb = 0x80808080u, k32 = 0x20202020u;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const u32x4_a2 la = *reinterpret_cast<const u32x4_a2*>(wr + 64 * h + 16 * half);
+                const u32x4_a2 lb = *reinterpret_cast<const u32x4_a2*>(wr + 64 * h + 32 + 16 * half);
+                const u32x4_a2 qq = *reinterpret_cast<const u32x4_a2*>(wr + 128 + 32 * h + 16 * half);
+#pragma unroll
+                for (int gg = 0; gg < 4; gg++) {
+                    const u32x4_a2 src = (gg & 1) ? lb : la;
+                    v4i bw;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const uint32_t lo = (gg >> 1) ? (src[e] >> 4) & m4 : src[e] & m4;
+                        const uint32_t v = lo | (((qq[e] >> (2 * gg)) & m3) << 4);  // q in [0, 63] per byte
+                        bw[e] = (int)(((v | hb) - k32) ^ hb);                         // q - 32 per byte, no borrows
+                    }
+                    const v4i b0 = half ? v4i{} : bw, b1 = half ? bw : v4i{};  // columns 0-15, then 16-31
+                    const int si = 8 * h + 2 * gg;
+                    const int s0 = (int)(int8_t)(uint8_t)(scw[si >> 2] >> (8 * (si & 3)));
+                    const int s1 = (int)(int8_t)(uint8_t)(scw[(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
+#pragma unroll
+                    for (int i = 0; i < KQ_TM; i++) {
+                        const v4i a = aop(cur, 4 * h + gg, i);
+                        const v16i I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, v16i{}, 0, 0, 0);
+                        const v16i I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, v16i{}, 0, 0, 0);
+                        // |dot| <= 16 * 128 * 32 and |sc| <= 128: the 24-bit products are exact
+#pragma unroll
+                        for (int r = 0; r < 16; r++) S[i][r] += __mul24(s0, I0[r]) + __mul24(s1, I1[r]);
+                    }
+#pragma unroll
+                    for (int i = 0; i < KQ_TM; i++) __asm__ volatile("" : "+v"(S[i]));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            d = kf_h2f(*reinterpret_cast<const uint16_t*>(wr + 208));
+        }
+        // acc += dx (d S - dmin mins); accumulator register r holds row (r % 4) + 8 (r / 4) + 4 (lane / 32)
+#pragma unroll
+        for (int i = 0; i < KQ_TM; i++) {
+            v16f mins = v16f{};
+            if constexpr (!G::Q6) {
+                const v8h xo = *reinterpret_cast<const v8h*>(cur + G::XS + (i * 32 + r32) * 32 + half * 16);
+                mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xo, mo, v16f{}, 0, 0, 0);
+            }
+            const float* dxp = reinterpret_cast<const float*>(cur + G::DX) + i * 32 + half * 4;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const v4f dx = *reinterpret_cast<const v4f*>(dxp + 8 * q);
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const int r = 4 * q + e;
+                    const float t = G::Q6 ? d * (float)S[i][r] : fmaf(-dm, mins[r], d * (float)S[i][r]);
+                    acc[i][r] = fmaf(t, dx[e], acc[i][r]);
+                }
+            }
+        }
+    };
+
+    // stage sb multiplies one buffer while sb + 1 lands in the other; every DMA wait is explicit
+    dma(buf0, 0);
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+    __syncthreads();
+#pragma unroll 1
+    for (int sb = 0; sb < nsb; sb += 2) {
+        if (sb + 1 < nsb) dma(buf1, sb + 1);
+        stage(buf0, sb);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        if (sb + 1 < nsb) {
+            if (sb + 2 < nsb) dma(buf0, sb + 2);
+            stage(buf1, sb + 1);
+            __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+            __syncthreads();
+        }
+    }
+
+    const int n = n0 + wave * 32 + r32;
+    if (n < N) {
+        const float bn = bias ? bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = m0 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
+                if (m >= M) continue;
+                const int64_t o = (int64_t)m * N + n;
+                y[o] = acc[i][r] + bn + (res ? res[o] : 0.0f);
+            }
+    }
+}
+
+}  // namespace
+
+// Whether the q5_K / q6_K GEMM takes these weights: K a multiple of 256 with 16-byte aligned rows (q5_K: always, 176-byte
+// super-blocks), q6_K rows that start 16-byte aligned (210-byte super-blocks: K a multiple of 2048), matrices below
+// 2 GB (row offsets travel as 32-bit values)
+bool kf_gemm_kq_ok(uint32_t ty, const void* w, int64_t row_bytes, int K, int N) {
+    if (K % 256 != 0 || (int64_t)N * row_bytes >= (1ll << 31) || (reinterpret_cast<uintptr_t>(w) & 15) != 0) return false;
+    if (ty == KF_TYPE_Q5_K) return row_bytes % 16 == 0;
+    if (ty == KF_TYPE_Q6_K) return row_bytes % 16 == 0;
+    return false;
+}
+
+// Host launcher, validated by the caller (kf_gemm_kq_ok; Q8K-kind activations in `act`)
+hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
+                             int M, int N, int K, hipStream_t s) {
+    const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
+    const char* base = static_cast<const char*>(act);
+    dim3 grid(((N + KQ_BN - 1) / KQ_BN) * ((M + KQ_BM - 1) / KQ_BM));
+    const auto* wb = static_cast<const uint8_t*>(w);
+    const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
+    const auto* xa = reinterpret_cast<const _Float16*>(base + o.xa);
+    const auto* xd = reinterpret_cast<const float*>(base + o.d32);
+    if (ty == KF_TYPE_Q5_K)
+        gemm_kq_kernel<KF_TYPE_Q5_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
+    else
+        gemm_kq_kernel<KF_TYPE_Q6_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
+    return hipGetLastError();
+}

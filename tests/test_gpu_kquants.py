@@ -123,3 +123,107 @@ def test_multi_row_matrix_cores(cuda, ty, rows, n, n_out):
     bound = 1e-4 + 1e-3 * np.abs(want) + 2e-6 * np.abs(want).max()
     err = np.abs(got - want)
     assert (err <= bound).all(), f"max err {err.max():.3e} at {np.unravel_index(np.argmax(err - bound), err.shape)}"
+
+
+def _gemm_bound(got, want):
+    # as test_multi_row_matrix_cores: the GPU adds an output's n / 256 super-block terms in another order than the
+    # CPU, and on random blocks its largest terms are as large as the largest outputs
+    got, want = got.astype(np.float64), want.astype(np.float64)
+    bound = 1e-4 + 1e-3 * np.abs(want) + 2e-6 * np.abs(want).max()
+    err = np.abs(got - want)
+    assert (err <= bound).all(), f"max err {err.max():.3e} at {np.unravel_index(np.argmax(err - bound), err.shape)}"
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("rows,n,n_out", [(1, 2048, 33), (64, 2048, 256), (70, 4096, 300), (130, 2048, 520),
+                                          (200, 14336, 96), (17, 6144, 257)])
+def test_gemm_tile_random_blocks(cuda, ty, rows, n, n_out):
+    """The q5_K / q6_K prefill GEMM (64 x 256 block tiles over native super-blocks): ragged row panels and column
+    tiles, one row, 14336 and 6144 columns (q6_K rows 16-byte aligned: n a multiple of 2048), random block bytes (every
+    scale, min and bit pattern), bias and residual, against the CPU backend's int8 path (the same quantized
+    activations and dot_i8 integers)."""
+    import torch
+
+    rng = np.random.default_rng(rows * 7 + n + n_out + ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    bias = rng.standard_normal(n_out).astype(np.float32)
+    res = rng.standard_normal((rows, n_out)).astype(np.float32)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(ty, _tensor(w, cuda), act, y, rows, n, n_out, bias=_tensor(bias, cuda), res=_tensor(res, cuda))
+    torch.cuda.synchronize()
+    _gemm_bound(y.cpu().numpy(), oracle.matmul_i8(ty, w, n, n_out, x, bias) + res)
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
+def test_gemm_prefill_shapes(cuda, ty, n, n_out):
+    """M = 2048 at the Llama-3-8B gate and down shapes with weights from the build's encoder: every 97th row against
+    the CPU backend's float product (rows are independent), and the whole output against the few-row matrix-core
+    product (kf_hip_gemv) within the same bar."""
+    import torch
+
+    rows = 2048
+    w = kf.quantize(ty, kf.synth_normal(3, 0.02, n * n_out).reshape(n_out, n))
+    x = kf.synth_normal(4, 1.0, rows * n).reshape(rows, n)
+    wt = _tensor(w, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(ty, wt, act, y, rows, n, n_out)
+    y2 = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemv(ty, wt, act, y2, rows, n, n_out)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    sample = np.arange(0, rows, 97)
+    _close(got[sample], oracle.matmul_slice(ty, w, n, n_out, x[sample], None))
+    _close(got, y2.cpu().numpy())
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+def test_gemm_shapes_it_declines(cuda, ty):
+    """2304 columns: q6_K's 210-byte super-block rows are then not 16-byte aligned, so kf_hip_gemm_i8 refuses
+    (KF_E_UNSUPPORTED) and kf_hip_matmul takes the few-row product; q5_K's 176-byte rows stay aligned and the GEMM takes
+    them. Against the CPU backend's int8 path either way."""
+    import torch
+
+    n, n_out, rows = 2304, 40, 128
+    rng = np.random.default_rng(ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    if ty == kf.TYPE_Q6_K:
+        with pytest.raises(kf.KfError):
+            kf.gemm_i8(ty, _tensor(w, cuda), act, y, rows, n, n_out)
+    kf.matmul(ty, _tensor(w, cuda), _tensor(x, cuda), act, y, n_out)
+    torch.cuda.synchronize()
+    _gemm_bound(y.cpu().numpy(), oracle.matmul_i8(ty, w, n, n_out, x, None))
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("rows", [63, 97, 256])
+def test_matmul_picks_gemm_by_cost(cuda, ty, rows):
+    """kf_hip_matmul around its few-row / tile GEMM switch at the gate shape (4096 -> 14336: the few-row product below
+    about 96 rows, the GEMM above; KF_KQ_GEMM forces each) gives the same outputs from both products, within the bar."""
+    import torch
+
+    n, n_out = 4096, 14336
+    rng = np.random.default_rng(rows + ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    wt, xt = _tensor(w, cuda), _tensor(x, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.matmul(ty, wt, xt, act, y, n_out)
+    y2 = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemv(ty, wt, act, y2, rows, n, n_out)
+    y3 = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(ty, wt, act, y3, rows, n, n_out)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    _gemm_bound(got, y2.cpu().numpy())
+    _gemm_bound(got, y3.cpu().numpy())

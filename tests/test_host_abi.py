@@ -152,10 +152,11 @@ def test_quantize_q5_k_and_q6_k_round_trip():
     assert rel[kf.TYPE_Q6_K] < rel[kf.TYPE_Q5_K] < np.sqrt(((q4 - x) ** 2).mean() / (x ** 2).mean())
 
 
-def test_k_quant_types_take_the_k_product_and_reject_the_gemm():
+def test_k_quant_types_take_the_k_product_and_the_gemm_where_aligned():
     L = kf.lib()
     assert kf.act_kind(kf.TYPE_Q5_K) == kf.ACT_Q8K and kf.act_kind(kf.TYPE_Q6_K) == kf.ACT_Q8K
-    rc = L.kf_hip_gemm_i8(kf.TYPE_Q6_K, FAKE, kf.row_bytes(14, 4096), FAKE, None, None, FAKE, 64, 4096, 16, None)
+    # the q6_K GEMM needs rows that start 16-byte aligned (2304 columns: 9 x 210 bytes a row)
+    rc = L.kf_hip_gemm_i8(kf.TYPE_Q6_K, FAKE, kf.row_bytes(14, 2304), FAKE, None, None, FAKE, 64, 2304, 16, None)
     assert rc == kf.KF_E_UNSUPPORTED and "kf_hip_gemv" in kf.last_error()
     rc = L.kf_hip_moe_gemv(kf.TYPE_Q5_K, FAKE, None, kf.row_bytes(13, 4096) * 16, kf.row_bytes(13, 4096), FAKE, 1, 4096, 16,
                            FAKE, FAKE, 1, 1, 0, FAKE, None)
