@@ -148,6 +148,13 @@ def gemm_q4_k_section(dev):
     return gemm_section(dev, ty=kf.TYPE_Q4_K)
 
 
+def gemm_k_quants_section(dev):
+    """The q5_K and q6_K prefill GEMM (SURVEY's second "next" row) at the configs[3] shapes, M = 2048."""
+    import kungfu_amd as kf
+
+    return {"q5_K": gemm_section(dev, ty=kf.TYPE_Q5_K), "q6_K": gemm_section(dev, ty=kf.TYPE_Q6_K)}
+
+
 def small_batch_section(dev):
     """batch 8..64 of the Llama-3-8B shapes with Q8_0 weights: the product kernel alone on resident
     quantized activations (µs per call, weight-streaming GB/s, TOPS) and the whole kf_hip_matmul (quant_act + product)."""
@@ -468,7 +475,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "small", "small_q4_k", "moe", "moe_prefill", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
+    ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "gemm_kq", "small", "small_q4_k", "moe", "moe_prefill", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the path shards along n_out across GPUs, "
@@ -482,7 +489,7 @@ def main():
     dev = torch.device("cuda:0")
     kf.lib()
     if args.only:
-        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "small": small_batch_section, "small_q4_k": small_batch_q4_k_section, "moe": moe_section, "moe_prefill": moe_prefill_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
+        sec = {"gemm": gemm_section, "gemm_q4_k": gemm_q4_k_section, "gemm_kq": gemm_k_quants_section, "small": small_batch_section, "small_q4_k": small_batch_q4_k_section, "moe": moe_section, "moe_prefill": moe_prefill_section, "fused": fused_section, "kquant": kquant_section, "group": group_section, "traffic": traffic_section}[args.only]
         print(json.dumps(sec(dev)), flush=True)
         return
     layer_w_bytes = sum(kf.row_bytes(kf.TYPE_Q4_K, n) * no for _, n, no in LAYER)
@@ -556,6 +563,7 @@ def main():
     out["int8_gemm"] = gemm_section(dev)
     out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
     out["int8_gemm_q4_k"] = gemm_q4_k_section(dev)
+    out["int8_gemm_k_quants"] = gemm_k_quants_section(dev)
     out["small_batch_q8_0"] = small_batch_section(dev)
     out["small_batch_q4_k"] = small_batch_q4_k_section(dev)
     out["moe_q4_k"] = moe_section(dev)

@@ -247,6 +247,10 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
     const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
     if (rc != KF_OK) return rc;
     if (ty == KF_TYPE_Q4_K) {
+        if (getenv("KF_Q4K_KQ") && kf_gemm_kq_ok(ty, w, row_bytes, n, n_out)) {  // a comparison knob
+            const hipError_t e = kf_launch_gemm_kq(ty, w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
+            return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
+        }
         const hipError_t e = kf_launch_gemm_q4k(w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
         return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
     }

@@ -42,9 +42,10 @@ constexpr int KQ_BN = 32 * KQ_WAVES;           // 256: one 32-column tile per wa
 
 template <uint32_t TY>
 struct KqGeo {
-    static constexpr bool Q6 = TY == KF_TYPE_Q6_K;
-    static constexpr int SBB = Q6 ? KF_Q6_K_BYTES : KF_Q5_K_BYTES;  // bytes of a super-block
-    static constexpr int WROW = Q6 ? 224 : KF_Q5_K_BYTES;            // LDS bytes of a weight row's super-block
+    static constexpr bool Q6 = TY == KF_TYPE_Q6_K, Q4 = TY == KF_TYPE_Q4_K;
+    static constexpr int SBB = Q6 ? KF_Q6_K_BYTES : Q4 ? KF_Q4_K_BYTES : KF_Q5_K_BYTES;  // bytes of a super-block
+    static constexpr int WROW = Q6 ? 224 : SBB;                      // LDS bytes of a weight row's super-block
+    static constexpr int QS = Q4 ? 16 : 48;                          // q4_K / q5_K: the nibbles' offset
     static constexpr int PR = WROW / 16;                             // its 16-byte pieces
     static constexpr int A = 0;                                      // activations [row 64][256]
     static constexpr int W = A + KQ_BM * 256;                        // weights [row 256][WROW]
@@ -137,12 +138,12 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
             // bytes 16 half.. of qs[32 (g / 2)..] (low nibbles: g even) with bit g of qh[16 half..]
             const uint8_t* wr = cur + G::W + wcol;
             const uint4 hd = *reinterpret_cast<const uint4*>(wr);
-            const uint4 qh = *reinterpret_cast<const uint4*>(wr + 16 + 16 * half);
+            const uint4 qh = G::Q4 ? make_uint4(0u, 0u, 0u, 0u) : *reinterpret_cast<const uint4*>(wr + 16 + 16 * half);
             const uint32_t qhv[4] = {qh.x, qh.y, qh.z, qh.w};
             const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
 #pragma unroll
             for (int p = 0; p < 4; p++) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(wr + 48 + 32 * p + 16 * half);
+                const uint4 raw = *reinterpret_cast<const uint4*>(wr + G::QS + 32 * p + 16 * half);
                 const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
                 uint32_t sc2, m2;
                 kf_q4k_scales(hd.y, hd.z, hd.w, p, sc2, m2);
@@ -278,7 +279,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
 // 2 GB (row offsets travel as 32-bit values)
 bool kf_gemm_kq_ok(uint32_t ty, const void* w, int64_t row_bytes, int K, int N) {
     if (K % 256 != 0 || (int64_t)N * row_bytes >= (1ll << 31) || (reinterpret_cast<uintptr_t>(w) & 15) != 0) return false;
-    if (ty == KF_TYPE_Q5_K) return row_bytes % 16 == 0;
+    if (ty == KF_TYPE_Q4_K || ty == KF_TYPE_Q5_K) return row_bytes % 16 == 0;
     if (ty == KF_TYPE_Q6_K) return row_bytes % 16 == 0;
     return false;
 }
@@ -293,7 +294,9 @@ hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, cons
     const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
     const auto* xa = reinterpret_cast<const _Float16*>(base + o.xa);
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
-    if (ty == KF_TYPE_Q5_K)
+    if (ty == KF_TYPE_Q4_K)
+        gemm_kq_kernel<KF_TYPE_Q4_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
+    else if (ty == KF_TYPE_Q5_K)
         gemm_kq_kernel<KF_TYPE_Q5_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
     else
         gemm_kq_kernel<KF_TYPE_Q6_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
