@@ -290,7 +290,8 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
 // q4_K: whether the tile GEMM beats the few-row product. The few-row product streams the weights once per 16
 // activation rows: about 0.28 us per MB and pass plus 1 us. A GEMM block computes a 128 x 256 tile over all of K, about
 // 24 us per 1024 columns (measured at M = 2048: 333 us for 3.5 rounds of 16 super-blocks), and its grid runs in rounds of
-// one block a CU. The few-row constants were fitted at the Llama shapes, 8-256 rows.
+// one block a CU; a last round at most half full runs its tiles as two K halves, a round of half the length (so a grid
+// below half the CUs costs half a round). The few-row constants were fitted at the Llama shapes, 8-256 rows.
 // Rows wider than the few-row product stages go one GEMV launch per row, so the GEMM takes them from 96 rows.
 static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
     if (rows < 64) return false;
@@ -299,7 +300,9 @@ static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
     const double mb = (double)n_out * row_bytes / 1e6;
     const double t_rows = ((rows + 15) / 16) * (0.28 * mb + 1.0);
     const int64_t blocks = (int64_t)((n_out + 255) / 256) * ((rows + 127) / 128);
-    const double t_gemm = 24.0 * n_in / 1024.0 * (double)((blocks + cus - 1) / cus);
+    const int64_t rem = blocks % cus;
+    const double rounds = (double)(blocks / cus) + (rem == 0 ? 0.0 : rem <= cus / 2 && n_in >= 1024 ? 0.5 : 1.0);
+    const double t_gemm = 24.0 * n_in / 1024.0 * rounds;
     return t_gemm < t_rows;
 }
 

@@ -61,15 +61,24 @@ __device__ __forceinline__ uint32_t g4_pmul(uint32_t x, uint32_t s) {
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// XCD-aware tile order: block b runs tile (b % 8) (T / 8) + b / 8 (tiles numbered M-fastest), so XCD x (blocks go to
-// the eight XCDs round-robin) works through a contiguous range of weight tiles against every activation panel.
-// Identity when T is not a multiple of eight.
-__device__ __forceinline__ void g4_tile(int nt, int mt, int& tm, int& tn) {
-    const int T = nt * mt, b = blockIdx.x;
+// XCD-aware tile order over the first T tiles: block b < T runs tile (b % 8) (T / 8) + b / 8 (tiles numbered
+// M-fastest), so XCD x (blocks go to the eight XCDs round-robin) works through a contiguous range of weight tiles
+// against every activation panel. Identity when T is not a multiple of eight.
+__device__ __forceinline__ void g4_tile(int T, int mt, int b, int& tm, int& tn) {
     const int t = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);
     tn = t / mt;
     tm = t - tn * mt;
 }
+
+// The grid's tail: when the tiles leave a last round of blocks at most half full (tiles % CUs <= CUs / 2), the tiles
+// from `full` on run as two blocks each, over the two halves of K. Each half writes its 128 x 256 partial tile to
+// `part` ([tail tile][half][register][thread]); the second to arrive (a ticket per tail tile) adds the other's, in
+// half order, and stores the tile. part == nullptr: no split.
+struct G4Tail {
+    float* part;
+    int* tickets;
+    int full;
+};
 
 #ifndef G4_PRIO
 #define G4_PRIO 1
@@ -115,18 +124,32 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
                                                                   const int8_t* __restrict__ xq, const _Float16* __restrict__ xa,
                                                                   const float* __restrict__ xd32, const float* __restrict__ bias,
                                                                   const float* __restrict__ res, float* __restrict__ y, int M, int N,
-                                                                  int K, G4Moe moe) {
+                                                                  int K, G4Moe moe, G4Tail tail) {
     __shared__ __align__(16) uint8_t buf0[G4_STAGE];
     __shared__ __align__(16) uint8_t buf1[G4_STAGE];
     __shared__ __align__(16) uint8_t recs[3 * G4_REC];  // records of super-blocks sb % 3
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int half = lane >> 5, r32 = lane & 31;
-    int tm, tn;
-    g4_tile((N + G4_BN - 1) / G4_BN, (M + G4_BM - 1) / G4_BM, tm, tn);
-    int m0 = tm * G4_BM, n0 = tn * G4_BN;
+    __shared__ int last;
+    const int mt = (M + G4_BM - 1) / G4_BM;
     const int kg = K >> 5;
     const int nsb = K >> 8;
+    int tm, tn;
+    int s0 = 0, s1 = nsb, half_k = -1, tt = 0;  // super-blocks [s0, s1); a tail block's half and tail tile
+    if (!MOE && tail.part && (int)blockIdx.x >= tail.full) {
+        const int b = blockIdx.x - tail.full;
+        tt = b >> 1;
+        half_k = b & 1;
+        const int t = tail.full + tt;
+        tn = t / mt;
+        tm = t - tn * mt;
+        s0 = half_k ? nsb / 2 : 0;
+        s1 = half_k ? nsb : nsb / 2;
+    } else {
+        g4_tile(tail.part ? tail.full : ((N + G4_BN - 1) / G4_BN) * mt, mt, blockIdx.x, tm, tn);
+    }
+    int m0 = tm * G4_BM, n0 = tn * G4_BN;
     int m_end = M;  // rows of the block's slot end here
     const uint8_t* wt = w + (int64_t)n0 * row_bytes;
     int n_end = N;  // columns of the block's matrix end here (as output columns)
@@ -296,8 +319,8 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
     uint4 hprev = make_uint4(0u, 0u, 0u, 0u);  // late waves: the header of the previous super-block
     auto stage = [&](auto latec, const uint8_t* cur, uint8_t* nxt, int sb) __attribute__((always_inline)) {
         constexpr bool LATE = decltype(latec)::value;
-        if (sb + 1 < nsb && !(G4_ABL & 1)) dma(nxt, sb + 1);
-        if (LATE && sb > 0) rescale2(hprev, record(sb - 1));
+        if (sb + 1 < s1 && !(G4_ABL & 1)) dma(nxt, sb + 1);
+        if (LATE && sb > s0) rescale2(hprev, record(sb - 1));
         __builtin_amdgcn_sched_barrier(0);
         // the MFMA phase at raised issue priority: a SIMD's other wave, in its rescale, fills the issue slots the MFMAs
         // leave
@@ -315,14 +338,14 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
     };
     auto kloop = [&](auto latec) __attribute__((always_inline)) {
 #pragma unroll 1
-        for (int sb = 0; sb < nsb; sb += 2) {
+        for (int sb = s0; sb < s1; sb += 2) {
             stage(latec, buf0, buf1, sb);
-            if (sb + 1 < nsb) stage(latec, buf1, buf0, sb + 1);
+            if (sb + 1 < s1) stage(latec, buf1, buf0, sb + 1);
         }
-        if (decltype(latec)::value) rescale2(hprev, record(nsb - 1));
+        if (decltype(latec)::value) rescale2(hprev, record(s1 - 1));
     };
 
-    dma(buf0, 0);
+    dma(buf0, s0);
     if (G4_ABL & 1) dma(buf1, 0);
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
     __syncthreads();
@@ -331,6 +354,30 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
     else
         kloop(std::false_type{});
 
+
+    if (half_k >= 0) {
+        // a tail half: its partial tile through system-scope stores (they write through to memory, so the other
+        // half's block sees them from any XCD without an L2 write-back), a ticket, and the second to arrive adds
+        float* pp = tail.part + (size_t)(2 * tt + half_k) * G4_TM * 16 * G4_THREADS + tid;
+#pragma unroll
+        for (int i = 0; i < G4_TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) __hip_atomic_store(pp + (i * 16 + r) * G4_THREADS, acc[i][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        if (tid == 0) last = __hip_atomic_fetch_add(&tail.tickets[tt], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 1;
+        __syncthreads();
+        if (!last) return;
+        const float* po = tail.part + (size_t)(2 * tt + (half_k ^ 1)) * G4_TM * 16 * G4_THREADS + tid;
+        float other[G4_TM * 16];
+#pragma unroll
+        for (int k = 0; k < G4_TM * 16; k++) other[k] = __hip_atomic_load(po + k * G4_THREADS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+        for (int i = 0; i < G4_TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][r] = half_k ? other[i * 16 + r] + acc[i][r] : acc[i][r] + other[i * 16 + r];
+        if (tid == 0) __hip_atomic_store(&tail.tickets[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
 
     const int n = n0 + wave * 32 + r32;
     if (n < N) {
@@ -362,10 +409,23 @@ hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act,
                               int N, int K, hipStream_t s) {
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
     const char* base = static_cast<const char*>(act);
-    dim3 grid(((N + G4_BN - 1) / G4_BN) * ((M + G4_BM - 1) / G4_BM));
-    gemm_q4k_kernel<false><<<grid, G4_THREADS, 0, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
-                                                        reinterpret_cast<const _Float16*>(base + o.xa),
-                                                        reinterpret_cast<const float*>(base + o.d32), bias, res, y, M, N, K, G4Moe{});
+    const int T = ((N + G4_BN - 1) / G4_BN) * ((M + G4_BM - 1) / G4_BM);
+    // the tail split (one block a CU): a last round at most half full runs its tiles as K halves in one round of
+    // half the length; it needs the split scratch (KF_GEMM_NO_TAIL turns it off, a comparison knob)
+    G4Tail tail{nullptr, nullptr, T};
+    int blocks = T;
+    const int cus = kf_cu_count(), rem = T % cus;
+    const size_t part_bytes = (size_t)rem * 2 * G4_TM * 16 * G4_THREADS * 4;
+    if (rem > 0 && rem <= cus / 2 && K / 256 >= 4 && rem <= KF_SPLIT_TICKETS &&
+        part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !getenv("KF_GEMM_NO_TAIL")) {
+        if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
+            tail = G4Tail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), T - rem};
+            blocks = T + rem;
+        }
+    }
+    gemm_q4k_kernel<false><<<blocks, G4_THREADS, 0, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
+                                                          reinterpret_cast<const _Float16*>(base + o.xa),
+                                                          reinterpret_cast<const float*>(base + o.d32), bias, res, y, M, N, K, G4Moe{}, tail);
     return hipGetLastError();
 }
 
@@ -384,6 +444,6 @@ hipError_t kf_launch_gemm_q4k_moe(const void* w, const void* w2, int64_t expert_
     gemm_q4k_kernel<true><<<grid, G4_THREADS, 0, s>>>(static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q),
                                                        reinterpret_cast<const _Float16*>(base + o.xa),
                                                        reinterpret_cast<const float*>(base + o.d32), nullptr, nullptr, y, mt * G4_BM, N, K,
-                                                       moe);
+                                                       moe, G4Tail{nullptr, nullptr, 0});
     return hipGetLastError();
 }

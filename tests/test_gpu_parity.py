@@ -600,3 +600,34 @@ def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
     kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt, res=rt)
     torch.cuda.synchronize()
     _close(outs[0], y.cpu().numpy())
+
+
+@pytest.mark.parametrize("rows,n,n_out", [(2048, 4096, 14336), (130, 2048, 600), (257, 1024, 300), (96, 14336, 512)])
+def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out):
+    """The q4_K GEMM's tail split: tiles of a last round at most half full (all of them when the grid is below half
+    the CUs) run as two K halves whose partial tiles the second to arrive adds in half order. Against the unsplit
+    kernel (KF_GEMM_NO_TAIL) within the f32 bar, bit-identical over two calls on one stream (the tickets return to
+    zero), and the smaller shapes against the CPU backend; odd super-block counts (1024 and 14336 columns give 4 and
+    56, 2048 gives 8) and ragged tiles."""
+    import torch
+
+    w = _weights(kf.TYPE_Q4_K, n_out, n, seed=rows + n)
+    x = kf.synth_normal(rows + 3, 1.0, rows * n).reshape(rows, n)
+    bias = kf.synth_normal(5, 1.0, n_out)
+    wt, bt = _tensor(w, cuda), _tensor(bias, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    outs = []
+    for _ in range(2):
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        kf.gemm_i8(kf.TYPE_Q4_K, wt, act, y, rows, n, n_out, bias=bt)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    monkeypatch.setenv("KF_GEMM_NO_TAIL", "1")
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q4_K, wt, act, y, rows, n, n_out, bias=bt)
+    torch.cuda.synchronize()
+    _close(outs[0], y.cpu().numpy())
+    if rows * n_out <= 300 * 600:
+        _close(outs[0], oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x, bias))
