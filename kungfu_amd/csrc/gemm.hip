@@ -460,6 +460,16 @@ __device__ __forceinline__ void gm_tile(int nt, int mt, int& tm, int& tn) {
     tm = t - tn * mt;
 }
 
+// The grid's tail (the DMA GEMM, two blocks a CU): when the tiles leave a last round of blocks at most half full, the
+// tiles from `full` on run as two blocks each over the two halves of K; each half writes its partial tile to `part`
+// ([tail tile][half][register][thread]) and the second to arrive (a ticket per tail tile) adds the other's in half
+// order and stores the tile. part == nullptr: no split.
+struct GmTail {
+    float* part;
+    int* tickets;
+    int full;
+};
+
 // ----------------------------------------------------------------------------------- q8_0 prefill GEMM, DMA staging
 // The product of gemm_q8_0_kernel (per group and 32 x 32 tile: the exact int32 dots I_g from v_mfma_i32_32x32x32_i8,
 // the outer product d_x (x) d_w of the f16 scales from one v_mfma_f32_32x32x16_f16 with a single non-zero k slot,
@@ -493,18 +503,35 @@ template <int WM, int WN, int TM, int TN>
 __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
                                                                      const int8_t* __restrict__ xq, const float* __restrict__ xd32,
                                                                      const float* __restrict__ bias, const float* __restrict__ res,
-                                                                     float* __restrict__ y, int M, int N, int K) {
+                                                                     float* __restrict__ y, int M, int N, int K, GmTail tail) {
     using C = GqCfg<WM, WN, TM, TN>;
     __shared__ __align__(16) uint8_t buf0[C::STAGE];
     __shared__ __align__(16) uint8_t buf1[C::STAGE];
+    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WN, wn = wave % WN;
-    int tm, tn;
-    gm_tile((N + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM, tm, tn);
-    const int m0 = tm * C::BM, n0 = tn * C::BN;
+    const int mt = (M + C::BM - 1) / C::BM;
     const int kg = K >> 5;
     const int nst = K / GM_BK;
+    int tm, tn;
+    int s0 = 0, s1 = nst, half_k = -1, tt = 0;  // stages [s0, s1) (even counts); a tail block's half and tail tile
+    if (tail.part && (int)blockIdx.x >= tail.full) {
+        const int b = blockIdx.x - tail.full;
+        tt = b >> 1;
+        half_k = b & 1;
+        const int t = tail.full + tt;
+        tn = t / mt;
+        tm = t - tn * mt;
+        s0 = half_k ? nst / 2 : 0;
+        s1 = half_k ? nst : nst / 2;
+    } else {
+        const int T = tail.part ? tail.full : ((N + C::BN - 1) / C::BN) * mt, b = blockIdx.x;
+        const int t = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);
+        tn = t / mt;
+        tm = t - tn * mt;
+    }
+    const int m0 = tm * C::BM, n0 = tn * C::BN;
     const int half = lane >> 5, r32 = lane & 31;
 
     // DMA sources: buffer resources over the tile's first rows; per-lane offsets fixed for the K loop, a stage adds
@@ -591,20 +618,53 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
         }
     };
 
-    dma(0, buf0);
+    dma(s0, buf0);
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
     __syncthreads();
 #pragma unroll 1
-    for (int st = 0; st < nst; st += 2) {
-        // nst is even (K % 256 == 0)
+    for (int st = s0; st < s1; st += 2) {
+        // the stage count is even (K % 256 == 0; halves: K % 512 == 0)
         dma(st + 1, buf1);
         stage(buf0, st);
         __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
         __syncthreads();
-        if (st + 2 < nst) dma(st + 2, buf0);
+        if (st + 2 < s1) dma(st + 2, buf0);
         stage(buf1, st + 1);
         __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
         __syncthreads();
+    }
+
+    if (half_k >= 0) {
+        // a tail half: its partial tile through system-scope stores (they write through to memory, so the other
+        // half's block sees them from any XCD without an L2 write-back), a ticket, and the second to arrive adds
+        constexpr int R = TM * TN * 16;
+        float* pp = tail.part + (size_t)(2 * tt + half_k) * R * C::THREADS + tid;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    __hip_atomic_store(pp + ((i * TN + j) * 16 + r) * C::THREADS, acc[i][j][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        if (tid == 0) last = __hip_atomic_fetch_add(&tail.tickets[tt], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 1;
+        __syncthreads();
+        if (!last) return;
+        const float* po = tail.part + (size_t)(2 * tt + (half_k ^ 1)) * R * C::THREADS + tid;
+        float other[R];
+#pragma unroll
+        for (int k = 0; k < R; k++) other[k] = __hip_atomic_load(po + k * C::THREADS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const float o = other[(i * TN + j) * 16 + r];
+                    acc[i][j][r] = half_k ? o + acc[i][j][r] : acc[i][j][r] + o;
+                }
+        if (tid == 0) __hip_atomic_store(&tail.tickets[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 
     // 32 x 32 accumulator layout: lane l holds column l % 32; register r holds row (r % 4) + 8 (r / 4) + 4 (l / 32)
@@ -1077,8 +1137,22 @@ template <int WM, int WN, int TM, int TN>
 hipError_t gemm_q8_0_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
                                 float* y, int M, int N, int K, hipStream_t s) {
     using C = GqCfg<WM, WN, TM, TN>;
-    dim3 grid(((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM));
-    gemm_q8_0_dma_kernel<WM, WN, TM, TN><<<grid, C::THREADS, 0, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K);
+    const int T = ((N + C::BN - 1) / C::BN) * ((M + C::BM - 1) / C::BM);
+    // the tail split: a last round (8 / (WM WN) blocks a CU) at most half full runs its tiles as K halves in one round
+    // of half the length; it needs the split scratch and K % 512 == 0 (even stage counts; KF_GEMM_NO_TAIL turns it
+    // off, a comparison knob)
+    GmTail tail{nullptr, nullptr, T};
+    int blocks = T;
+    const int slots = kf_cu_count() * (8 / (WM * WN)), rem = T % slots;
+    const size_t part_bytes = (size_t)rem * 2 * TM * TN * 16 * C::THREADS * 4;
+    if (rem > 0 && rem <= slots / 2 && K % 512 == 0 && K / GM_BK >= 4 && rem <= KF_SPLIT_TICKETS &&
+        part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !getenv("KF_GEMM_NO_TAIL")) {
+        if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
+            tail = GmTail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), T - rem};
+            blocks = T + rem;
+        }
+    }
+    gemm_q8_0_dma_kernel<WM, WN, TM, TN><<<blocks, C::THREADS, 0, s>>>(w, row_bytes, xq, xd32, bias, res, y, M, N, K, tail);
     return hipGetLastError();
 }
 

@@ -631,3 +631,32 @@ def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out):
     _close(outs[0], y.cpu().numpy())
     if rows * n_out <= 300 * 600:
         _close(outs[0], oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x, bias))
+
+
+@pytest.mark.parametrize("rows,n,n_out", [(2048, 4096, 14336), (300, 1024, 1000), (129, 14336, 600)])
+def test_gemm_q8_0_tail_halves(cuda, monkeypatch, rows, n, n_out):
+    """The q8_0 tile GEMM's tail split (two blocks a CU: a last round at most half full, or a grid below half of
+    them, runs its tiles as two K halves added in half order by the second to arrive): against the unsplit kernel
+    (KF_GEMM_NO_TAIL) within the f32 bar, bit-identical over two calls, the smaller shapes against the CPU backend."""
+    import torch
+
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n)
+    x = kf.synth_normal(rows + 7, 1.0, rows * n).reshape(rows, n)
+    bias = kf.synth_normal(6, 1.0, n_out)
+    wt, bt = _tensor(w, cuda), _tensor(bias, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8_0)
+    outs = []
+    for _ in range(2):
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    monkeypatch.setenv("KF_GEMM_NO_TAIL", "1")
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt)
+    torch.cuda.synchronize()
+    _close(outs[0], y.cpu().numpy())
+    if rows * n_out <= 300 * 1000:
+        _close(outs[0], oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias))
