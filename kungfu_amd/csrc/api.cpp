@@ -42,6 +42,7 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
 int kf_gemm_k_multiple();
 
 bool kf_gemm_kq_ok(uint32_t ty, const void* w, int64_t row_bytes, int K, int N);
+double kf_gemm_kq_sb_rounds(int M, int N, int K);
 hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                              int M, int N, int K, hipStream_t s);
 hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
@@ -307,19 +308,17 @@ static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
 }
 
 // q5_K / q6_K: whether the tile GEMM beats the few-row product. The few-row product streams the weights once per 64
-// activation rows, about 1.05 (q5_K) / 1.55 (q6_K) us per MB and pass; a GEMM block computes a 64 x 256 tile over all
-// of K, about 3.45 / 5.6 us per super-block, and its grid runs in rounds of one block a CU (MI355X, Llama-3-8B gate and
-// down shapes at 32-2048 rows: the model picks the faster product at every measured point). KF_KQ_GEMM=0 / 1 forces
-// the choice (a comparison knob).
+// activation rows, about 1.05 (q5_K) / 1.55 (q6_K) us per MB and pass; the GEMM costs about 14.5 us plus 3.23 / 5.72
+// us per super-block of its rounds (kf_gemm_kq_sb_rounds: one 64 x 256 tile a CU a round, a last round at most half
+// full split over 2 or 4 K ranges). Fitted on MI355X at the Llama-3-8B gate and down shapes, 32-512 rows: the model
+// picks the faster product at every measured point. KF_KQ_GEMM=0 / 1 forces the choice (a comparison knob).
 static bool kq_gemm_pays(uint32_t ty, int rows, int n_in, int n_out, int64_t row_bytes) {
     if (const char* e = getenv("KF_KQ_GEMM")) return atoi(e) != 0;
     if (rows < 2) return false;
     const bool q6 = ty == KF_TYPE_Q6_K;
     const double mb = (double)n_out * row_bytes / 1e6;
     const double t_rows = rows / 64.0 * mb * (q6 ? 1.55 : 1.05);
-    const int64_t blocks = (int64_t)((n_out + 255) / 256) * ((rows + 63) / 64);
-    const int cus = kf_cu_count();
-    const double t_gemm = (double)((blocks + cus - 1) / cus) * (n_in / 256) * (q6 ? 5.6 : 3.45);
+    const double t_gemm = 14.5 + kf_gemm_kq_sb_rounds(rows, n_out, n_in) * (q6 ? 5.72 : 3.23);
     return t_gemm < t_rows;
 }
 

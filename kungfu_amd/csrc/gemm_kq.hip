@@ -58,32 +58,56 @@ struct KqGeo {
     static_assert(2 * STAGE <= 160 * 1024, "two stages fit the LDS");
 };
 
-// XCD-aware tile order: block b runs tile (b % 8) (T / 8) + b / 8 (tiles numbered M-fastest), so XCD x (blocks go to
-// the eight XCDs round-robin) works through a contiguous range of weight tiles against every activation panel.
-// Identity when T is not a multiple of eight.
-__device__ __forceinline__ void kq_tile(int nt, int mt, int& tm, int& tn) {
-    const int T = nt * mt, b = blockIdx.x;
+// XCD-aware tile order over the first T tiles: block b < T runs tile (b % 8) (T / 8) + b / 8 (tiles numbered
+// M-fastest), so XCD x (blocks go to the eight XCDs round-robin) works through a contiguous range of weight tiles
+// against every activation panel. Identity when T is not a multiple of eight.
+__device__ __forceinline__ void kq_tile(int T, int mt, int b, int& tm, int& tn) {
     const int t = (T & 7) ? b : (b & 7) * (T >> 3) + (b >> 3);
     tn = t / mt;
     tm = t - tn * mt;
 }
 
+// The grid's tail: the tiles from `full` on (a last round of blocks at most half full, or a whole grid below half
+// the CUs) run as S blocks each over S consecutive ranges of K; each writes its 64 x 256 partial tile to `part`
+// ([tail tile][split][register][thread]), and the last of them to arrive (a ticket per tail tile) adds all S in split
+// order and stores the tile. part == nullptr: no split.
+struct KqTail {
+    float* part;
+    int* tickets;
+    int full, S;
+};
+
 template <uint32_t TY>
 __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
                                                                  const int8_t* __restrict__ xq, const _Float16* __restrict__ xa,
                                                                  const float* __restrict__ xd32, const float* __restrict__ bias,
-                                                                 const float* __restrict__ res, float* __restrict__ y, int M, int N, int K) {
+                                                                 const float* __restrict__ res, float* __restrict__ y, int M, int N, int K,
+                                                                 KqTail tail) {
     using G = KqGeo<TY>;
     __shared__ __align__(16) uint8_t buf0[G::STAGE];
     __shared__ __align__(16) uint8_t buf1[G::STAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int half = lane >> 5, r32 = lane & 31;
-    int tm, tn;
-    kq_tile((N + KQ_BN - 1) / KQ_BN, (M + KQ_BM - 1) / KQ_BM, tm, tn);
-    const int m0 = tm * KQ_BM, n0 = tn * KQ_BN;
+    __shared__ int last;
+    const int mt = (M + KQ_BM - 1) / KQ_BM;
     const int kg = K >> 5;
     const int nsb = K >> 8;
+    int tm, tn;
+    int s0 = 0, s1 = nsb, sp = -1, tt = 0;  // super-blocks [s0, s1); a tail block's split and tail tile
+    if (tail.part && (int)blockIdx.x >= tail.full) {
+        const int b = blockIdx.x - tail.full;
+        tt = b / tail.S;
+        sp = b - tt * tail.S;
+        const int t = tail.full + tt;
+        tn = t / mt;
+        tm = t - tn * mt;
+        s0 = nsb * sp / tail.S;
+        s1 = nsb * (sp + 1) / tail.S;
+    } else {
+        kq_tile(tail.part ? tail.full : ((N + KQ_BN - 1) / KQ_BN) * mt, mt, blockIdx.x, tm, tn);
+    }
+    const int m0 = tm * KQ_BM, n0 = tn * KQ_BN;
 
     const kf_arsrc_t rw = kf_arsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
     const kf_arsrc_t rx = kf_arsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
@@ -240,21 +264,50 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
     };
 
     // stage sb multiplies one buffer while sb + 1 lands in the other; every DMA wait is explicit
-    dma(buf0, 0);
+    dma(buf0, s0);
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
     __syncthreads();
 #pragma unroll 1
-    for (int sb = 0; sb < nsb; sb += 2) {
-        if (sb + 1 < nsb) dma(buf1, sb + 1);
+    for (int sb = s0; sb < s1; sb += 2) {
+        if (sb + 1 < s1) dma(buf1, sb + 1);
         stage(buf0, sb);
         __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
         __syncthreads();
-        if (sb + 1 < nsb) {
-            if (sb + 2 < nsb) dma(buf0, sb + 2);
+        if (sb + 1 < s1) {
+            if (sb + 2 < s1) dma(buf0, sb + 2);
             stage(buf1, sb + 1);
             __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
             __syncthreads();
         }
+    }
+
+    if (sp >= 0) {
+        // a split: its partial tile through system-scope stores (they write through to memory, so the other splits'
+        // blocks see them from any XCD without an L2 write-back), a ticket, and the last to arrive adds all S
+        constexpr int R = KQ_TM * 16;
+        float* pp = tail.part + (size_t)(tail.S * tt + sp) * R * KQ_THREADS + tid;
+#pragma unroll
+        for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) __hip_atomic_store(pp + (i * 16 + r) * KQ_THREADS, acc[i][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        if (tid == 0) last = __hip_atomic_fetch_add(&tail.tickets[tt], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == tail.S - 1;
+        __syncthreads();
+        if (!last) return;
+        const float* p0 = tail.part + (size_t)tail.S * tt * R * KQ_THREADS + tid;
+#pragma unroll
+        for (int i = 0; i < KQ_TM; i++) acc[i] = v16f{};
+        for (int k = 0; k < tail.S; k++) {
+            float part[R];
+#pragma unroll
+            for (int e = 0; e < R; e++) part[e] = __hip_atomic_load(p0 + ((size_t)k * R + e) * KQ_THREADS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+            for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][r] += part[i * 16 + r];
+        }
+        if (tid == 0) __hip_atomic_store(&tail.tickets[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 
     const int n = n0 + wave * 32 + r32;
@@ -284,21 +337,50 @@ bool kf_gemm_kq_ok(uint32_t ty, const void* w, int64_t row_bytes, int K, int N) 
     return false;
 }
 
+// The tail split of an M x N x K launch: the number of K ranges the last round's tiles run as (1: none) and the rounds'
+// length in super-blocks (full rounds of nsb, plus nsb / S for a split tail), as the launcher plans them
+static int kq_splits(int T, int nsb, int cus) {
+    const int rem = T % cus;
+    int S = 1;
+    while (S < 4 && rem * S * 2 <= cus && nsb / (S * 2) >= 2) S *= 2;
+    return S;
+}
+
+double kf_gemm_kq_sb_rounds(int M, int N, int K) {
+    const int T = ((N + KQ_BN - 1) / KQ_BN) * ((M + KQ_BM - 1) / KQ_BM), nsb = K / 256, cus = kf_cu_count();
+    const int rem = T % cus, S = kq_splits(T, nsb, cus);
+    return (double)(T / cus) * nsb + (rem == 0 ? 0.0 : (double)nsb / S);
+}
+
 // Host launcher, validated by the caller (kf_gemm_kq_ok; Q8K-kind activations in `act`)
 hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                              int M, int N, int K, hipStream_t s) {
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
     const char* base = static_cast<const char*>(act);
-    dim3 grid(((N + KQ_BN - 1) / KQ_BN) * ((M + KQ_BM - 1) / KQ_BM));
+    const int T = ((N + KQ_BN - 1) / KQ_BN) * ((M + KQ_BM - 1) / KQ_BM);
+    // the tail split (one block a CU): the tiles of a last round at most half full run as S = 2 or 4 blocks over K
+    // ranges of at least two super-blocks, S as large as the round holds (KF_GEMM_NO_TAIL turns it off, a comparison
+    // knob); it needs the split scratch
+    KqTail tail{nullptr, nullptr, T, 1};
+    int blocks = T;
+    const int cus = kf_cu_count(), rem = T % cus;
+    const int S = kq_splits(T, K / 256, cus);
+    const size_t part_bytes = (size_t)rem * S * KQ_TM * 16 * KQ_THREADS * 4;
+    if (S > 1 && rem <= KF_SPLIT_TICKETS && part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !getenv("KF_GEMM_NO_TAIL")) {
+        if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
+            tail = KqTail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), T - rem, S};
+            blocks = T - rem + rem * S;
+        }
+    }
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
     const auto* xa = reinterpret_cast<const _Float16*>(base + o.xa);
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
     if (ty == KF_TYPE_Q4_K)
-        gemm_kq_kernel<KF_TYPE_Q4_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
+        gemm_kq_kernel<KF_TYPE_Q4_K><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail);
     else if (ty == KF_TYPE_Q5_K)
-        gemm_kq_kernel<KF_TYPE_Q5_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
+        gemm_kq_kernel<KF_TYPE_Q5_K><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail);
     else
-        gemm_kq_kernel<KF_TYPE_Q6_K><<<grid, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K);
+        gemm_kq_kernel<KF_TYPE_Q6_K><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail);
     return hipGetLastError();
 }

@@ -207,8 +207,8 @@ def test_gemm_shapes_it_declines(cuda, ty):
 @pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
 @pytest.mark.parametrize("rows", [63, 97, 256])
 def test_matmul_picks_gemm_by_cost(cuda, ty, rows):
-    """kf_hip_matmul around its few-row / tile GEMM switch at the gate shape (4096 -> 14336: the few-row product below
-    about 96 rows, the GEMM above; KF_KQ_GEMM forces each) gives the same outputs from both products, within the bar."""
+    """kf_hip_matmul around its few-row / tile GEMM switch at the gate shape (4096 -> 14336: the cost model moves to
+    the GEMM at about 64 rows for q5_K and 32 for q6_K) gives the outputs of both products, within the bar."""
     import torch
 
     n, n_out = 4096, 14336
@@ -227,3 +227,34 @@ def test_matmul_picks_gemm_by_cost(cuda, ty, rows):
     got = y.cpu().numpy()
     _gemm_bound(got, y2.cpu().numpy())
     _gemm_bound(got, y3.cpu().numpy())
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q5_K, kf.TYPE_Q6_K])
+@pytest.mark.parametrize("rows,n,n_out", [(256, 14336, 4096), (100, 2048, 300), (64, 4096, 1000), (2048, 4096, 2304)])
+def test_gemm_tail_splits(cuda, monkeypatch, ty, rows, n, n_out):
+    """The q5_K / q6_K GEMM's tail split: tiles of a last round at most half full (or a grid below half the CUs) run
+    as 2 or 4 blocks over K ranges, added in split order by the last to arrive. Bit-identical over two calls, within
+    the bar of the unsplit kernel (KF_GEMM_NO_TAIL), and the smaller shapes against the CPU backend's int8 path."""
+    import torch
+
+    rng = np.random.default_rng(rows + n + ty)
+    w = _random_blocks(ty, n_out, n, rng)
+    x = rng.standard_normal((rows, n)).astype(np.float32)
+    bias = rng.standard_normal(n_out).astype(np.float32)
+    wt, bt = _tensor(w, cuda), _tensor(bias, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8K)
+    outs = []
+    for _ in range(2):
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        kf.gemm_i8(ty, wt, act, y, rows, n, n_out, bias=bt)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    monkeypatch.setenv("KF_GEMM_NO_TAIL", "1")
+    y = torch.full((rows, n_out), float("nan"), device=cuda)
+    kf.gemm_i8(ty, wt, act, y, rows, n, n_out, bias=bt)
+    torch.cuda.synchronize()
+    _gemm_bound(outs[0], y.cpu().numpy())
+    if rows * n_out <= 100000:
+        _gemm_bound(outs[0], oracle.matmul_i8(ty, w, n, n_out, x, bias))
