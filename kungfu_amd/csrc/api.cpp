@@ -5,6 +5,7 @@
 // product kernel chosen by the number of activation rows.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 
 #include <cstdarg>
@@ -43,6 +44,8 @@ int kf_gemm_k_multiple();
 
 bool kf_gemm_kq_ok(uint32_t ty, const void* w, int64_t row_bytes, int K, int N);
 double kf_gemm_kq_sb_rounds(int M, int N, int K);
+double kf_gemm_q4k_sb_rounds(int M, int N, int K);
+static bool q4k_gemm_kq_pays(int rows, int n_in, int n_out);
 hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                              int M, int N, int K, hipStream_t s);
 hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
@@ -248,7 +251,7 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
     const int rc = check_product(ty, w, row_bytes, act, y, rows, n, n_out);
     if (rc != KF_OK) return rc;
     if (ty == KF_TYPE_Q4_K) {
-        if (getenv("KF_Q4K_KQ") && kf_gemm_kq_ok(ty, w, row_bytes, n, n_out)) {  // a comparison knob
+        if (q4k_gemm_kq_pays(rows, n, n_out) && kf_gemm_kq_ok(ty, w, row_bytes, n, n_out)) {
             const hipError_t e = kf_launch_gemm_kq(ty, w, row_bytes, act, bias, res, y, rows, n_out, n, static_cast<hipStream_t>(stream));
             return e == hipSuccess ? KF_OK : hip_fail(e, "gemm launch");
         }
@@ -288,22 +291,32 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
 
 }  // extern "C"
 
+// q4_K GEMM costs (MI355X, Llama-3-8B QKV / O / gate / down shapes at 32-2048 rows, least squares over the rounds each
+// launcher plans): the split-scale kernel (gemm_q4k.hip, 128 x 256 tiles, two K halves for a half-full last round)
+// about 7.4 us plus 4.84 us per super-block of its rounds; the one-MFMA-per-group kernel (gemm_kq.hip, 64 x 256
+// tiles, 2-4 K ranges for a half-full last round) 13.2 us plus 2.95 us. The first wins where its rounds are full
+// (gate from about 384 rows, down from 768), the second on smaller grids.
+static double q4k_gemm_us(int rows, int n_in, int n_out, bool kq) {
+    return kq ? 13.2 + 2.95 * kf_gemm_kq_sb_rounds(rows, n_out, n_in) : 7.4 + 4.84 * kf_gemm_q4k_sb_rounds(rows, n_out, n_in);
+}
+
+// Which q4_K GEMM kf_hip_gemm_i8 runs: the one-MFMA-per-group kernel where it costs less (KF_Q4K_KQ=0 / 1 forces the
+// choice, a comparison knob)
+static bool q4k_gemm_kq_pays(int rows, int n_in, int n_out) {
+    if (const char* e = getenv("KF_Q4K_KQ")) return atoi(e) != 0;
+    return q4k_gemm_us(rows, n_in, n_out, true) < q4k_gemm_us(rows, n_in, n_out, false);
+}
+
 // q4_K: whether the tile GEMM beats the few-row product. The few-row product streams the weights once per 16
-// activation rows: about 0.28 us per MB and pass plus 1 us. A GEMM block computes a 128 x 256 tile over all of K, about
-// 24 us per 1024 columns (measured at M = 2048: 333 us for 3.5 rounds of 16 super-blocks), and its grid runs in rounds of
-// one block a CU; a last round at most half full runs its tiles as two K halves, a round of half the length (so a grid
-// below half the CUs costs half a round). The few-row constants were fitted at the Llama shapes, 8-256 rows.
-// Rows wider than the few-row product stages go one GEMV launch per row, so the GEMM takes them from 96 rows.
+// activation rows: about 0.28 us per MB and pass plus 1 us (fitted at the Llama shapes, 8-256 rows); the GEMM costs
+// the cheaper of the two kernels above. Rows wider than the few-row product stages go one GEMV launch per row, so the
+// GEMM takes them from 96 rows.
 static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
-    if (rows < 64) return false;
+    if (rows < 2) return false;
     if (n_in > kf_rows_max_n(KF_TYPE_Q4_K)) return rows >= 96;
-    const int cus = kf_cu_count();
     const double mb = (double)n_out * row_bytes / 1e6;
     const double t_rows = ((rows + 15) / 16) * (0.28 * mb + 1.0);
-    const int64_t blocks = (int64_t)((n_out + 255) / 256) * ((rows + 127) / 128);
-    const int64_t rem = blocks % cus;
-    const double rounds = (double)(blocks / cus) + (rem == 0 ? 0.0 : rem <= cus / 2 && n_in >= 1024 ? 0.5 : 1.0);
-    const double t_gemm = 24.0 * n_in / 1024.0 * rounds;
+    const double t_gemm = std::min(q4k_gemm_us(rows, n_in, n_out, true), q4k_gemm_us(rows, n_in, n_out, false));
     return t_gemm < t_rows;
 }
 

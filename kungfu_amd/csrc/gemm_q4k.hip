@@ -124,31 +124,40 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
                                                                   const int8_t* __restrict__ xq, const _Float16* __restrict__ xa,
                                                                   const float* __restrict__ xd32, const float* __restrict__ bias,
                                                                   const float* __restrict__ res, float* __restrict__ y, int M, int N,
-                                                                  int K, G4Moe moe, G4Tail tail) {
+                                                                  int K, G4Moe moe, G4Tail tail_arg) {
+    // the grouped form never splits: its tail is a compile-time nothing there
+    const G4Tail tail = MOE ? G4Tail{nullptr, nullptr, 0} : tail_arg;
     __shared__ __align__(16) uint8_t buf0[G4_STAGE];
     __shared__ __align__(16) uint8_t buf1[G4_STAGE];
     __shared__ __align__(16) uint8_t recs[3 * G4_REC];  // records of super-blocks sb % 3
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int half = lane >> 5, r32 = lane & 31;
-    __shared__ int last;
-    const int mt = (M + G4_BM - 1) / G4_BM;
     const int kg = K >> 5;
     const int nsb = K >> 8;
-    int tm, tn;
-    int s0 = 0, s1 = nsb, half_k = -1, tt = 0;  // super-blocks [s0, s1); a tail block's half and tail tile
-    if (!MOE && tail.part && (int)blockIdx.x >= tail.full) {
-        const int b = blockIdx.x - tail.full;
-        tt = b >> 1;
-        half_k = b & 1;
-        const int t = tail.full + tt;
-        tn = t / mt;
-        tm = t - tn * mt;
-        s0 = half_k ? nsb / 2 : 0;
-        s1 = half_k ? nsb : nsb / 2;
-    } else {
-        g4_tile(tail.part ? tail.full : ((N + G4_BN - 1) / G4_BN) * mt, mt, blockIdx.x, tm, tn);
-    }
+    // the block's tile, and for a tail half its half (else -1) and tail tile; the super-blocks it runs are [s0, s1),
+    // literal bounds in the grouped instantiation (bounds derived from the tail fields left it 17 more spilled
+    // registers: the stage code's lambdas capture them by reference)
+    struct Place {
+        int tm, tn, half, tt;
+    };
+    const Place pl = [&]() {
+        Place r{0, 0, -1, 0};
+        const int mt = (M + G4_BM - 1) / G4_BM;
+        if (!MOE && tail.part && (int)blockIdx.x >= tail.full) {
+            const int b = blockIdx.x - tail.full;
+            r.tt = b >> 1;
+            r.half = b & 1;
+            const int t = tail.full + r.tt;
+            r.tn = t / mt;
+            r.tm = t - r.tn * mt;
+        } else {
+            g4_tile(tail.part ? tail.full : ((N + G4_BN - 1) / G4_BN) * mt, mt, blockIdx.x, r.tm, r.tn);
+        }
+        return r;
+    }();
+    const int tm = pl.tm, tn = pl.tn, half_k = pl.half, tt = pl.tt;
+    const int s0 = MOE ? 0 : half_k > 0 ? nsb / 2 : 0, s1 = MOE ? nsb : half_k == 0 ? nsb / 2 : nsb;
     int m0 = tm * G4_BM, n0 = tn * G4_BN;
     int m_end = M;  // rows of the block's slot end here
     const uint8_t* wt = w + (int64_t)n0 * row_bytes;
@@ -355,7 +364,8 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
         kloop(std::false_type{});
 
 
-    if (half_k >= 0) {
+    if (!MOE && half_k >= 0) {
+        __shared__ int last;
         // a tail half: its partial tile through system-scope stores (they write through to memory, so the other
         // half's block sees them from any XCD without an L2 write-back), a ticket, and the second to arrive adds
         float* pp = tail.part + (size_t)(2 * tt + half_k) * G4_TM * 16 * G4_THREADS + tid;
@@ -402,6 +412,14 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
 }
 
 }  // namespace
+
+// The rounds of an M x N x K launch in super-blocks, as the launcher plans them: one 128 x 256 tile a CU a round, a
+// last round at most half full as two K halves (half a round)
+double kf_gemm_q4k_sb_rounds(int M, int N, int K) {
+    const int T = ((N + G4_BN - 1) / G4_BN) * ((M + G4_BM - 1) / G4_BM), cus = kf_cu_count(), rem = T % cus, nsb = K / 256;
+    const double last = rem == 0 ? 0.0 : rem <= cus / 2 && nsb >= 4 ? 0.5 : 1.0;
+    return ((double)(T / cus) + last) * nsb;
+}
 
 // Host launcher of the q4_K prefill GEMM, validated by the caller (api.cpp): K a multiple of 256, Q8K-kind activations
 // in `act`

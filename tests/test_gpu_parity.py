@@ -602,14 +602,17 @@ def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
     _close(outs[0], y.cpu().numpy())
 
 
+@pytest.mark.parametrize("kq", ["0", "1"])
 @pytest.mark.parametrize("rows,n,n_out", [(2048, 4096, 14336), (130, 2048, 600), (257, 1024, 300), (96, 14336, 512)])
-def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out):
-    """The q4_K GEMM's tail split: tiles of a last round at most half full (all of them when the grid is below half
-    the CUs) run as two K halves whose partial tiles the second to arrive adds in half order. Against the unsplit
+def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out, kq):
+    """The q4_K GEMMs' tail split, both kernels (KF_Q4K_KQ: 0 the split-scale kernel, two K halves; 1 the
+    one-MFMA-per-group kernel, 2-4 K ranges): tiles of a last round at most half full (all of them when the grid is
+    below half the CUs) run over K ranges whose partial tiles the last to arrive adds in order. Against the unsplit
     kernel (KF_GEMM_NO_TAIL) within the f32 bar, bit-identical over two calls on one stream (the tickets return to
-    zero), and the smaller shapes against the CPU backend; odd super-block counts (1024 and 14336 columns give 4 and
-    56, 2048 gives 8) and ragged tiles."""
+    zero), and the smaller shapes against the CPU backend; 4, 8 and 56 super-blocks a row, ragged tiles."""
     import torch
+
+    monkeypatch.setenv("KF_Q4K_KQ", kq)
 
     w = _weights(kf.TYPE_Q4_K, n_out, n, seed=rows + n)
     x = kf.synth_normal(rows + 3, 1.0, rows * n).reshape(rows, n)
