@@ -77,12 +77,24 @@ struct KqTail {
     int full, S;
 };
 
-template <uint32_t TY>
+// The grouped (MoE) form: the activation rows are routed pairs in group order (slot s: rows offsets[s]..offsets[s + 1]),
+// slot s multiplies its own expert matrix (w + s expert_bytes; with w2, output columns from n_split on come from
+// w2 + s expert_bytes, row n - n_split), and output row p goes to y row out_rows[p] (or p). n_slots == 0: one matrix.
+struct KqMoe {
+    const int32_t* offsets;
+    const int32_t* out_rows;
+    const uint8_t* w2;
+    int64_t expert_bytes;
+    int n_slots, n_split;
+};
+
+template <uint32_t TY, bool MOE>
 __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* __restrict__ w, int64_t row_bytes,
                                                                  const int8_t* __restrict__ xq, const _Float16* __restrict__ xa,
                                                                  const float* __restrict__ xd32, const float* __restrict__ bias,
                                                                  const float* __restrict__ res, float* __restrict__ y, int M, int N, int K,
-                                                                 KqTail tail) {
+                                                                 KqTail tail_arg, KqMoe moe) {
+    const KqTail tail = MOE ? KqTail{nullptr, nullptr, 0, 1} : tail_arg;  // the grouped form never splits
     using G = KqGeo<TY>;
     __shared__ __align__(16) uint8_t buf0[G::STAGE];
     __shared__ __align__(16) uint8_t buf1[G::STAGE];
@@ -95,7 +107,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
     const int nsb = K >> 8;
     int tm, tn;
     int s0 = 0, s1 = nsb, sp = -1, tt = 0;  // super-blocks [s0, s1); a tail block's split and tail tile
-    if (tail.part && (int)blockIdx.x >= tail.full) {
+    if (!MOE && tail.part && (int)blockIdx.x >= tail.full) {
         const int b = blockIdx.x - tail.full;
         tt = b / tail.S;
         sp = b - tt * tail.S;
@@ -107,12 +119,35 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
     } else {
         kq_tile(tail.part ? tail.full : ((N + KQ_BN - 1) / KQ_BN) * mt, mt, blockIdx.x, tm, tn);
     }
-    const int m0 = tm * KQ_BM, n0 = tn * KQ_BN;
+    int m0 = tm * KQ_BM;
+    const int n0 = tn * KQ_BN;
+    int m_end = M;  // rows of the block's slot end here
+    const uint8_t* wt = w + (int64_t)n0 * row_bytes;
+    int n_end = N;  // columns of the block's matrix end here (as output columns)
+    if (MOE) {
+        // M counts the grid's row tiles over all slots (an upper bound): tile tm is the slot's tile tm - (the tiles of
+        // the slots before it); past the last slot's tiles the block has nothing to do
+        int sl = 0, t0 = 0;
+        for (; sl < moe.n_slots; sl++) {
+            const int rows = moe.offsets[sl + 1] - moe.offsets[sl], t = (rows + KQ_BM - 1) / KQ_BM;
+            if (tm < t0 + t) break;
+            t0 += t;
+        }
+        if (sl == moe.n_slots) return;  // whole block, before any barrier
+        m0 = moe.offsets[sl] + (tm - t0) * KQ_BM;
+        m_end = moe.offsets[sl + 1];
+        if (moe.w2 && n0 >= moe.n_split) {
+            wt = moe.w2 + sl * moe.expert_bytes + (int64_t)(n0 - moe.n_split) * row_bytes;
+        } else {
+            wt = w + sl * moe.expert_bytes + (int64_t)n0 * row_bytes;
+            if (moe.w2) n_end = moe.n_split;
+        }
+    }
 
-    const kf_arsrc_t rw = kf_arsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
-    const kf_arsrc_t rx = kf_arsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
-    const kf_arsrc_t rs = kf_arsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(M - m0) * nsb * 32);
-    const kf_arsrc_t rd = kf_arsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    const kf_arsrc_t rw = kf_arsrc(wt, (uint64_t)(n_end - n0) * row_bytes);
+    const kf_arsrc_t rx = kf_arsrc(xq + (int64_t)m0 * K, (uint64_t)(m_end - m0) * K);
+    const kf_arsrc_t rs = kf_arsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(m_end - m0) * nsb * 32);
+    const kf_arsrc_t rd = kf_arsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(m_end - m0) * kg * 4);
     // activation instruction i (rows 4 i..) is wave i % 8's: lane l takes chunk (l % 16) ^ (row % 16) of row
     // 4 i + l / 16 and writes it at position l % 16, so the MFMA operand reads below hit distinct banks
     int va[G::NA / KQ_WAVES];
@@ -281,7 +316,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
         }
     }
 
-    if (sp >= 0) {
+    if (!MOE && sp >= 0) {
         // a split: its partial tile through system-scope stores (they write through to memory, so the other splits'
         // blocks see them from any XCD without an L2 write-back), a ticket, and the last to arrive adds all S
         constexpr int R = KQ_TM * 16;
@@ -318,8 +353,8 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int m = m0 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
-                if (m >= M) continue;
-                const int64_t o = (int64_t)m * N + n;
+                if (m >= m_end) continue;
+                const int64_t o = (int64_t)(MOE && moe.out_rows ? moe.out_rows[m] : m) * N + n;
                 y[o] = acc[i][r] + bn + (res ? res[o] : 0.0f);
             }
     }
@@ -377,10 +412,27 @@ hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, cons
     const auto* xa = reinterpret_cast<const _Float16*>(base + o.xa);
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
     if (ty == KF_TYPE_Q4_K)
-        gemm_kq_kernel<KF_TYPE_Q4_K><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail);
+        gemm_kq_kernel<KF_TYPE_Q4_K, false><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail, KqMoe{});
     else if (ty == KF_TYPE_Q5_K)
-        gemm_kq_kernel<KF_TYPE_Q5_K><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail);
+        gemm_kq_kernel<KF_TYPE_Q5_K, false><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail, KqMoe{});
     else
-        gemm_kq_kernel<KF_TYPE_Q6_K><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail);
+        gemm_kq_kernel<KF_TYPE_Q6_K, false><<<blocks, KQ_THREADS, 0, s>>>(wb, row_bytes, xq, xa, xd, bias, res, y, M, N, K, tail, KqMoe{});
+    return hipGetLastError();
+}
+
+// Grouped (MoE) form on q4_K experts: `act` holds `pairs` activation rows in group order (slot s: rows
+// offsets[s]..offsets[s + 1], device offsets), slot s multiplies w + s expert_bytes (N output columns; with w2,
+// columns n_split.. from w2), output row p goes to y row out_rows[p] (nullable: p). Validated by the caller: K a
+// multiple of 256, n_split a multiple of 256, 16-byte aligned matrices and rows.
+hipError_t kf_launch_gemm_kq_moe(const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, int n_split, const void* act, int pairs,
+                                 int n_slots, const int32_t* offsets, const int32_t* out_rows, float* y, int N, int K, hipStream_t s) {
+    const kf_act_offsets o = kf_act_layout((size_t)pairs, (size_t)K);
+    const char* base = static_cast<const char*>(act);
+    // row tiles over all slots: each slot adds at most one partial tile
+    const int mt = (pairs + KQ_BM - 1) / KQ_BM + n_slots;
+    const KqMoe moe{offsets, out_rows, static_cast<const uint8_t*>(w2), expert_bytes, n_slots, n_split};
+    gemm_kq_kernel<KF_TYPE_Q4_K, true><<<((N + KQ_BN - 1) / KQ_BN) * mt, KQ_THREADS, 0, s>>>(
+        static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q), reinterpret_cast<const _Float16*>(base + o.xa),
+        reinterpret_cast<const float*>(base + o.d32), nullptr, nullptr, y, mt * KQ_BM, N, K, KqTail{nullptr, nullptr, 0, 1}, moe);
     return hipGetLastError();
 }
