@@ -500,10 +500,10 @@ int kf_hip_moe_gemm(uint32_t ty, const void* w, const void* w2, int64_t expert_b
         return fail(KF_E_INVALID, "split at column %d of %d (a multiple of 256 inside the output) or unaligned second matrix", n_split, n_out);
     if (expert_bytes < (int64_t)mat_rows * row_bytes || expert_bytes % 16 != 0)
         return fail(KF_E_INVALID, "expert stride %lld for %d rows of %lld bytes (16-byte multiple)", (long long)expert_bytes, mat_rows, (long long)row_bytes);
-    // KF_MOE_KQ=1 (a comparison knob): the one-MFMA-per-group kernel, 64-row tiles (less of each slot's partial tile
-    // idle); it measured the same as the split-scale kernel at 512 tokens top-2 over 8 experts (905 against 896 us)
+    // the one-MFMA-per-group kernel (64-row tiles: less of each slot's partial tile idle; 839 against 894 us for the
+    // split-scale kernel at 512 tokens top-2 over 8 experts) unless KF_MOE_KQ=0 (a comparison knob)
     const char* ke = getenv("KF_MOE_KQ");
-    const bool kq = ke && atoi(ke) != 0 && row_bytes % 16 == 0 && aligned(w, 16);
+    const bool kq = !(ke && atoi(ke) == 0) && row_bytes % 16 == 0 && aligned(w, 16);
     const hipError_t e = kq ? kf_launch_gemm_kq_moe(w, w2, expert_bytes, row_bytes, w2 ? n_split : 0, act, pairs, n_slots, offsets, out_rows, y,
                                                     n_out, n, static_cast<hipStream_t>(stream))
                             : kf_launch_gemm_q4k_moe(w, w2, expert_bytes, row_bytes, w2 ? n_split : 0, act, pairs, n_slots, offsets, out_rows, y,

@@ -200,36 +200,65 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
             const uint4 qh = G::Q4 ? make_uint4(0u, 0u, 0u, 0u) : *reinterpret_cast<const uint4*>(wr + 16 + 16 * half);
             const uint32_t qhv[4] = {qh.x, qh.y, qh.z, qh.w};
             const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
+            uint4 raw[4];
+            uint32_t sc2[4];
 #pragma unroll
             for (int p = 0; p < 4; p++) {
-                const uint4 raw = *reinterpret_cast<const uint4*>(wr + G::QS + 32 * p + 16 * half);
-                const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
-                uint32_t sc2, m2;
-                kf_q4k_scales(hd.y, hd.z, hd.w, p, sc2, m2);
+                raw[p] = *reinterpret_cast<const uint4*>(wr + G::QS + 32 * p + 16 * half);
+                uint32_t m2;
+                kf_q4k_scales(hd.y, hd.z, hd.w, p, sc2[p], m2);
                 mo[2 * p] = (_Float16)(float)((half ? 1u : 64u) * (m2 & 0xffu));
                 mo[2 * p + 1] = (_Float16)(float)((half ? 1u : 64u) * (m2 >> 8));
-#pragma unroll
-                for (int gg = 0; gg < 2; gg++) {
-                    const int g = 2 * p + gg;
-                    v4i b;
-#pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        b[e] = (int)(((gg ? v[e] >> 4 : v[e]) & m4) | (((qhv[e] >> g) & m1) << 4));  // 0..31
-                    const int sc = (int)(gg ? sc2 >> 8 : sc2 & 0xffu);
-#pragma unroll
-                    for (int i = 0; i < KQ_TM; i++) {
-                        const v16i I = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop(cur, g, i), b, v16i{}, 0, 0, 0);
-#pragma unroll
-                        for (int r = 0; r < 16; r++) S[i][r] += __mul24(sc, I[r]);  // |sc I| < 2^22
-                    }
-                    // keep the groups apart: the running sums are materialized here (left free, the compiler
-                    // reassociates the integer adds across groups and holds every product), and no later group's
-                    // MFMAs are hoisted above this one's multiply-adds (16 registers per MFMA in flight)
-#pragma unroll
-                    for (int i = 0; i < KQ_TM; i++) __asm__ volatile("" : "+v"(S[i]));
-                    __builtin_amdgcn_sched_barrier(0);
-                }
             }
+            // group g's MFMAs (operand: 0..31 per byte, the fifth bit from qh)
+            auto issue = [&](auto gc, v16i (&I)[KQ_TM]) __attribute__((always_inline)) {
+                constexpr int g = decltype(gc)::value;
+                const uint32_t v[4] = {raw[g / 2].x, raw[g / 2].y, raw[g / 2].z, raw[g / 2].w};
+                v4i b;
+#pragma unroll
+                for (int e = 0; e < 4; e++) b[e] = (int)((((g & 1) ? v[e] >> 4 : v[e]) & m4) | (((qhv[e] >> g) & m1) << 4));
+#pragma unroll
+                for (int i = 0; i < KQ_TM; i++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop(cur, g, i), b, v16i{}, 0, 0, 0);
+            };
+            // Software-pipelined by one group: group g + 1's MFMAs are issued before group g's multiply-adds, which
+            // depend on none of them, so the adds run while the matrix core works. The running sums are
+            // materialized after each group (left free, the compiler reassociates the integer adds across groups
+            // and holds every product), and the sched barriers keep the groups in this order.
+            v16i Ia[KQ_TM], Ib[KQ_TM];
+            auto mads = [&](int g, const v16i (&I)[KQ_TM]) __attribute__((always_inline)) {
+                const int sc = (int)((g & 1) ? sc2[g / 2] >> 8 : sc2[g / 2] & 0xffu);
+#pragma unroll
+                for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                    for (int r = 0; r < 16; r++) S[i][r] += __mul24(sc, I[i][r]);  // |sc I| < 2^22
+#pragma unroll
+                for (int i = 0; i < KQ_TM; i++) __asm__ volatile("" : "+v"(S[i]));
+            };
+            issue(std::integral_constant<int, 0>{}, Ia);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 1>{}, Ib);
+            mads(0, Ia);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 2>{}, Ia);
+            mads(1, Ib);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 3>{}, Ib);
+            mads(2, Ia);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 4>{}, Ia);
+            mads(3, Ib);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 5>{}, Ib);
+            mads(4, Ia);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 6>{}, Ia);
+            mads(5, Ib);
+            __builtin_amdgcn_sched_barrier(0);
+            issue(std::integral_constant<int, 7>{}, Ib);
+            mads(6, Ia);
+            __builtin_amdgcn_sched_barrier(0);
+            mads(7, Ib);
+            __builtin_amdgcn_sched_barrier(0);
             d = kf_h2f(hd.x & 0xffffu);
             dm = kf_h2f(hd.x >> 16);
         } else {
