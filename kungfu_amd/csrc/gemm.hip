@@ -1214,6 +1214,76 @@ int kf_gemm_k_multiple() { return GM_BK; }
 
 
 // Host launcher, validated by the caller (api.cpp): K a multiple of 128, Q8_0-kind activations in `act`
+// Whether 65.. q8_0 rows run faster as 64-row slices through the small-batch products than on the tile GEMM
+// (MI355X, Llama-3-8B shapes at 96-512 rows; the model picks the faster form at all 24 measured points): a 64-row
+// slice costs about 9 us + 0.45 us per weight MB, the tile GEMM about 3 us per 128-column stage per round of one
+// block a CU (a last round at most half full as K halves: half a round; the kernel is VALU-bound, so a second block
+// on a CU does not shorten a round). KF_GEMM_SLICE=0 / 1 forces the choice (a comparison knob).
+static bool q8_0_slices_pay(int M, int N, int K, int64_t row_bytes) {
+    if (const char* e = getenv("KF_GEMM_SLICE")) return atoi(e) != 0;
+    const double mb = (double)N * row_bytes / 1e6;
+    const double t_slices = ((M + 63) / 64) * (9.0 + 0.45 * mb);
+    const int cus = gm_cus();
+    const int64_t T = (int64_t)((N + 127) / 128) * ((M + 127) / 128), rem = T % cus;
+    const double rounds = (double)(T / cus) + (rem == 0 ? 0.0 : rem <= cus / 2 && K % 512 == 0 ? 0.5 : 1.0);
+    const double t_tile = 3.0 * (K / 128) * rounds;
+    return t_slices < t_tile;
+}
+
+// The small-batch products of 1..64 activation rows (K % 256 == 0, 16-byte aligned rows): hipErrorNotSupported when
+// none takes the shape
+static hipError_t small_q8_0(const uint8_t* wb, int64_t row_bytes, const int8_t* xq, const float* xd, const float* bias, const float* res,
+                             float* y, int M, int N, int K, hipStream_t s) {
+    // 17..64 rows with K split across blocks, for matrices above 4096 x 4096 (MI355X, Llama-3-8B shapes, 32 / 64
+    // rows: QKV 17.0 / 23.4 against 21.1 / 28.4 us, gate 26.4 / 38.2 against 35.6 / 50.0, down 27.8 / 38.9
+    // against 31.4 / 48.0; O at 4096 x 4096 15.2 / 20.5 against 12.1 / 18.4, so not there). KF_GEMM_SK=0 turns
+    // it off, KF_GEMM_SK=1 on for every size (comparison knobs)
+    const char* ske = getenv("KF_GEMM_SK");
+    const bool sk = ske ? atoi(ske) != 0 : (int64_t)N * K > (1ll << 24);
+    if (M > 16 && M <= 64 && K % 128 == 0 && (K / 32) % 2 == 0 && sk) {
+        const char* ve = getenv("KF_GEMM_SK_V");  // 10 G + NS (groups a chunk, ring stages): a tuning knob
+        const int var = ve ? atoi(ve) : 0;
+        // 8-group chunks in two stages where K allows (MI355X, Llama-3-8B shapes at 32 / 64 rows: gate 25.1 / 37.2
+        // against 26.0 / 38.3 us with 4-group chunks in three, down 24.5 / 37.4 against 25.3 / 39.3)
+        const int v = var ? var : K % 256 == 0 ? 82 : 43;
+        hipError_t e = hipErrorNotSupported;
+        if (K % (32 * (v / 10)) == 0) {
+            if (M <= 32)
+                e = v == 83    ? gemm_sk_launch<2, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                    : v == 82  ? gemm_sk_launch<2, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                    : v == 162 ? gemm_sk_launch<2, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                               : gemm_sk_launch<2, 1, 4, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+            else
+                e = v == 83    ? gemm_sk_launch<4, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                    : v == 82  ? gemm_sk_launch<4, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                    : v == 162 ? gemm_sk_launch<4, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
+                               : gemm_sk_launch<4, 1, 4, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+        }
+        if (e != hipErrorNotSupported) return e;
+    }
+    if (M > 48 && M <= MR_ROWS && K % (32 * MR_G) == 0 && !getenv("KF_GEMM_NO_MR")) {
+        // 49..64 rows in one weight pass where it measured faster than four 16-row blocks (MI355X, Llama-3-8B
+        // shapes at 64 rows: O 18.4 against 21.6 us, down 48.3 against 57.0, gate 49.8 against 55.2; QKV and
+        // 17..48 rows: no gain). One 16-row weight tile a block, 4 waves splitting K for N <= 4096 (too few tiles
+        // otherwise), one wave for wide outputs. KF_GEMM_MR=11 / 14 forces a variant (a comparison knob)
+        const char* fe = getenv("KF_GEMM_MR");
+        const int v = fe ? atoi(fe) : N >= 8192 ? 11 : N <= 4096 ? 14 : 0;
+        if (v == 11) return gemm_mr_launch<1, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+        if (v == 14) return gemm_mr_launch<1, 4>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+    }
+    if (M <= 64) {  // M / 16 row blocks
+        // one 16-column tile a wave when that still gives at most one block per CU (a block holds a CU), else two
+        static const int tn = [] {  // KF_GEMM_SMALL_TN: a tuning knob
+            const char* e = getenv("KF_GEMM_SMALL_TN");
+            return e ? atoi(e) : 0;
+        }();
+        if (tn == 1 || (tn != 2 && (int64_t)((N + 15) / 16) * ((M + 15) / 16) <= gm_cus()))
+            return gemm_small_launch<16, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 16), s);
+        return gemm_small_launch<16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 32), s);
+    }
+    return hipErrorNotSupported;
+}
+
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s) {
     const kf_act_offsets o = kf_act_layout((size_t)M, (size_t)K);
@@ -1221,54 +1291,19 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
     const auto* xq = reinterpret_cast<const int8_t*>(base + o.q);
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
     const auto* wb = static_cast<const uint8_t*>(w);
-    // the small-batch kernel reads whole 16-byte pieces of rows, which needs 16-byte aligned rows (K % 256 == 0)
+    // the small-batch kernels read whole 16-byte pieces of rows, which needs 16-byte aligned rows (K % 256 == 0)
     if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31) && !getenv("KF_GEMM_TILE")) {
-        // 17..64 rows with K split across blocks, for matrices above 4096 x 4096 (MI355X, Llama-3-8B shapes, 32 / 64
-        // rows: QKV 17.0 / 23.4 against 21.1 / 28.4 us, gate 26.4 / 38.2 against 35.6 / 50.0, down 27.8 / 38.9
-        // against 31.4 / 48.0; O at 4096 x 4096 15.2 / 20.5 against 12.1 / 18.4, so not there). KF_GEMM_SK=0 turns
-        // it off, KF_GEMM_SK=1 on for every size (comparison knobs)
-        const char* ske = getenv("KF_GEMM_SK");
-        const bool sk = ske ? atoi(ske) != 0 : (int64_t)N * K > (1ll << 24);
-        if (M > 16 && M <= 64 && K % 128 == 0 && (K / 32) % 2 == 0 && sk) {
-            const char* ve = getenv("KF_GEMM_SK_V");  // 10 G + NS (groups a chunk, ring stages): a tuning knob
-            const int var = ve ? atoi(ve) : 0;
-            // 8-group chunks in two stages where K allows (MI355X, Llama-3-8B shapes at 32 / 64 rows: gate 25.1 / 37.2
-            // against 26.0 / 38.3 us with 4-group chunks in three, down 24.5 / 37.4 against 25.3 / 39.3)
-            const int v = var ? var : K % 256 == 0 ? 82 : 43;
-            hipError_t e = hipErrorNotSupported;
-            if (K % (32 * (v / 10)) == 0) {
-                if (M <= 32)
-                    e = v == 83    ? gemm_sk_launch<2, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                        : v == 82  ? gemm_sk_launch<2, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                        : v == 162 ? gemm_sk_launch<2, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                                   : gemm_sk_launch<2, 1, 4, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
-                else
-                    e = v == 83    ? gemm_sk_launch<4, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                        : v == 82  ? gemm_sk_launch<4, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                        : v == 162 ? gemm_sk_launch<4, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
-                                   : gemm_sk_launch<4, 1, 4, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
-            }
+        if (M <= 64) {
+            const hipError_t e = small_q8_0(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
             if (e != hipErrorNotSupported) return e;
-        }
-        if (M > 48 && M <= MR_ROWS && K % (32 * MR_G) == 0 && !getenv("KF_GEMM_NO_MR")) {
-            // 49..64 rows in one weight pass where it measured faster than four 16-row blocks (MI355X, Llama-3-8B
-            // shapes at 64 rows: O 18.4 against 21.6 us, down 48.3 against 57.0, gate 49.8 against 55.2; QKV and
-            // 17..48 rows: no gain). One 16-row weight tile a block, 4 waves splitting K for N <= 4096 (too few tiles
-            // otherwise), one wave for wide outputs. KF_GEMM_MR=11 / 14 forces a variant (a comparison knob)
-            const char* fe = getenv("KF_GEMM_MR");
-            const int v = fe ? atoi(fe) : N >= 8192 ? 11 : N <= 4096 ? 14 : 0;
-            if (v == 11) return gemm_mr_launch<1, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
-            if (v == 14) return gemm_mr_launch<1, 4>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
-        }
-        if (M <= 64) {  // M / 16 row blocks
-            // one 16-column tile a wave when that still gives at most one block per CU (a block holds a CU), else two
-            static const int tn = [] {  // KF_GEMM_SMALL_TN: a tuning knob
-                const char* e = getenv("KF_GEMM_SMALL_TN");
-                return e ? atoi(e) : 0;
-            }();
-            if (tn == 1 || (tn != 2 && (int64_t)((N + 15) / 16) * ((M + 15) / 16) <= gm_cus()))
-                return gemm_small_launch<16, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 16), s);
-            return gemm_small_launch<16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 32), s);
+        } else if (q8_0_slices_pay(M, N, K, row_bytes)) {
+            // 65.. rows as 64-row slices through the small-batch products (each slice its own weight pass)
+            for (int m0 = 0; m0 < M; m0 += 64) {
+                const hipError_t e = small_q8_0(wb, row_bytes, xq + (int64_t)m0 * K, xd + (int64_t)m0 * (K / 32), bias,
+                                                res ? res + (int64_t)m0 * N : nullptr, y + (int64_t)m0 * N, std::min(64, M - m0), N, K, s);
+                if (e != hipSuccess) return e;
+            }
+            return hipSuccess;
         }
     }
     if (K % 256 == 0 && row_bytes % 16 == 0) return gemm_q8_0_dma_launch<2, 4, 2, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);

@@ -663,3 +663,35 @@ def test_gemm_q8_0_tail_halves(cuda, monkeypatch, rows, n, n_out):
     _close(outs[0], y.cpu().numpy())
     if rows * n_out <= 300 * 1000:
         _close(outs[0], oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias))
+
+
+@pytest.mark.parametrize("rows,n,n_out", [(96, 14336, 600), (130, 4096, 4096), (250, 14336, 520), (65, 4096, 6144)])
+def test_gemm_q8_0_row_slices(cuda, monkeypatch, rows, n, n_out):
+    """65.. q8_0 rows as 64-row slices through the small-batch products (the cost model's pick at down- and O-like
+    shapes up to a few hundred rows; KF_GEMM_SLICE forces each form): ragged last slices (2, 58 and 1 rows), bias and
+    residual; the sliced and tile forms within the f32 bar of each other, and the auto choice against the CPU backend."""
+    import torch
+
+    w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + 11)
+    x = kf.synth_normal(rows + 13, 1.0, rows * n).reshape(rows, n)
+    bias = kf.synth_normal(9, 1.0, n_out)
+    res = kf.synth_normal(10, 1.0, rows * n_out).reshape(rows, n_out)
+    wt, bt, rt = _tensor(w, cuda), _tensor(bias, cuda), _tensor(res, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.ACT_Q8_0)
+    outs = {}
+    for force in (None, "1", "0"):
+        if force is None:
+            monkeypatch.delenv("KF_GEMM_SLICE", raising=False)
+        else:
+            monkeypatch.setenv("KF_GEMM_SLICE", force)
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt, res=rt)
+        torch.cuda.synchronize()
+        outs[force] = y.cpu().numpy()
+    _close(outs["1"], outs["0"])
+    if rows * n_out <= 250 * 600:
+        _close(outs[None], oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res)
+    else:
+        sample = np.arange(0, rows, 7)
+        _close(outs[None][sample], oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x[sample], bias) + res[sample])
