@@ -579,25 +579,31 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
         for (int j = 0; j < TN; j++) acc[i][j] = v16f{};
 
     // one group per trip: fully unrolled, the scheduler hoists every group's MFMAs above the rescales and spills
+    // the scales' operand tuples (the f16 scale at k = 0, zeros elsewhere) live across the stages: only their first
+    // register changes per group, so the zeros are not rebuilt every time
+    v4u ua[TM], ub[TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++) ua[i] = v4u{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < TN; j++) ub[j] = v4u{0u, 0u, 0u, 0u};
     auto stage = [&](const uint8_t* buf, int st) {
         const int wo = (136 * st) & 15;  // the stage's offset in its weight windows
 #pragma unroll 1
         for (int g = 0; g < GM_G; g++) {
             v4i a[TM], b[TN];
-            uint32_t sa[TM], sb[TN];
 #pragma unroll
             for (int i = 0; i < TM; i++) {
                 a[i] = *reinterpret_cast<const v4i*>(buf + ((g * C::MT + wm * TM + i) * 64 + lane) * 16);
                 // Q8_0-kind activation scales are f16-rounded values, so this conversion is exact
                 const float dx = reinterpret_cast<const float*>(buf + C::D_OFF)[((wm * TM + i) * 32 + r32) * 4 + g];
-                sa[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)dx) & (uint32_t)(half - 1);  // lanes >= 32: zero
+                ua[i].x = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)dx) & (uint32_t)(half - 1);  // lanes >= 32: zero
             }
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint8_t* rp = buf + C::B_OFF + ((wn * TN + j) * 32 + r32) * C::ROW + wo + g * KF_Q8_0_BYTES;
                 const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(rp + 2 + 16 * half);
                 b[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
-                sb[j] = *reinterpret_cast<const uint16_t*>(rp);
+                ub[j].x = *reinterpret_cast<const uint16_t*>(rp);
             }
             v16i c[TM][TN];
             v16f s[TM][TN];
@@ -606,8 +612,7 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     c[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], v16i{}, 0, 0, 0);
-                    const v4u ua = {sa[i], 0u, 0u, 0u}, ub = {sb[j], 0u, 0u, 0u};
-                    s[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ua), __builtin_bit_cast(v8h, ub), v16f{}, 0, 0, 0);
+                    s[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(v8h, ua[i]), __builtin_bit_cast(v8h, ub[j]), v16f{}, 0, 0, 0);
                 }
 #pragma unroll
             for (int i = 0; i < TM; i++)
