@@ -416,6 +416,27 @@ def traffic_section(dev):
     return {"copy_bytes": src.numel(), "gemv_algorithmic_bytes": sh.bytes}
 
 
+def read_probe(gate_up, dev):
+    """HBM read rate of the streaming-read probe (kf_hip_stream_read: plain 16-byte loads, the whole buffer requested at
+    launch), best of 4, 8 and 16 pieces a thread: over 4 GiB (the box's steady-state peak) and over the gate+up launch's
+    own weight copies in the same rotation as the GEMV (that launch size's ceiling: launch, ramp and tail included)."""
+    import torch
+
+    import kungfu_amd as kf
+
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    big = torch.empty(4 << 30, dtype=torch.uint8, device=dev)
+    best_big = best_same = 0.0
+    for p in (4, 8, 16):
+        us = time_launches(lambda i: kf.stream_read(big, sink, p), 4)
+        best_big = max(best_big, big.numel() / us / 1e3)
+        ws = gate_up.w
+        us = time_launches(lambda i: kf.stream_read(ws[i % len(ws)], sink, p), 200)
+        best_same = max(best_same, ws[0].numel() / us / 1e3)
+    del big
+    return {"peak_measured": round(best_big, 1), "ceiling_same_bytes": round(best_same, 1)}
+
+
 def read_traffic():
     """HBM bytes per gate+up GEMV launch from the committed counter summary (null when it is absent)."""
     try:
@@ -531,6 +552,7 @@ def main():
             k1_bytes += sh.bytes
             k1_us += us
     achieved = k1_bytes / k1_us / 1e3
+    probe = read_probe(shapes[2], dev)
 
     # Q8_0 GEMV of configs[0] (4096x4096) on the GPU, rotating copies
     q8 = Shape("q8_0", kf.TYPE_Q8_0, 4096, 4096, max(2, -(-2 * MALL_BYTES // (kf.row_bytes(8, 4096) * 4096)) + 1), dev)
@@ -556,7 +578,11 @@ def main():
         "roofline": {"bound": "hbm", "kernel": "gemv_pipe_kernel<q4_K, one wave a row> (the gate+up launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "algorithmic_bytes": gemv_bytes(kf.TYPE_Q4_K, 4096, 2 * 14336)},
+                     "algorithmic_bytes": gemv_bytes(kf.TYPE_Q4_K, 4096, 2 * 14336),
+                     # the streaming-read probe on this box: over 4 GiB, and over the same weight bytes per launch
+                     "peak_measured": probe["peak_measured"], "frac_of_measured": round(achieved / probe["peak_measured"], 4),
+                     "ceiling_same_bytes": probe["ceiling_same_bytes"],
+                     "frac_of_ceiling": round(achieved / probe["ceiling_same_bytes"], 4)},
         "shapes": per,
         "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1)},
     }

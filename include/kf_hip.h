@@ -231,6 +231,11 @@ int kf_hip_moe_ffn(uint32_t ty, const void* gate, const void* up, const void* do
 int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void* act, int rows, int n, int n_out, int32_t* out,
                       void* stream);
 
+/* Streaming read of `bytes` bytes at buf (16-byte aligned, bytes a multiple of 16, below 2^36) with plain 16-byte loads,
+ * per_thread (4, 8 or 16) pieces a thread, all requested at launch; writes at most one word to sink (4 bytes). No
+ * reference counterpart: the measurement's HBM read peak on the box, reported beside the spec peak. */
+int kf_hip_stream_read(const void* buf, size_t bytes, int per_thread, uint32_t* sink, void* stream);
+
 /* ---------------------------------------------------------------------------------------------------------------
  * Backend mirror (crates/kf-core/src/backend.rs:206-269 Backend; WeightSource :7-13). Host buffers in and out; the
  * backend owns device copies of its weights (ensure_weight, crates/kf-backend-cuda/src/exec.rs:1347-1359) and a

@@ -77,6 +77,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_gemv_group": ([U, P, L64, P, P, I, I, P, I, P], I),
         "kf_hip_matmul_group": ([U, P, I, P, I, P, P, P, I, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
+        "kf_hip_stream_read": ([P, S, I, P, P], I),
         "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_moe_group": ([P, I, I, P, P, P], I),
         "kf_hip_moe_gemv": ([U, P, P, L64, L64, P, I, I, I, P, P, I, I, I, P, P], I),
@@ -267,6 +268,11 @@ def matmul_group(ty: int, members, x, act, stream=None) -> None:
 
 def block_ints(ty: int, w, act, out, rows: int, n: int, n_out: int, stream=None) -> None:
     check(lib().kf_hip_block_ints(ty, _ptr(w), row_bytes(ty, n), _ptr(act), rows, n, n_out, _ptr(out), _stream(stream)))
+
+
+def stream_read(buf, sink, per_thread: int = 8, stream=None) -> None:
+    """Streaming read of a device tensor with plain 16-byte loads (kf_hip_stream_read): the HBM read-rate probe."""
+    check(lib().kf_hip_stream_read(_ptr(buf), buf.numel() * buf.element_size(), per_thread, _ptr(sink), _stream(stream)))
 
 
 def moe_group(slots, total: int, n_slots: int, order, offsets, stream=None) -> None:

@@ -18,7 +18,7 @@ LIB = os.path.join(OUT_DIR, "libkf_hip.so")
 OBJ_DIR = os.path.join(HERE, "build", "obj")
 
 ARCH = "gfx950"
-DEVICE_SOURCES = ["quant_act.hip", "gemv.hip", "gemv_k.hip", "gemm.hip", "gemm_q4k.hip", "gemm_kq.hip", "rows.hip", "rows_mma.hip", "noalloc.hip"]
+DEVICE_SOURCES = ["quant_act.hip", "gemv.hip", "gemv_k.hip", "gemm.hip", "gemm_q4k.hip", "gemm_kq.hip", "rows.hip", "rows_mma.hip", "noalloc.hip", "probe.hip"]
 HOST_SOURCES = ["api.cpp", "host_quant.cpp", "gguf.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]

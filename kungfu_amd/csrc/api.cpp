@@ -22,6 +22,7 @@ static_assert(KF_HIP_MAX_SEGMENTS == KF_MAX_SEGS, "one segment limit");
 
 // Launchers in the .hip translation units
 hipError_t kf_launch_quant_act(const float* x, void* act, int rows, int n, int kind, hipStream_t s);
+hipError_t kf_launch_stream_read(const void* buf, size_t bytes, int per_thread, uint32_t* sink, hipStream_t s);
 hipError_t kf_launch_gemv_k(uint32_t ty, const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y,
                             int rows, int n, int n_out, hipStream_t s);
 hipError_t kf_launch_rms_norm_q8(const float* x, const float* w, const float* b, float eps, void* act, int rows, int n, int kind,
@@ -618,6 +619,16 @@ int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void*
     if (rc != KF_OK) return rc;
     const hipError_t e = kf_launch_block_ints(ty, w, row_bytes, act, rows, n, n_out, out, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "block_ints launch");
+}
+
+int kf_hip_stream_read(const void* buf, size_t bytes, int per_thread, uint32_t* sink, void* stream) {
+    if (!buf || !sink) return fail(KF_E_INVALID, "null buffer or sink");
+    if (reinterpret_cast<uintptr_t>(buf) % 16 != 0 || bytes % 16 != 0 || bytes == 0 || bytes >= (1ull << 36))
+        return fail(KF_E_INVALID, "%zu bytes at a %s address: the probe reads 16-byte aligned pieces, below 64 GB", bytes,
+                    reinterpret_cast<uintptr_t>(buf) % 16 ? "misaligned" : "16-byte aligned");
+    if (per_thread != 4 && per_thread != 8 && per_thread != 16) return fail(KF_E_INVALID, "%d pieces a thread (4, 8 or 16)", per_thread);
+    const hipError_t e = kf_launch_stream_read(buf, bytes, per_thread, sink, static_cast<hipStream_t>(stream));
+    return e == hipSuccess ? KF_OK : hip_fail(e, "stream_read launch");
 }
 
 }  // extern "C"

@@ -695,3 +695,19 @@ def test_gemm_q8_0_row_slices(cuda, monkeypatch, rows, n, n_out):
     else:
         sample = np.arange(0, rows, 7)
         _close(outs[None][sample], oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x[sample], bias) + res[sample])
+
+
+def test_stream_read_probe(cuda):
+    """The benchmark's read probe (kf_hip_stream_read) on ragged sizes: it runs for every per-thread count, leaves the
+    sink alone (no data matches its key) and does not touch the buffer."""
+    import torch
+
+    sink = torch.zeros(1, dtype=torch.int32, device=cuda)
+    for nbytes in (16, 4096 + 48, 3 << 20):
+        buf = torch.arange(nbytes, dtype=torch.int64, device=cuda).to(torch.uint8)
+        before = buf.clone()
+        for p in (4, 8, 16):
+            kf.stream_read(buf, sink, p)
+        torch.cuda.synchronize()
+        assert torch.equal(buf, before)
+    assert int(sink.item()) == 0

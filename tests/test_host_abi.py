@@ -76,6 +76,21 @@ def test_quant_act_argument_checks():
     assert L.kf_hip_matmul(kf.TYPE_Q4_K, FAKE, 4096 + 32, 8, FAKE, 1, FAKE, None, None, FAKE, None) == kf.KF_E_INVALID
 
 
+def test_stream_read_argument_checks():
+    """The read probe's checks run before any device call: null, misaligned, ragged or oversized buffers and an
+    unsupported per-thread count are refused."""
+    L = kf.lib()
+    assert L.kf_hip_stream_read(None, 4096, 8, FAKE, None) == kf.KF_E_INVALID
+    assert L.kf_hip_stream_read(FAKE, 4096, 8, None, None) == kf.KF_E_INVALID
+    assert L.kf_hip_stream_read(FAKE + 8, 4096, 8, FAKE, None) == kf.KF_E_INVALID
+    assert "misaligned" in kf.last_error()
+    assert L.kf_hip_stream_read(FAKE, 4100, 8, FAKE, None) == kf.KF_E_INVALID
+    assert L.kf_hip_stream_read(FAKE, 0, 8, FAKE, None) == kf.KF_E_INVALID
+    assert L.kf_hip_stream_read(FAKE, 1 << 36, 8, FAKE, None) == kf.KF_E_INVALID
+    assert L.kf_hip_stream_read(FAKE, 4096, 6, FAKE, None) == kf.KF_E_INVALID
+    assert "pieces a thread" in kf.last_error()
+
+
 def test_backend_errors_without_a_device():
     import torch
 
