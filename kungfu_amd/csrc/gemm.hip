@@ -1202,16 +1202,6 @@ int small_waves(int M, int N, int K, int rows_per_block) {
     return w;
 }
 
-// Compute units of the current device (cached per process; the build targets one gfx950 device model)
-int gm_cus() {
-    static const int n = [] {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 256;
-        return v;
-    }();
-    return n;
-}
-
 }  // namespace
 
 int kf_gemm_k_multiple() { return GM_BK; }
@@ -1228,7 +1218,7 @@ static bool q8_0_slices_pay(int M, int N, int K, int64_t row_bytes) {
     if (const char* e = getenv("KF_GEMM_SLICE")) return atoi(e) != 0;
     const double mb = (double)N * row_bytes / 1e6;
     const double t_slices = ((M + 63) / 64) * (9.0 + 0.45 * mb);
-    const int cus = gm_cus();
+    const int cus = kf_cu_count();
     const int64_t T = (int64_t)((N + 127) / 128) * ((M + 127) / 128), rem = T % cus;
     const double rounds = (double)(T / cus) + (rem == 0 ? 0.0 : rem <= cus / 2 && K % 512 == 0 ? 0.5 : 1.0);
     const double t_tile = 3.0 * (K / 128) * rounds;
@@ -1282,7 +1272,7 @@ static hipError_t small_q8_0(const uint8_t* wb, int64_t row_bytes, const int8_t*
             const char* e = getenv("KF_GEMM_SMALL_TN");
             return e ? atoi(e) : 0;
         }();
-        if (tn == 1 || (tn != 2 && (int64_t)((N + 15) / 16) * ((M + 15) / 16) <= gm_cus()))
+        if (tn == 1 || (tn != 2 && (int64_t)((N + 15) / 16) * ((M + 15) / 16) <= kf_cu_count()))
             return gemm_small_launch<16, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 16), s);
         return gemm_small_launch<16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 32), s);
     }
