@@ -257,10 +257,11 @@ def moe_prefill_section(dev):
 
 
 def layer_with_producers_section(shapes, dev):
-    """The decode layer step with its activation producers, batch 1, Q4_K: rms_norm_q8 -> QKV, quant_act of the
-    attention output -> O, rms_norm_q8 -> gate+up, gated_act_q8 of the gate+up output -> down (every product's
-    activations made inside the step, the cost Op::MatMul pays at M=1). GB/s over the same algorithmic bytes as the
-    headline step."""
+    """The decode layer step with its activation producers, batch 1, Q4_K (every product's activations made inside the
+    step, the cost Op::MatMul pays at M=1), GB/s over the same algorithmic bytes as the headline step: the library's
+    path (kf_hip_rms_norm_matmul for QKV and gate+up, kf_hip_matmul for O, each one launch; gated_act_q8 -> down: five
+    launches), and beside it the producers as launches of their own (rms_norm_q8 -> QKV, quant_act -> O, rms_norm_q8 ->
+    gate+up, gated_act_q8 -> down: eight launches)."""
     import torch
 
     import kungfu_amd as kf
@@ -282,10 +283,24 @@ def layer_with_producers_section(shapes, dev):
         kf.gated_act_q8(gu[:, :n_ff], gu[:, n_ff:], by["down"].act, kf.ACT_Q8K, 1, n_ff, 2 * n_ff)
         by["down"].gemv(i)
 
-    us = time_launches(step, 50)
+    def step_fused(i):
+        # the library's own decode path: the norm (QKV, gate+up) or the quantization (O) inside the GEMV launch
+        for nm, inp in (("qkv", x), ("o", attn), ("gate_up", x)):
+            sh = by[nm]
+            wi = sh.w[i % len(sh.w)]
+            if nm == "o":
+                kf.matmul(sh.ty, wi, inp, sh.act, sh.y, sh.n_out)
+            else:
+                kf.rms_norm_matmul(sh.ty, wi, inp, sh.act, sh.y, sh.n_out, wn, None, 1e-5)
+        gu = by["gate_up"].y
+        kf.gated_act_q8(gu[:, :n_ff], gu[:, n_ff:], by["down"].act, kf.ACT_Q8K, 1, n_ff, 2 * n_ff)
+        by["down"].gemv(i)
+
+    us_sep = time_launches(step, 50)
+    us = time_launches(step_fused, 50)
     nb = sum(s.bytes for s in shapes)
-    return {"us": round(us, 2), "GBs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
-            "launches": 8}
+    return {"us": round(us, 2), "GBs": round(nb / us / 1e3, 1), "frac": round(nb / us / 1e3 / HBM_PEAK_GBS, 4), "launches": 5,
+            "separate_producers": {"us": round(us_sep, 2), "GBs": round(nb / us_sep / 1e3, 1), "launches": 8}}
 
 
 def fused_section(dev):

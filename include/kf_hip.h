@@ -140,6 +140,16 @@ int kf_hip_gemm_i8(uint32_t ty, const void* w, int64_t row_bytes, const void* ac
 int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, void* act, const float* bias,
                   const float* res, float* y, void* stream);
 
+/* kf_hip_rms_norm_q8 and kf_hip_matmul as one call: y = W . quant(rms_norm(x) * norm_w + norm_b) + bias + res, the
+ * normalised rows quantized into `act` as kf_hip_rms_norm_q8 writes them, then the product kf_hip_matmul selects.
+ * One row of q8_0 / q4_K (n_in <= 4096, x, norm_w, norm_b and the weights 16-byte aligned) runs as one launch: every
+ * block of the GEMV normalises and quantizes the row itself (the same f64 sum of squares, correctly rounded square
+ * root and division and unfused multiply-adds, so the same integers) and `act` is left unwritten
+ * (KF_MATMUL_NO_FUSE: two launches). Replaces the reference's rms_norm_q8 launch followed by matmul_launch
+ * (exec.rs:2439, 2061-2093) for the decode products whose input is a normalised row (QKV, gate/up). */
+int kf_hip_rms_norm_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, const float* norm_w, const float* norm_b,
+                           float eps, void* act, const float* bias, const float* res, float* y, void* stream);
+
 /* kf_hip_matmul without the `act` argument, for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). No counterpart in the reference. The activation
  * scratch is a static device array of KF_NOALLOC_SCRATCH_BYTES inside the library, one per GPU, held until the process

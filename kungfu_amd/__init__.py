@@ -78,6 +78,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_matmul_group": ([U, P, I, P, I, P, P, P, I, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
         "kf_hip_stream_read": ([P, S, I, P, P], I),
+        "kf_hip_rms_norm_matmul": ([U, P, I, I, P, I, P, P, ctypes.c_float, P, P, P, P, P], I),
         "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_moe_group": ([P, I, I, P, P, P], I),
         "kf_hip_moe_gemv": ([U, P, P, L64, L64, P, I, I, I, P, P, I, I, I, P, P], I),
@@ -268,6 +269,14 @@ def matmul_group(ty: int, members, x, act, stream=None) -> None:
 
 def block_ints(ty: int, w, act, out, rows: int, n: int, n_out: int, stream=None) -> None:
     check(lib().kf_hip_block_ints(ty, _ptr(w), row_bytes(ty, n), _ptr(act), rows, n, n_out, _ptr(out), _stream(stream)))
+
+
+def rms_norm_matmul(ty: int, w, x, act, y, n_out: int, norm_w=None, norm_b=None, eps: float = 1e-5, bias=None, res=None, stream=None) -> None:
+    """rms_norm of x [rows][n_in], quantization and the product kf_hip_matmul selects, one launch at one row
+    (kf_hip_rms_norm_matmul)."""
+    rows, n_in = x.shape
+    check(lib().kf_hip_rms_norm_matmul(ty, _ptr(w), n_in, n_out, _ptr(x), rows, _ptr(norm_w), _ptr(norm_b), eps, _ptr(act), _ptr(bias), _ptr(res),
+                                       _ptr(y), _stream(stream)))
 
 
 def stream_read(buf, sink, per_thread: int = 8, stream=None) -> None:

@@ -37,7 +37,8 @@ bool kf_rows_mma_1_ok(uint32_t ty, const void* w, int64_t row_bytes, int n, int 
 hipError_t kf_launch_rows_mma_1(uint32_t ty, const void* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, int n,
                                 int n_out, int rows, const float* bias, const float* res, float* y, hipStream_t s);
 hipError_t kf_launch_gemv1_fused(uint32_t ty, const void* w, int64_t row_bytes, const float* x, const float* bias, const float* res, float* y,
-                                 int n, int n_out, const KfSegs* segs, hipStream_t s);
+                                 int n, int n_out, const KfSegs* segs, hipStream_t s, const float* norm_w = nullptr, const float* norm_b = nullptr,
+                                 float norm_eps = 0.0f, bool norm = false);
 int kf_gemv_max_n();
 hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act, const float* bias, const float* res, float* y, int M,
                                int N, int K, hipStream_t s);
@@ -288,6 +289,29 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
         if (e != hipErrorNotSupported) return hip_fail(e, "fused gemv launch");
     }
     const int q = kf_hip_quant_act(x, act, rows, n_in, kind_of(ty), stream);
+    if (q != KF_OK) return q;
+    return product(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
+}
+
+int kf_hip_rms_norm_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, const float* norm_w, const float* norm_b,
+                           float eps, void* act, const float* bias, const float* res, float* y, void* stream) {
+    int block, bytes;
+    if (!type_info(ty, block, bytes)) return fail(KF_E_UNSUPPORTED, "ggml type %u is not on the int8 path (q8_0=8, q4_K=12, q5_K=13, q6_K=14)", ty);
+    if (n_in <= 0 || n_in % block != 0) return fail(KF_E_INVALID, "%d columns against blocks of %d", n_in, block);
+    const int64_t rb = (int64_t)(n_in / block) * bytes;
+    const int rc = check_product(ty, w, rb, act, y, rows, n_in, n_out);
+    if (rc != KF_OK) return rc;
+    if (!x || !aligned(x, 16) || (norm_w && !aligned(norm_w, 16)) || (norm_b && !aligned(norm_b, 16)))
+        return fail(KF_E_INVALID, "x (and norm_w, norm_b when given) must be 16-byte aligned device pointers");
+    if (!(eps >= 0.0f)) return fail(KF_E_INVALID, "eps %g", (double)eps);
+    if (rows == 1 && !no_fusion()) {
+        // one launch: every block of the GEMV normalises and quantizes the row itself
+        const hipError_t e = kf_launch_gemv1_fused(ty, w, rb, x, bias, res, y, n_in, n_out, nullptr, static_cast<hipStream_t>(stream), norm_w,
+                                                   norm_b, eps, true);
+        if (e == hipSuccess) return KF_OK;
+        if (e != hipErrorNotSupported) return hip_fail(e, "fused rms_norm gemv launch");
+    }
+    const int q = kf_hip_rms_norm_q8(x, norm_w, norm_b, rows, n_in, eps, kind_of(ty), act, stream);
     if (q != KF_OK) return q;
     return product(ty, w, rb, act, bias, res, y, rows, n_in, n_out, stream);
 }

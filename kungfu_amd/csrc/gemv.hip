@@ -172,15 +172,71 @@ __device__ __forceinline__ void gv_stage_store(uint8_t* smem, size_t sums_at, si
 template <int QX>
 struct GvXf {
     float4 v[QX > 0 ? QX : 1];
+    float4 w[QX > 0 ? QX : 1], b[QX > 0 ? QX : 1];  // the norm's weight and bias columns (the rms_norm variants)
 };
 
-template <int QX>
-__device__ __forceinline__ void gv_xf_load(GvXf<QX>& r, const float* __restrict__ x, int n, int wave, int lane) {
+// The rms_norm the fused variants apply before quantizing (NM = 1): weight and bias columns (either may be null) and
+// eps; unused by the other variants
+struct GvNorm {
+    const float* w;
+    const float* b;
+    float eps;
+};
+
+template <int QX, int NM = 0>
+__device__ __forceinline__ void gv_xf_load(GvXf<QX>& r, const float* __restrict__ x, int n, int wave, int lane, const GvNorm& nm = GvNorm{}) {
 #pragma unroll
     for (int i = 0; i < QX; i++) {
         // unpredicated: a lane past the row's end reloads the row's last four columns, which it does not quantize
-        const int c0 = (wave + GV_WAVES * i) * 256 + 4 * lane;
-        r.v[i] = *reinterpret_cast<const float4*>(x + min(c0, n - 4));
+        const int c0 = min((wave + GV_WAVES * i) * 256 + 4 * lane, n - 4);
+        r.v[i] = *reinterpret_cast<const float4*>(x + c0);
+        if constexpr (NM) {
+            r.w[i] = nm.w ? *reinterpret_cast<const float4*>(nm.w + c0) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
+            r.b[i] = nm.b ? *reinterpret_cast<const float4*>(nm.b + c0) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
+    }
+}
+
+// rms_norm of the row the block's waves hold in their chunks (crates/kf-backend-cpu/src/ops.rs:222-239, as
+// rms_norm_q8_kernel computes it): f32 squares summed in f64 (lane, then wave in a fixed tree, then the waves in
+// order through LDS), ss / n rounded to f32, correctly rounded f32 square root and division, then (v * inv) * w + b
+// unfused, in place. Every wave of the block calls it (one barrier, waiting on LDS only).
+template <int QX>
+__device__ __forceinline__ void gv_xf_norm(GvXf<QX>& r, double* part, int n, int wave, int lane, float eps) {
+#pragma clang fp contract(off)
+    double s = 0.0;
+#pragma unroll
+    for (int i = 0; i < QX; i++) {
+        const int ch = wave + GV_WAVES * i;
+        if (ch * 256 < n && ch * 256 + 4 * lane < n) {
+            const float4 t = r.v[i];
+            const float a0 = t.x * t.x, a1 = t.y * t.y, a2 = t.z * t.z, a3 = t.w * t.w;
+            s += (double)a0;
+            s += (double)a1;
+            s += (double)a2;
+            s += (double)a3;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o, 64);
+    if (lane == 0) part[wave] = s;
+    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
+    __builtin_amdgcn_s_barrier();
+    double t = 0.0;
+#pragma unroll
+    for (int k = 0; k < GV_WAVES; k++) t += part[k];
+    const float ss = (float)(t / (double)n);
+    const float rr = (float)sqrt((double)(ss + eps));
+    const float inv = (float)(1.0 / (double)rr);
+#pragma unroll
+    for (int i = 0; i < QX; i++) {
+        float4& v = r.v[i];
+        const float4 w = r.w[i], b = r.b[i];
+        float u;
+        u = v.x * inv; u = u * w.x; v.x = u + b.x;
+        u = v.y * inv; u = u * w.y; v.y = u + b.y;
+        u = v.z * inv; u = u * w.z; v.z = u + b.z;
+        u = v.w * inv; u = u * w.w; v.w = u + b.w;
     }
 }
 
@@ -289,7 +345,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_kernel(const uint8_t* __restr
                                                           const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                           const float* __restrict__ bias, const float* __restrict__ res,
                                                           float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
-                                                          const float* __restrict__) {
+                                                          const float* __restrict__, const GvNorm) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
@@ -426,7 +482,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
                                                               const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                               const float* __restrict__ bias, const float* __restrict__ res,
                                                               float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
-                                                              const float* __restrict__) {
+                                                              const float* __restrict__, const GvNorm) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;  // blocks per step
@@ -543,12 +599,12 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_dma_kernel(const uint8_t* __r
 // multiplied, the loads of rows i+1 and i+2 are in flight, so the arithmetic of a wave overlaps its own weight stream
 // (a wave that computes only after all its loads land holds its slot while the memory pipe idles). The activation
 // row reaches LDS by DMA before any weight is requested.
-template <uint32_t TY, int WPR, int D, int QX = 0>
+template <uint32_t TY, int WPR, int D, int QX = 0, int NM = 0>
 __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                                const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
                                                                const float* __restrict__ bias, const float* __restrict__ res,
                                                                float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
-                                                               const float* __restrict__ xf) {
+                                                               const float* __restrict__ xf, const GvNorm nm) {
     constexpr int RPB = GV_WAVES / WPR;
     constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
     constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;
@@ -571,7 +627,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     // chunks first and quantizes them once its first rows' weights are requested
     GvXf<QX> xr;
     if constexpr (QX > 0) {
-        gv_xf_load<QX>(xr, xf, n, wave, lane);
+        gv_xf_load<QX, NM>(xr, xf, n, wave, lane, nm);
         __builtin_amdgcn_sched_barrier(0);
     } else {
         const int nchunks = n >> 4, n32 = n >> 5;
@@ -661,6 +717,10 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     for (int k = 0; k < D; k++) gv_load_step<TY>(ring[k], row_ptr(k), len, ln);
     if constexpr (QX > 0) {
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (NM) {
+            __shared__ double norm_part[GV_WAVES];
+            gv_xf_norm<QX>(xr, norm_part, n, wave, lane, nm.eps);
+        }
         gv_xf_quant<TY, QX>(smem, L.sums, L.scales, xr, n, wave, lane);
     }
     // the activation stores are LDS writes of this block only: waiting on lgkmcnt and a bare barrier order them
@@ -788,7 +848,7 @@ int cu_count() {
 }
 
 typedef void (*GvKernel)(const uint8_t*, int64_t, const int8_t*, const int32_t*, const float*, const float*, const float*, float*, int, int, int, const KfSegs,
-                         const float*);
+                         const float*, const GvNorm);
 
 // Most blocks of one kernel resident per CU at a dynamic LDS size, cached per (kernel, LDS)
 int resident_blocks(GvKernel k, size_t smem) {
@@ -813,10 +873,12 @@ int resident_blocks(GvKernel k, size_t smem) {
 // whose weights travel through registers, so the compiler waits on the activation loads alone (with the one-shot
 // kernel's LDS DMA in flight it waits on everything before the quantization)
 template <uint32_t TY, int WPR>
-GvKernel gv_fused_pipe(int qx) {
-    switch (qx) {
+GvKernel gv_fused_pipe(int qx, bool norm) {
+    switch (qx + (norm ? 2 : 0)) {
         case 1: return gemv_pipe_kernel<TY, WPR, KF_GV_DEPTH, 1>;
         case 2: return gemv_pipe_kernel<TY, WPR, KF_GV_DEPTH, 2>;
+        case 3: return gemv_pipe_kernel<TY, WPR, KF_GV_DEPTH, 1, 1>;
+        case 4: return gemv_pipe_kernel<TY, WPR, KF_GV_DEPTH, 2, 1>;
     }
     return nullptr;
 }
@@ -826,7 +888,8 @@ GvKernel gv_fused_pipe(int qx) {
 template <uint32_t TY, int SPW, int WPR>
 hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const int32_t* xs32, const float* xd32, const float* bias,
                        const float* res, float* y, int n, int n_out, int maxit_env, const KfSegs& sg, hipStream_t s, const float* xf = nullptr,
-                       int qx = 0) {
+                       int qx = 0, const GvNorm* norm = nullptr) {
+    const GvNorm nm = norm ? *norm : GvNorm{nullptr, nullptr, 0.0f};
     constexpr int RPB = GV_WAVES / WPR;
     const int groups = (n_out + RPB - 1) / RPB;
     const bool fused = xf != nullptr;
@@ -843,7 +906,7 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         const size_t smem = gd_lds(TY, n, 1, WPR, 1, 1).total;
         GvKernel k = gemv_dma_kernel<TY, 1, WPR, 1>;
         if (groups <= cu_count() * resident_blocks(k, smem) && smem <= 65536) {
-            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1, sg, xf);
+            k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1, sg, xf, nm);
             return hipGetLastError();
         }
     }
@@ -854,7 +917,7 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
             const int v = e ? atoi(e) : 0;
             return v >= 2 && v <= 4 ? v : KF_GV_DEPTH;
         }();
-        GvKernel k = fused ? gv_fused_pipe<TY, WPR>(qx)
+        GvKernel k = fused ? gv_fused_pipe<TY, WPR>(qx, norm != nullptr)
                            : depth == 4 ? gemv_pipe_kernel<TY, WPR, 4> : depth == 3 ? gemv_pipe_kernel<TY, WPR, 3> : gemv_pipe_kernel<TY, WPR, 2>;
         const size_t base_lds = gd_lds(TY, n, 0, WPR, 1, 1).total;
         // two blocks (16 waves) per CU measured best on MI355X (3.9-4.1 TB/s at 33 MB against 3.2-3.5 with every
@@ -866,7 +929,7 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         const int iters = (groups + grid - 1) / grid;
         const size_t smem = gd_lds(TY, n, iters, WPR, 1, 1).total;
         if (k && smem <= 65536) {
-            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, xf);
+            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, xf, nm);
             return hipGetLastError();
         }
     }
@@ -877,10 +940,10 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         const int iters = (groups + grid - 1) / grid;                                                                    \
         if (dma && gd_lds(TY, n, iters, WPR, M, SPW).total <= 65536) {                                                   \
             const size_t smem = gd_lds(TY, n, iters, WPR, M, SPW).total;                                                 \
-            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr); \
+            gemv_dma_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr, nm); \
         } else {                                                                                                         \
             const size_t smem = gv_lds(TY, n, iters, WPR).total;                                                         \
-            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr); \
+            gemv_kernel<TY, SPW, WPR, M><<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr, nm); \
         }                                                                                                                \
         return hipGetLastError();                                                                                        \
     }
@@ -945,7 +1008,9 @@ int kf_gemv_fused_max_n() { return 2 * GV_WAVES * 256; }
 // integers and scales, so the same outputs bit for bit). hipErrorNotSupported when no fused variant fits (n above
 // kf_gemv_fused_max_n, rows or x not 16-byte aligned, a type other than q8_0 / q4_K): the caller quantizes first.
 hipError_t kf_launch_gemv1_fused(uint32_t ty, const void* wv, int64_t row_bytes, const float* x, const float* bias, const float* res, float* y,
-                                 int n, int n_out, const KfSegs* segs, hipStream_t s) {
+                                 int n, int n_out, const KfSegs* segs, hipStream_t s, const float* norm_w, const float* norm_b, float norm_eps,
+                                 bool norm) {
+    const GvNorm nmv{norm_w, norm_b, norm_eps};
     if (n_out == 0) return hipSuccess;
     if (n > kf_gemv_fused_max_n() || n % 4 != 0 || (ty != KF_TYPE_Q4_K && ty != KF_TYPE_Q8_0)) return hipErrorNotSupported;
     KfSegs sg{};
@@ -958,7 +1023,7 @@ hipError_t kf_launch_gemv1_fused(uint32_t ty, const void* wv, int64_t row_bytes,
     const int qx = per_wave <= 1 ? 1 : 2;
 #define KF_GVF(TY, WPR)                                                                                                    \
     if (ty == TY && spw == 1 && wpr == WPR)                                                                               \
-        return launch_gemv<TY, 1, WPR>(w, row_bytes, nullptr, nullptr, nullptr, bias, res, y, n, n_out, 0, sg, s, x, qx);
+        return launch_gemv<TY, 1, WPR>(w, row_bytes, nullptr, nullptr, nullptr, bias, res, y, n, n_out, 0, sg, s, x, qx, norm ? &nmv : nullptr);
     KF_GVF(KF_TYPE_Q4_K, 1)
     KF_GVF(KF_TYPE_Q4_K, 2)
     KF_GVF(KF_TYPE_Q4_K, 4)

@@ -95,3 +95,40 @@ def test_producer_feeds_the_product(cuda):
     want = oracle.matmul_slice(kf.TYPE_Q4_K, wq, n, n_out, oracle.rms_norm(x, w_norm, None, 1e-5))
     err = np.abs(y.cpu().numpy() - want)
     assert (err <= 1e-4 + 1e-3 * np.abs(want)).all(), err.max()
+
+
+@pytest.mark.parametrize("ty", [kf.TYPE_Q4_K, kf.TYPE_Q8_0])
+@pytest.mark.parametrize("rows,n,n_out,affine", [(1, 4096, 520, True), (1, 2048, 300, False), (1, 256, 64, True), (1, 4096, 6144, False),
+                                                 (1, 3584, 96, True), (3, 4096, 200, True)])
+def test_rms_norm_matmul(cuda, monkeypatch, ty, rows, n, n_out, affine):
+    """kf_hip_rms_norm_matmul: at one row the GEMV normalises and quantizes the row in every block (one launch),
+    bit-identical to kf_hip_rms_norm_q8 followed by the product (KF_MATMUL_NO_FUSE); both against the CPU backend's
+    matmul_slice of its rms_norm. Three rows take the two-launch path. Widths of one to sixteen 256-column chunks
+    (some waves of a block hold no chunk)."""
+    import torch
+
+    rng = np.random.default_rng(n + n_out + ty)
+    x = (rng.standard_normal((rows, n)) * rng.uniform(0.05, 30, (rows, 1))).astype(np.float32)
+    wn = (1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32) if affine else None
+    bn = (0.01 * rng.standard_normal(n)).astype(np.float32) if affine else None
+    w = kf.quantize(ty, kf.synth_normal(n + 3, 0.02, n * n_out).reshape(n_out, n))
+    bias = kf.synth_normal(5, 1.0, n_out)
+    res = kf.synth_normal(6, 1.0, rows * n_out).reshape(rows, n_out)
+    wt, xt, bt, rt = (_tensor(a, cuda) for a in (w, x, bias, res))
+    wnt = None if wn is None else _tensor(wn, cuda)
+    bnt = None if bn is None else _tensor(bn, cuda)
+    act = kf.alloc_act(rows, n, cuda)
+    outs = []
+    for fuse in (True, False):
+        if fuse:
+            monkeypatch.delenv("KF_MATMUL_NO_FUSE", raising=False)
+        else:
+            monkeypatch.setenv("KF_MATMUL_NO_FUSE", "1")
+        y = torch.full((rows, n_out), float("nan"), device=cuda)
+        kf.rms_norm_matmul(ty, wt, xt, act, y, n_out, wnt, bnt, 1e-5, bias=bt, res=rt)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    want = oracle.matmul_slice(ty, w, n, n_out, oracle.rms_norm(x, wn, bn, 1e-5), bias) + res
+    err = np.abs(outs[0].astype(np.float64) - want)
+    assert (err <= 1e-4 + 1e-3 * np.abs(want)).all(), f"max error {err.max():.3e}"
