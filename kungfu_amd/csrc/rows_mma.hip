@@ -348,8 +348,16 @@ RmPlan rm_plan(int n, int n_out, int slots, bool glu, int avg_rows) {
         const int tiles = (n_out + 15) / 16;
         const int per_cu = std::max(1, RM_LDS_MAX / (int)(rm_lds(pl.kc, pl.rt).total + pl.nb * buf));
         const int want = std::max(1, kf_cu_count() * per_cu / slots);
-        const int per_wave = std::max(1, std::min(16, (tiles + want * RM_WAVES - 1) / (want * RM_WAVES)));
-        pl.rpb = 16 * RM_WAVES * per_wave;
+        // tiles a block: enough that the slots' blocks fill one round, at least one a wave, at most 16 a wave; not
+        // necessarily a multiple of the waves (C5: 28 tiles a block, 256 blocks, where whole tiles a wave gave 32 and
+        // 224 blocks, leaving 32 CUs idle)
+        static const int whole = [] {  // KF_RM_WHOLE=1: whole tiles a wave (a comparison knob)
+            const char* e = getenv("KF_RM_WHOLE");
+            return e ? atoi(e) : 0;
+        }();
+        int tpb = std::max(RM_WAVES, std::min(16 * RM_WAVES, (tiles + want - 1) / want));
+        if (whole) tpb = RM_WAVES * std::max(1, std::min(16, (tiles + want * RM_WAVES - 1) / (want * RM_WAVES)));
+        pl.rpb = 16 * tpb;
     }
     return pl;
 }
