@@ -326,6 +326,20 @@ __device__ __forceinline__ float gv_q4k_lane(const uint8_t* wl, const uint4* xs,
     return fmaf(-dm, (float)imin, d * (float)isum);
 }
 
+// gv_q4k_lane with the activation side already in registers: x0..x3 the lane's four activation pieces, bs its two
+// sub-block sums, dx the super-block's scale
+__device__ __forceinline__ float gv_q4k_lane_r(const uint8_t* wl, const uint4 x0, const uint4 x1, const uint4 x2, const uint4 x3, const int2 bs,
+                                               float dx, int j) {
+    const uint4 hdr = *reinterpret_cast<const uint4*>(wl);
+    const uint4 qa = *reinterpret_cast<const uint4*>(wl + 16 + 32 * j);
+    const uint4 qb = *reinterpret_cast<const uint4*>(wl + 32 + 32 * j);
+    int isum, imin;
+    kf_q4k_lane(hdr, qa, qb, j, x0, x1, x2, x3, bs.x, bs.y, isum, imin);
+    const float d = kf_h2f(hdr.x & 0xffffu) * dx;
+    const float dm = kf_h2f(hdr.x >> 16) * dx;
+    return fmaf(-dm, (float)imin, d * (float)isum);
+}
+
 // The lane's block of one q8_0 step: the 34 bytes at 34 * lane of the step; b is the block's index in the row
 __device__ __forceinline__ float gv_q8_0_lane(const uint8_t* wl, const uint4* xs, const float* sd, int b) {
     const kf_u32x4_a2 q0 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 2);
@@ -333,6 +347,15 @@ __device__ __forceinline__ float gv_q8_0_lane(const uint8_t* wl, const uint4* xs
     const uint32_t wq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
     const int dt = kf_q8_0_dot(wq, xs[0], xs[64]);
     return kf_h2f(*reinterpret_cast<const uint16_t*>(wl)) * sd[b] * (float)dt;
+}
+
+// gv_q8_0_lane with the activation side in registers (x0, x1 the lane's pieces, dx its block's scale)
+__device__ __forceinline__ float gv_q8_0_lane_r(const uint8_t* wl, const uint4 x0, const uint4 x1, float dx) {
+    const kf_u32x4_a2 q0 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 2);
+    const kf_u32x4_a2 q1 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 18);
+    const uint32_t wq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    const int dt = kf_q8_0_dot(wq, x0, x1);
+    return kf_h2f(*reinterpret_cast<const uint16_t*>(wl)) * dx * (float)dt;
 }
 
 // Decode GEMV of one activation row. Block b, iteration it (< iters <= MAXIT), row group rg (= wave / WPR) owns row
@@ -689,6 +712,25 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
         return gv_row_ptr(sg, w, row_bytes, o) + at;
     };
+    // the wave's activation operands are the same for every row it walks (its step is fixed): read once from LDS,
+    // after the barrier that publishes them
+    uint4 xa4[4];
+    int2 xbs = make_int2(0, 0);
+    float xdx = 0.0f;
+    auto load_act = [&]() {
+        const int bb = min(blk, nblk - 1);
+        if constexpr (TY == KF_TYPE_Q4_K) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) xa4[k] = xl[64 * k];
+            xbs = *reinterpret_cast<const int2*>(ss + bb * 8 + 2 * j);
+            xdx = sd[bb * 8];
+        } else {
+            xa4[0] = xl[0];
+            xa4[1] = xl[64];
+            xa4[2] = xa4[3] = make_uint4(0u, 0u, 0u, 0u);
+            xdx = sd[bb];
+        }
+    };
     auto process = [&](const uint4* v, int it) {
         if (!(KF_GV_ABLATE & 4)) gv_park<TY>(wb, v, len, ln);
         __builtin_amdgcn_wave_barrier();
@@ -697,9 +739,9 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
             acc = (KF_GV_ABLATE & 4) ? (float)(v[0].x ^ v[1].y ^ v[2].z) : (float)(*reinterpret_cast<const uint32_t*>(wl) ^ xl[0].x);
         } else if (has_step && blk < nblk) {
             if constexpr (TY == KF_TYPE_Q4_K)
-                acc = gv_q4k_lane(wl, xl, ss, sd, blk, j);
+                acc = gv_q4k_lane_r(wl, xa4[0], xa4[1], xa4[2], xa4[3], xbs, xdx, j);
             else
-                acc = gv_q8_0_lane(wl, xl, sd, blk);
+                acc = gv_q8_0_lane_r(wl, xa4[0], xa4[1], xdx);
         }
         __builtin_amdgcn_wave_barrier();
         acc = kf_wave_sum_dpp(acc);
@@ -727,6 +769,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     // (__syncthreads would add a release fence that waits on the weight loads as well)
     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(63) & ~(15 << 8));
     __builtin_amdgcn_s_barrier();
+    load_act();
     KF_GV_STAMP(1)
     // a ring of D rows in flight: row it is multiplied while rows it+1 .. it+D-1 stream, then its registers take row
     // it+D
