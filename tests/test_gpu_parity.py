@@ -248,6 +248,29 @@ def test_gemv_launch_variants(cuda, monkeypatch, dma, maxit, ty, n, n_out):
     _close(y.cpu().numpy(), oracle.matmul_slice(ty, w, n, n_out, x))
 
 
+@pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 4096, 1030), (kf.TYPE_Q4_K, 4096, 6144), (kf.TYPE_Q8_0, 4096, 777),
+                                        (kf.TYPE_Q4_K, 2304, 9)])
+def test_gemv_one_shot_variant(cuda, monkeypatch, ty, n, n_out):
+    """The one-shot GEMV (every wave's row fetched straight into LDS at launch; KF_GEMV_ONESHOT=1, no longer the
+    default for any shape) against the default persistent variant, bit for bit, and the CPU backend."""
+    import torch
+
+    w = _tensor(_weights(ty, n_out, n, seed=37), cuda)
+    x = kf.synth_normal(38, 1.0, n).reshape(1, n)
+    act = kf.alloc_act(1, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.act_kind(ty))
+    outs = []
+    for one_shot in (False, True):
+        if one_shot:
+            monkeypatch.setenv("KF_GEMV_ONESHOT", "1")
+        y = torch.full((1, n_out), float("nan"), device=cuda)
+        kf.gemv(ty, w, act, y, 1, n, n_out)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    _close(outs[1], oracle.matmul_slice(ty, w.cpu().numpy(), n, n_out, x))
+
+
 @pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 256, 40), (kf.TYPE_Q4_K, 1280, 300), (kf.TYPE_Q4_K, 4096, 1030),
                                         (kf.TYPE_Q4_K, 2304, 777), (kf.TYPE_Q4_K, 14336, 64),
                                         (kf.TYPE_Q8_0, 32, 7), (kf.TYPE_Q8_0, 1056, 300), (kf.TYPE_Q8_0, 4096, 777),
