@@ -601,8 +601,14 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint8_t* rp = buf + C::B_OFF + ((wn * TN + j) * 32 + r32) * C::ROW + wo + g * KF_Q8_0_BYTES;
-                const u32x4_a2 v = *reinterpret_cast<const u32x4_a2*>(rp + 2 + 16 * half);
-                b[j] = v4i{(int)v.x, (int)v.y, (int)v.z, (int)v.w};
+                // the 16 weight bytes start 2 bytes past a dword boundary in even groups and on one in odd groups
+                // (windows and rows are 16-byte aligned, blocks 34 bytes): five aligned dwords and a byte realignment
+                // instead of a 2-byte aligned 16-byte read, which stalls the LDS
+                const int sh = (g & 1) ? 0 : 2;
+                const uint32_t* ap = reinterpret_cast<const uint32_t*>(rp + 2 + 16 * half - sh);
+                const uint32_t d0 = ap[0], d1 = ap[1], d2 = ap[2], d3 = ap[3], d4 = ap[4];
+                b[j] = v4i{(int)kf_alignbyte(d1, d0, sh), (int)kf_alignbyte(d2, d1, sh), (int)kf_alignbyte(d3, d2, sh),
+                           (int)kf_alignbyte(d4, d3, sh)};
                 ub[j].x = *reinterpret_cast<const uint16_t*>(rp);
             }
             v16i c[TM][TN];
