@@ -62,8 +62,12 @@ __device__ __forceinline__ void kf_q4k_lane(const uint4 hdr, const uint4 qa, con
     int dlo, dhi;
     kf_q4k_pair_dots(qa, qb, x0, x1, x2, x3, dlo, dhi);
     // 24-bit multiplies are exact here: scales and mins are 6-bit, |dot| <= 15*127*32 and |bsum| <= 128*32
-    isum = __mul24((int)(sc2 & 0xffu), dlo) + __mul24((int)(sc2 >> 8), dhi);
-    imin = __mul24((int)(m2 & 0xffu), bs0) + __mul24((int)(m2 >> 8), bs1);
+    // The empty asm hides what the compiler knows of sc2 and m2 (below 2^14) so that the byte masks stay in the
+    // block of the products: the products are matched to 24-bit multiplies only from ranges visible there, and the
+    // scale words come from another block (a full-width quarter-rate multiply otherwise)
+    asm("" : "+v"(sc2), "+v"(m2));
+    isum = __mul24((int)(sc2 & 0xffu), dlo) + __mul24((int)((sc2 >> 8) & 0xffu), dhi);
+    imin = __mul24((int)(m2 & 0xffu), bs0) + __mul24((int)((m2 >> 8) & 0xffu), bs1);
 }
 
 __device__ __forceinline__ int kf_q8_0_dot(const uint32_t* wq, const uint4 x0, const uint4 x1) {
