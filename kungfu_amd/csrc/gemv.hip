@@ -351,9 +351,16 @@ __device__ __forceinline__ float gv_q8_0_lane(const uint8_t* wl, const uint4* xs
 
 // gv_q8_0_lane with the activation side in registers (x0, x1 the lane's pieces, dx its block's scale)
 __device__ __forceinline__ float gv_q8_0_lane_r(const uint8_t* wl, const uint4 x0, const uint4 x1, float dx) {
-    const kf_u32x4_a2 q0 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 2);
-    const kf_u32x4_a2 q1 = *reinterpret_cast<const kf_u32x4_a2*>(wl + 18);
-    const uint32_t wq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    // the block's quants start 2 bytes past a dword boundary when its byte offset (34 x lane) is a multiple of 4: read
+    // nine aligned dwords and realign (v_alignbyte_b32) rather than 2-byte aligned 16-byte LDS reads
+    const uint32_t sh = (reinterpret_cast<uintptr_t>(wl) & 2u) ? 0u : 2u;
+    const uint32_t* ap = reinterpret_cast<const uint32_t*>(wl + 2 - sh);
+    uint32_t dw[9];
+#pragma unroll
+    for (int i = 0; i < 9; i++) dw[i] = ap[i];
+    uint32_t wq[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) wq[i] = kf_alignbyte(dw[i + 1], dw[i], sh);
     const int dt = kf_q8_0_dot(wq, x0, x1);
     return kf_h2f(*reinterpret_cast<const uint16_t*>(wl)) * dx * (float)dt;
 }
