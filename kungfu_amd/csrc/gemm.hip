@@ -243,7 +243,15 @@ __global__ void __launch_bounds__(GM_THREADS, 2) gemm_q8_0_kernel(const uint8_t*
 typedef long v1l;
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef int v4i_ __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+
+// The 8 bytes at a 2-byte aligned LDS address as a long: aligned dwords realigned by v_alignbyte_b32 (an LDS read
+// that is not dword aligned stalls). Reads only the dwords that hold the 8 bytes: a third one when they straddle it.
+__device__ __forceinline__ long sk_lds_u64_a2(const uint8_t* p) {
+    const uint32_t sh = (uint32_t)reinterpret_cast<uintptr_t>(p) & 2u;
+    const uint32_t* ap = reinterpret_cast<const uint32_t*>(p - sh);
+    const uint32_t d0 = ap[0], d1 = ap[1], d2 = ap[1 + (sh >> 1)];
+    return (long)kf_alignbyte(d1, d0, sh) | ((long)kf_alignbyte(d2, d1, sh) << 32);
+}
 
 // Ablation switch for measurement builds only (0 in the product): bit 1 drops the MFMA/VALU arithmetic, bit 2 the
 // LDS staging and operand reads, bit 4 the activation loads
@@ -380,8 +388,7 @@ __global__ void __launch_bounds__(512) gemm_q8_0_small_kernel(const uint8_t* __r
 #pragma unroll
             for (int j = 0; j < SK_TN; j++) {
                 const uint8_t* wp = lw + (16 * j + c) * SK_STRIDE + g * KF_Q8_0_BYTES;
-                const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
-                b[j] = (long)bv.x | ((long)bv.y << 32);
+                b[j] = sk_lds_u64_a2(wp + 2 + 8 * q);
                 sb[j] = v4h{};
                 sb[j][0] = q == 0 ? *reinterpret_cast<const _Float16*>(wp) : (_Float16)0.0f;
             }
@@ -788,8 +795,7 @@ __global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __r
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint8_t* wp = a_b + MR_ABUF + (16 * j + c) * MR_WCH + g * KF_Q8_0_BYTES;
-                const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
-                b[j] = (long)bv.x | ((long)bv.y << 32);
+                b[j] = sk_lds_u64_a2(wp + 2 + 8 * q);
                 dw[j] = (float)*reinterpret_cast<const _Float16*>(wp);
             }
 #pragma unroll
@@ -1002,8 +1008,7 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
 #pragma unroll
             for (int j = 0; j < TN; j++) {
                 const uint8_t* wp = wr + 16 * j * Geo::WCH + g * KF_Q8_0_BYTES;
-                const u32x2_a2 bv = *reinterpret_cast<const u32x2_a2*>(wp + 2 + 8 * q);
-                bq[j] = (long)bv.x | ((long)bv.y << 32);
+                bq[j] = sk_lds_u64_a2(wp + 2 + 8 * q);
                 const _Float16 dw = *reinterpret_cast<const _Float16*>(wp);
                 sb[j] = v4h{};
                 sb[j][0] = q == 0 ? dw : (_Float16)0.0f;
