@@ -192,7 +192,7 @@ int kf_hip_matmul_group(uint32_t ty, const void* w, int n_in, const float* x, in
 
 /* Pairs grouped by slot: offsets[s] .. offsets[s + 1] index `order`, which lists the pair indices of slot s in
  * increasing order (deterministic; the reference's atomic placement leaves it unspecified). offsets has n_slots + 1
- * entries; slots outside [0, n_slots) are skipped. Replaces moe_group (crates/kf-backend-cuda/src/kernels/moe.cu:118-141). */
+ * entries; slots outside [0, n_slots) are skipped; n_slots at most 4096. Replaces moe_group (crates/kf-backend-cuda/src/kernels/moe.cu:118-141). */
 int kf_hip_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, void* stream);
 
 /* Grouped expert product: for each slot s and each pair p of its group, y[p][o] = W_s[o] . x, x the activation row p
@@ -245,6 +245,16 @@ int kf_hip_block_ints(uint32_t ty, const void* w, int64_t row_bytes, const void*
  * per_thread (4, 8 or 16) pieces a thread, all requested at launch; writes at most one word to sink (4 bytes). No
  * reference counterpart: the measurement's HBM read peak on the box, reported beside the spec peak. */
 int kf_hip_stream_read(const void* buf, size_t bytes, int per_thread, uint32_t* sink, void* stream);
+
+/* Launch knobs (KF_GEMV_MAXIT, KF_GEMM_NO_TAIL, ... : the kernel-variant and tuning switches the launchers consult).
+ * The library reads each from its environment variable once per process, at the first knob query; afterwards only
+ * kf_hip_set_knob changes them (value < 0 unsets the knob; a flag knob is on for any value >= 0). Returns KF_E_INVALID
+ * for an unknown name. kf_hip_get_knob returns the value, -1 when unset, -2 for an unknown name. Knobs are
+ * process-wide: a change applies to launches made after it on every thread. No reference counterpart (the reference
+ * reads its KF_* variables with std::env at use, e.g. crates/kf-backend-cuda/src/exec.rs); these exist so tests and
+ * tuning can compare kernel variants without racing the environment. */
+int kf_hip_set_knob(const char* name, int value);
+int kf_hip_get_knob(const char* name);
 
 /* ---------------------------------------------------------------------------------------------------------------
  * Backend mirror (crates/kf-core/src/backend.rs:206-269 Backend; WeightSource :7-13). Host buffers in and out; the

@@ -78,6 +78,8 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_matmul_group": ([U, P, I, P, I, P, P, P, I, P], I),
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
         "kf_hip_stream_read": ([P, S, I, P, P], I),
+        "kf_hip_set_knob": ([ctypes.c_char_p, I], I),
+        "kf_hip_get_knob": ([ctypes.c_char_p], I),
         "kf_hip_rms_norm_matmul": ([U, P, I, I, P, I, P, P, ctypes.c_float, P, P, P, P, P], I),
         "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
         "kf_hip_moe_group": ([P, I, I, P, P, P], I),
@@ -128,6 +130,19 @@ def check(rc: int) -> int:
     if rc < 0:
         raise KfError(rc, last_error())
     return rc
+
+
+def set_knob(name: str, value) -> None:
+    """Sets a launch knob (kf_hip_set_knob): an int, True / False for a flag knob, or None to unset it."""
+    v = -1 if value is None or value is False else 1 if value is True else int(value)
+    check(lib().kf_hip_set_knob(name.encode(), v))
+
+
+def get_knob(name: str) -> int:
+    v = lib().kf_hip_get_knob(name.encode())
+    if v == -2:
+        raise KfError(KF_E_INVALID, f"unknown knob {name}")
+    return v
 
 
 def last_error() -> str:

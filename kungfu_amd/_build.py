@@ -19,7 +19,7 @@ OBJ_DIR = os.path.join(HERE, "build", "obj")
 
 ARCH = "gfx950"
 DEVICE_SOURCES = ["quant_act.hip", "gemv.hip", "gemv_k.hip", "gemm.hip", "gemm_q4k.hip", "gemm_kq.hip", "rows.hip", "rows_mma.hip", "noalloc.hip", "probe.hip"]
-HOST_SOURCES = ["api.cpp", "host_quant.cpp", "gguf.cpp"]
+HOST_SOURCES = ["api.cpp", "host_quant.cpp", "gguf.cpp", "knobs.cpp"]
 
 COMMON = ["-O3", "-fPIC", "-std=c++17", "-Wall", "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
 DEVICE_FLAGS = [f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-ffp-contract=fast-honor-pragmas"]

@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "kf_knobs.h"
 #include "../../include/kf_hip.h"
 #include "kf_host.h"
 #include "kf_layout.h"
@@ -118,13 +119,11 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // Row iterations per GEMV block (1, 2 or 4); KF_GEMV_MAXIT overrides the built-in choice (a tuning knob, like the
 // reference's KF_* environment knobs)
 int gemv_maxit() {
-    const char* e = getenv("KF_GEMV_MAXIT");
-    const int v = e ? atoi(e) : 0;
-    return v < 0 ? 0 : v;
+    return kf_knob_or(KF_KNOB_GEMV_MAXIT, 0);
 }
 
 // KF_MATMUL_NO_FUSE set: one-row matmuls quantize into `act` and run the GEMV as two launches (a comparison knob)
-bool no_fusion() { return getenv("KF_MATMUL_NO_FUSE") != nullptr; }
+bool no_fusion() { return kf_knob_on(KF_KNOB_MATMUL_NO_FUSE); }
 
 int product(uint32_t ty, const void* w, int64_t rb, const void* act, const float* bias, const float* res, float* y, int rows, int n_in,
             int n_out, void* stream);
@@ -220,7 +219,7 @@ int kf_hip_gemv(uint32_t ty, const void* w, int64_t row_bytes, const void* act, 
     hipStream_t s = static_cast<hipStream_t>(stream);
     // q5_K / q6_K: several rows on the matrix cores (16 activation rows a weight pass), one row (or a layout the
     // matrix-core form does not take: q6_K rows with an odd number of super-blocks) on their own per-lane product
-    if ((ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) && rows > 1 && !getenv("KF_ROWS_VALU") && kf_rows_mma_1_ok(ty, w, row_bytes, n, n_out, rows)) {
+    if ((ty == KF_TYPE_Q5_K || ty == KF_TYPE_Q6_K) && rows > 1 && !kf_knob_on(KF_KNOB_ROWS_VALU) && kf_rows_mma_1_ok(ty, w, row_bytes, n, n_out, rows)) {
         const kf_act_offsets o = kf_act_layout((size_t)rows, (size_t)n);
         const char* base = static_cast<const char*>(act);
         const hipError_t e = kf_launch_rows_mma_1(ty, w, row_bytes, reinterpret_cast<const int8_t*>(base + o.q), reinterpret_cast<const int32_t*>(base + o.s32),
@@ -330,7 +329,7 @@ static double q4k_gemm_us(int rows, int n_in, int n_out, bool kq) {
 // Which q4_K GEMM kf_hip_gemm_i8 runs: the one-MFMA-per-group kernel where it costs less (KF_Q4K_KQ=0 / 1 forces the
 // choice, a comparison knob)
 static bool q4k_gemm_kq_pays(int rows, int n_in, int n_out) {
-    if (const char* e = getenv("KF_Q4K_KQ")) return atoi(e) != 0;
+    if (kf_knob_on(KF_KNOB_Q4K_KQ)) return kf_knob(KF_KNOB_Q4K_KQ) != 0;
     return q4k_gemm_us(rows, n_in, n_out, true) < q4k_gemm_us(rows, n_in, n_out, false);
 }
 
@@ -353,7 +352,7 @@ static bool q4k_gemm_pays(int rows, int n_in, int n_out, int64_t row_bytes) {
 // full split over 2 or 4 K ranges). Fitted on MI355X at the Llama-3-8B gate and down shapes, 32-512 rows: the model
 // picks the faster product at every measured point. KF_KQ_GEMM=0 / 1 forces the choice (a comparison knob).
 static bool kq_gemm_pays(uint32_t ty, int rows, int n_in, int n_out, int64_t row_bytes) {
-    if (const char* e = getenv("KF_KQ_GEMM")) return atoi(e) != 0;
+    if (kf_knob_on(KF_KNOB_KQ_GEMM)) return kf_knob(KF_KNOB_KQ_GEMM) != 0;
     if (rows < 2) return false;
     const bool q6 = ty == KF_TYPE_Q6_K;
     const double mb = (double)n_out * row_bytes / 1e6;
@@ -492,7 +491,7 @@ int kf_hip_matmul_group(uint32_t ty, const void* w, int n_in, const float* x, in
 
 int kf_hip_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, void* stream) {
     if (total < 0 || n_slots < 1) return fail(KF_E_INVALID, "%d pairs over %d slots", total, n_slots);
-    if (n_slots > 16384) return fail(KF_E_UNSUPPORTED, "%d slots (at most 16384)", n_slots);
+    if (n_slots > 4096) return fail(KF_E_UNSUPPORTED, "%d slots (at most 4096)", n_slots);
     if ((total > 0 && (!slots || !order)) || !offsets) return fail(KF_E_INVALID, "null slot, order or offset pointer");
     const hipError_t e = kf_launch_moe_group(slots, total, n_slots, order, offsets, static_cast<hipStream_t>(stream));
     return e == hipSuccess ? KF_OK : hip_fail(e, "moe_group launch");
@@ -527,8 +526,7 @@ int kf_hip_moe_gemm(uint32_t ty, const void* w, const void* w2, int64_t expert_b
         return fail(KF_E_INVALID, "expert stride %lld for %d rows of %lld bytes (16-byte multiple)", (long long)expert_bytes, mat_rows, (long long)row_bytes);
     // the one-MFMA-per-group kernel (64-row tiles: less of each slot's partial tile idle; 839 against 894 us for the
     // split-scale kernel at 512 tokens top-2 over 8 experts) unless KF_MOE_KQ=0 (a comparison knob)
-    const char* ke = getenv("KF_MOE_KQ");
-    const bool kq = !(ke && atoi(ke) == 0) && row_bytes % 16 == 0 && aligned(w, 16);
+    const bool kq = kf_knob(KF_KNOB_MOE_KQ) != 0 && row_bytes % 16 == 0 && aligned(w, 16);
     const hipError_t e = kq ? kf_launch_gemm_kq_moe(w, w2, expert_bytes, row_bytes, w2 ? n_split : 0, act, pairs, n_slots, offsets, out_rows, y,
                                                     n_out, n, static_cast<hipStream_t>(stream))
                             : kf_launch_gemm_q4k_moe(w, w2, expert_bytes, row_bytes, w2 ? n_split : 0, act, pairs, n_slots, offsets, out_rows, y,

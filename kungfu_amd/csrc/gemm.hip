@@ -23,6 +23,7 @@
 //     gemm_q8_0_small_kernel takes over: a block owns 32 output columns, its W waves split K among themselves, every
 //     lane loads its MFMA operand pieces straight from memory (no LDS staging) several groups ahead, and the waves'
 //     partial tiles are summed in LDS in a fixed tree order.
+#include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_host.h"
 #include "kf_device.h"
@@ -1128,7 +1129,7 @@ hipError_t gemm_sk_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq,
     const int tiles = (N + Geo::BR - 1) / Geo::BR, chunks = K / (32 * G);
     int S = std::max(1, BPC * kf_cu_count() / tiles);
     S = std::min(S, std::max(1, chunks / 3));  // at least three chunks a split
-    if (const char* e = getenv("KF_GEMM_SK_S")) S = std::max(1, std::min(atoi(e), chunks));  // a comparison knob
+    if (kf_knob_on(KF_KNOB_GEMM_SK_S)) S = std::max(1, std::min(kf_knob(KF_KNOB_GEMM_SK_S), chunks));  // a comparison knob
     const size_t room = (KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4) / ((size_t)tiles * Geo::TILE * 4);
     S = std::min<int>(S, (int)std::min<size_t>(room, 1 << 20));
     if (tiles > KF_SPLIT_TICKETS || S < 1) return hipErrorNotSupported;
@@ -1162,7 +1163,7 @@ hipError_t gemm_q8_0_dma_launch(const uint8_t* w, int64_t row_bytes, const int8_
     const int slots = kf_cu_count() * (8 / (WM * WN)), rem = T % slots;
     const size_t part_bytes = (size_t)rem * 2 * TM * TN * 16 * C::THREADS * 4;
     if (rem > 0 && rem <= slots / 2 && K % 512 == 0 && K / GM_BK >= 4 && rem <= KF_SPLIT_TICKETS &&
-        part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !getenv("KF_GEMM_NO_TAIL")) {
+        part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !kf_knob_on(KF_KNOB_GEMM_NO_TAIL)) {
         if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
             tail = GmTail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), T - rem};
             blocks = T + rem;
@@ -1200,10 +1201,7 @@ hipError_t gemm_small_launch(const uint8_t* w, int64_t row_bytes, const int8_t* 
 // Waves per block of the small-batch kernel: enough blocks x waves to fill the GPU (about 4096 waves), at least two
 // chunks a wave, a power of two, at most four; KF_GEMM_SMALL_W overrides it (a tuning knob)
 int small_waves(int M, int N, int K, int rows_per_block) {
-    static const int forced = [] {
-        const char* e = getenv("KF_GEMM_SMALL_W");
-        return e ? atoi(e) : 0;
-    }();
+    const int forced = kf_knob_or(KF_KNOB_GEMM_SMALL_W, 0);
     const int cap = 4;  // measured: four waves (more chunks each) beat eight on every Llama shape at M = 8..64
     const int rblocks = (M + 15) / 16;
     if (forced == 1 || forced == 2 || forced == 4 || forced == 8) return forced;
@@ -1226,7 +1224,7 @@ int kf_gemm_k_multiple() { return GM_BK; }
 // block a CU (a last round at most half full as K halves: half a round; the kernel is VALU-bound, so a second block
 // on a CU does not shorten a round). KF_GEMM_SLICE=0 / 1 forces the choice (a comparison knob).
 static bool q8_0_slices_pay(int M, int N, int K, int64_t row_bytes) {
-    if (const char* e = getenv("KF_GEMM_SLICE")) return atoi(e) != 0;
+    if (kf_knob_on(KF_KNOB_GEMM_SLICE)) return kf_knob(KF_KNOB_GEMM_SLICE) != 0;
     const double mb = (double)N * row_bytes / 1e6;
     const double t_slices = ((M + 63) / 64) * (9.0 + 0.45 * mb);
     const int cus = kf_cu_count();
@@ -1244,11 +1242,9 @@ static hipError_t small_q8_0(const uint8_t* wb, int64_t row_bytes, const int8_t*
     // rows: QKV 17.0 / 23.4 against 21.1 / 28.4 us, gate 26.4 / 38.2 against 35.6 / 50.0, down 27.8 / 38.9
     // against 31.4 / 48.0; O at 4096 x 4096 15.2 / 20.5 against 12.1 / 18.4, so not there). KF_GEMM_SK=0 turns
     // it off, KF_GEMM_SK=1 on for every size (comparison knobs)
-    const char* ske = getenv("KF_GEMM_SK");
-    const bool sk = ske ? atoi(ske) != 0 : (int64_t)N * K > (1ll << 24);
+    const bool sk = kf_knob_on(KF_KNOB_GEMM_SK) ? kf_knob(KF_KNOB_GEMM_SK) != 0 : (int64_t)N * K > (1ll << 24);
     if (M > 16 && M <= 64 && K % 128 == 0 && (K / 32) % 2 == 0 && sk) {
-        const char* ve = getenv("KF_GEMM_SK_V");  // 10 G + NS (groups a chunk, ring stages): a tuning knob
-        const int var = ve ? atoi(ve) : 0;
+        const int var = kf_knob_or(KF_KNOB_GEMM_SK_V, 0);  // 10 G + NS (groups a chunk, ring stages): a tuning knob
         // 8-group chunks in two stages where K allows (MI355X, Llama-3-8B shapes at 32 / 64 rows: gate 25.1 / 37.2
         // against 26.0 / 38.3 us with 4-group chunks in three, down 24.5 / 37.4 against 25.3 / 39.3)
         const int v = var ? var : K % 256 == 0 ? 82 : 43;
@@ -1267,22 +1263,18 @@ static hipError_t small_q8_0(const uint8_t* wb, int64_t row_bytes, const int8_t*
         }
         if (e != hipErrorNotSupported) return e;
     }
-    if (M > 48 && M <= MR_ROWS && K % (32 * MR_G) == 0 && !getenv("KF_GEMM_NO_MR")) {
+    if (M > 48 && M <= MR_ROWS && K % (32 * MR_G) == 0 && !kf_knob_on(KF_KNOB_GEMM_NO_MR)) {
         // 49..64 rows in one weight pass where it measured faster than four 16-row blocks (MI355X, Llama-3-8B
         // shapes at 64 rows: O 18.4 against 21.6 us, down 48.3 against 57.0, gate 49.8 against 55.2; QKV and
         // 17..48 rows: no gain). One 16-row weight tile a block, 4 waves splitting K for N <= 4096 (too few tiles
         // otherwise), one wave for wide outputs. KF_GEMM_MR=11 / 14 forces a variant (a comparison knob)
-        const char* fe = getenv("KF_GEMM_MR");
-        const int v = fe ? atoi(fe) : N >= 8192 ? 11 : N <= 4096 ? 14 : 0;
+        const int v = kf_knob_or(KF_KNOB_GEMM_MR, N >= 8192 ? 11 : N <= 4096 ? 14 : 0);
         if (v == 11) return gemm_mr_launch<1, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
         if (v == 14) return gemm_mr_launch<1, 4>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
     }
     if (M <= 64) {  // M / 16 row blocks
         // one 16-column tile a wave when that still gives at most one block per CU (a block holds a CU), else two
-        static const int tn = [] {  // KF_GEMM_SMALL_TN: a tuning knob
-            const char* e = getenv("KF_GEMM_SMALL_TN");
-            return e ? atoi(e) : 0;
-        }();
+        const int tn = kf_knob_or(KF_KNOB_GEMM_SMALL_TN, 0);  // a tuning knob
         if (tn == 1 || (tn != 2 && (int64_t)((N + 15) / 16) * ((M + 15) / 16) <= kf_cu_count()))
             return gemm_small_launch<16, 1>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 16), s);
         return gemm_small_launch<16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, small_waves(M, N, K, 32), s);
@@ -1298,7 +1290,7 @@ hipError_t kf_launch_gemm_q8_0(const void* w, int64_t row_bytes, const void* act
     const auto* xd = reinterpret_cast<const float*>(base + o.d32);
     const auto* wb = static_cast<const uint8_t*>(w);
     // the small-batch kernels read whole 16-byte pieces of rows, which needs 16-byte aligned rows (K % 256 == 0)
-    if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31) && !getenv("KF_GEMM_TILE")) {
+    if (K % 256 == 0 && row_bytes % 16 == 0 && (int64_t)N * row_bytes < (1ll << 31) && (int64_t)M * K < (1ll << 31) && !kf_knob_on(KF_KNOB_GEMM_TILE)) {
         if (M <= 64) {
             const hipError_t e = small_q8_0(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
             if (e != hipErrorNotSupported) return e;

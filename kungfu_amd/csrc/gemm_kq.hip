@@ -20,6 +20,7 @@
 // mins operands. Every DMA instruction reads whole 16-byte pieces of consecutive rows, issued through inline assembly
 // with explicit waits; rows past M or N read as zeros through the hardware range check. Blocks run in XCD order (each
 // XCD a contiguous range of tiles, M fastest), so the blocks in flight on an XCD share their weight tiles in its L2.
+#include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_device.h"
 #include "kf_host.h"
@@ -430,7 +431,7 @@ hipError_t kf_launch_gemm_kq(uint32_t ty, const void* w, int64_t row_bytes, cons
     const int cus = kf_cu_count(), rem = T % cus;
     const int S = kq_splits(T, K / 256, cus);
     const size_t part_bytes = (size_t)rem * S * KQ_TM * 16 * KQ_THREADS * 4;
-    if (S > 1 && rem <= KF_SPLIT_TICKETS && part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !getenv("KF_GEMM_NO_TAIL")) {
+    if (S > 1 && rem <= KF_SPLIT_TICKETS && part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !kf_knob_on(KF_KNOB_GEMM_NO_TAIL)) {
         if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
             tail = KqTail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), T - rem, S};
             blocks = T - rem + rem * S;

@@ -34,6 +34,7 @@
 // Measured at M = 2048 (ablation builds, us): gate/up 333 in all (MFMA with its LDS operand reads alone 147, the
 // staging alone 91), each of the staging, the plane expansion and the rescale adding 50-60 us: the matrix core and the
 // VALU of one wave still mostly take turns, which is what bounds the kernel.
+#include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_device.h"
 #include "kf_host.h"
@@ -435,7 +436,7 @@ hipError_t kf_launch_gemm_q4k(const void* w, int64_t row_bytes, const void* act,
     const int cus = kf_cu_count(), rem = T % cus;
     const size_t part_bytes = (size_t)rem * 2 * G4_TM * 16 * G4_THREADS * 4;
     if (rem > 0 && rem <= cus / 2 && K / 256 >= 4 && rem <= KF_SPLIT_TICKETS &&
-        part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !getenv("KF_GEMM_NO_TAIL")) {
+        part_bytes <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !kf_knob_on(KF_KNOB_GEMM_NO_TAIL)) {
         if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
             tail = G4Tail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), T - rem};
             blocks = T + rem;

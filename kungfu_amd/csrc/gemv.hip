@@ -16,6 +16,7 @@
 //   * Integer dots use v_dot4_i32_i8; the per-block float combine happens per lane; one wave reduction per row.
 #include <type_traits>
 
+#include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_host.h"
 #include "kf_qa.h"
@@ -948,12 +949,12 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
     const int want = maxit_env > 0 ? maxit_env : KF_GV_MAXIT;
     // the DMA variant needs 16-byte aligned rows and activation pieces
     const bool dma = row_bytes % 16 == 0 && (reinterpret_cast<uintptr_t>(w) & 15) == 0 &&
-                     (reinterpret_cast<uintptr_t>(fused ? static_cast<const void*>(xf) : xq) & 15) == 0 && !getenv("KF_GEMV_NO_DMA");
+                     (reinterpret_cast<uintptr_t>(fused ? static_cast<const void*>(xf) : xq) & 15) == 0 && !kf_knob_on(KF_KNOB_GEMV_NO_DMA);
     if (fused && (SPW != 1 || !dma)) return hipErrorNotSupported;
     // one-shot waves, each fetching its row straight into LDS, the whole matrix requested at launch (KF_GEMV_ONESHOT=1,
     // a comparison knob: one row a wave and every block resident at once). The persistent variant below measured
     // faster on q4_K QKV and O (5.34 / 4.25 us against 5.44 / 4.71) and level on q8_0, so it takes them too
-    if (!fused && SPW == 1 && WPR == 1 && dma && maxit_env == 0 && getenv("KF_GEMV_ONESHOT")) {
+    if (!fused && SPW == 1 && WPR == 1 && dma && maxit_env == 0 && kf_knob_on(KF_KNOB_GEMV_ONESHOT)) {
         const size_t smem = gd_lds(TY, n, 1, WPR, 1, 1).total;
         GvKernel k = gemv_dma_kernel<TY, 1, WPR, 1>;
         if (groups <= cu_count() * resident_blocks(k, smem) && smem <= 65536) {
@@ -962,19 +963,16 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         }
     }
     // the pipelined persistent variant: a resident grid, every wave walking its rows two in flight
-    if (SPW == 1 && dma && (fused || !getenv("KF_GEMV_NO_PIPE"))) {
-        static const int depth = [] {
-            const char* e = getenv("KF_GEMV_DEPTH");
-            const int v = e ? atoi(e) : 0;
-            return v >= 2 && v <= 4 ? v : KF_GV_DEPTH;
-        }();
+    if (SPW == 1 && dma && (fused || !kf_knob_on(KF_KNOB_GEMV_NO_PIPE))) {
+        const int dv = kf_knob(KF_KNOB_GEMV_DEPTH);
+        const int depth = dv >= 2 && dv <= 4 ? dv : KF_GV_DEPTH;
         GvKernel k = fused ? gv_fused_pipe<TY, WPR>(qx, norm != nullptr)
                            : depth == 4 ? gemv_pipe_kernel<TY, WPR, 4> : depth == 3 ? gemv_pipe_kernel<TY, WPR, 3> : gemv_pipe_kernel<TY, WPR, 2>;
         const size_t base_lds = gd_lds(TY, n, 0, WPR, 1, 1).total;
         // two blocks (16 waves) per CU measured best on MI355X (3.9-4.1 TB/s at 33 MB against 3.2-3.5 with every
         // resident slot filled, where waves contend for the memory pipe); KF_GEMV_BPC overrides it
-        const char* e = getenv("KF_GEMV_BPC");
-        const int per_cu = e && atoi(e) > 0 ? atoi(e) : std::min(2, resident_blocks(k, base_lds + (WPR > 1 ? 2048 : 0)));
+        const int bpc = kf_knob(KF_KNOB_GEMV_BPC);
+        const int per_cu = bpc > 0 ? bpc : std::min(2, resident_blocks(k, base_lds + (WPR > 1 ? 2048 : 0)));
         int grid = cu_count() * per_cu;
         if (grid > groups) grid = groups;
         const int iters = (groups + grid - 1) / grid;

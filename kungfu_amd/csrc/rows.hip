@@ -17,6 +17,7 @@
 // one lane a block). Activation rows sit in LDS wave-transposed (a lane's 16-byte pieces are contiguous across the
 // wave, conflict free), with their per-32 integer sums and scales. The next row's weights are requested before the
 // current row is multiplied.
+#include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_host.h"
 
@@ -310,68 +311,93 @@ __global__ void __launch_bounds__((rw_threads<STEPS, GLU>())) rows_kernel(const 
     }
 }
 
-// Pairs grouped by slot: counts by LDS atomics (order-free), offsets by one thread, then wave 0 places the pairs of
-// each 64-pair window in pair order, slot by slot (ballot ranks), so the order is deterministic. Slots < 0 or
-// >= n_slots are skipped.
-__global__ void __launch_bounds__(256) moe_group_kernel(const int32_t* __restrict__ slots, int total, int n_slots, int32_t* __restrict__ order,
-                                                        int32_t* __restrict__ offsets) {
-    extern __shared__ int cnt[];
-    for (int i = threadIdx.x; i < n_slots; i += blockDim.x) cnt[i] = 0;
-    __syncthreads();
-    for (int i = threadIdx.x; i < total; i += blockDim.x) {
-        const int s = slots[i];
-        if (s >= 0 && s < n_slots) atomicAdd(&cnt[s], 1);
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int run = 0;
-        for (int i = 0; i < n_slots; i++) {
-            const int c = cnt[i];
-            offsets[i] = run;
-            cnt[i] = run;
-            run += c;
-        }
-        offsets[n_slots] = run;
-    }
-    __syncthreads();
-    if (threadIdx.x >= 64) return;
-    const int lane = threadIdx.x;
-    for (int base = 0; base < total; base += 64) {
+// Stable grouping of the routed pairs by slot, as a parallel counting sort in one block of KF_GROUP_WAVES waves with
+// no atomics. The pairs are cut into one 64-aligned run per wave. Pass 1: each wave counts its run per slot into its
+// own column of tab[slot][wave] (one ballot per distinct slot of a 64-pair window; only the window's leader lane
+// writes). Scan: wave 0 turns tab into exclusive bases, slot-major and wave-minor (a shuffle prefix over 64 entries at
+// a time plus a running carry), so slot s starts at offsets[s] and within it the runs follow wave order. Pass 2: each
+// wave walks its run again and writes every pair at its slot's running base plus its ballot rank. Pair order is
+// therefore kept within a slot, and the result does not depend on timing. Slots < 0 or >= n_slots are skipped.
+constexpr int KF_GROUP_WAVES = 4;
+
+template <bool PLACE>
+__device__ __forceinline__ void moe_group_walk(const int32_t* __restrict__ slots, int b, int e, int n_slots, int* tab, int wave, int lane,
+                                               int32_t* __restrict__ order) {
+    for (int base = b; base < e; base += 64) {
         const int i = base + lane;
-        const int s = i < total ? slots[i] : -1;
-        bool todo = s >= 0 && s < n_slots;
-        uint64_t left = __ballot(todo);
+        const int s = i < e ? slots[i] : -1;
+        const bool live = s >= 0 && s < n_slots;
+        uint64_t left = __ballot(live);
         while (left) {
             const int leader = __builtin_ctzll(left);
             const int sv = __shfl(s, leader, 64);
-            const uint64_t m = __ballot(todo && s == sv);
-            const int start = cnt[sv];
-            if (todo && s == sv) {
-                order[start + __popcll(m & ((1ull << lane) - 1))] = i;
-                todo = false;
-            }
-            if (lane == leader) cnt[sv] = start + __popcll(m);
-            left &= ~m;
+            const uint64_t same = __ballot(live && s == sv);
+            int* cell = tab + sv * KF_GROUP_WAVES + wave;
+            const int at = *cell;
+            if (PLACE && live && s == sv) order[at + __popcll(same & ((1ull << lane) - 1))] = i;
+            if (lane == leader) *cell = at + __popcll(same);
+            left &= ~same;
         }
     }
 }
 
-// out[r][o] = sum over j of the row's pairs rj = r * n_used + j with 0 <= slots[rj] < n_slots of
-// wts[rj] * scale * part[rj][o] (+ host[r][o]), j in order; pairs outside the slots were skipped by the grouping, so
-// their part rows were never written
-__global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ part, const float* __restrict__ wts, const int32_t* __restrict__ slots,
-                                                          const float* __restrict__ host, float* __restrict__ out, int rows, int n_used, int n_embd,
-                                                          float scale, int n_slots) {
-    const int64_t total = (int64_t)rows * n_embd;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / n_embd, o = i - r * n_embd;
-        float acc = 0.0f;
-        for (int j = 0; j < n_used; j++) {
-            const int64_t rj = r * n_used + j;
-            if (slots[rj] >= 0 && slots[rj] < n_slots) acc += wts[rj] * scale * part[rj * n_embd + o];
+__global__ void __launch_bounds__(64 * KF_GROUP_WAVES) moe_group_kernel(const int32_t* __restrict__ slots, int total, int n_slots,
+                                                                        int32_t* __restrict__ order, int32_t* __restrict__ offsets) {
+    extern __shared__ int tab[];  // [n_slots][KF_GROUP_WAVES]
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int cells = n_slots * KF_GROUP_WAVES;
+    for (int i = threadIdx.x; i < cells; i += blockDim.x) tab[i] = 0;
+    __syncthreads();
+    const int run = ((total + KF_GROUP_WAVES - 1) / KF_GROUP_WAVES + 63) & ~63;
+    const int b = min(total, wave * run), e = min(total, b + run);
+    moe_group_walk<false>(slots, b, e, n_slots, tab, wave, lane, order);
+    __syncthreads();
+    if (wave == 0) {
+        int carry = 0;
+        for (int c = 0; c < cells; c += 64) {
+            const int k = c + lane;
+            const int v = k < cells ? tab[k] : 0;
+            int inc = v;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const int up = __shfl_up(inc, d, 64);
+                if (lane >= d) inc += up;
+            }
+            if (k < cells) {
+                tab[k] = carry + inc - v;
+                if (k % KF_GROUP_WAVES == 0) offsets[k / KF_GROUP_WAVES] = carry + inc - v;
+            }
+            carry += __shfl(inc, 63, 64);
         }
-        out[i] = acc + (host ? host[i] : 0.0f);
+        if (lane == 0) offsets[n_slots] = carry;
     }
+    __syncthreads();
+    moe_group_walk<true>(slots, b, e, n_slots, tab, wave, lane, order);
+}
+
+// Weighted sum of each token's expert outputs: out[r][o] = sum over j = 0..n_used-1 (in that order) of
+// (wts[r n_used + j] scale) part[r n_used + j][o] over the pairs whose slot is in [0, n_slots), plus host[r][o]
+// (nullable). Block r chunks + c covers columns [c, c + 1) x 256 V of token r: the pair weights and slot checks are wave-uniform and
+// read once per block; the columns move as V-wide vectors. Pairs outside the slots were skipped by the grouping, so
+// their part rows were never written and are not read.
+template <int V>
+__global__ void __launch_bounds__(256) moe_combine_kernel(const float* __restrict__ part, const float* __restrict__ wts, const int32_t* __restrict__ slots,
+                                                          const float* __restrict__ host, float* __restrict__ out, int n_used, int n_embd,
+                                                          float scale, int n_slots, int chunks) {
+    using vec = float __attribute__((ext_vector_type(V)));
+    const int64_t r = blockIdx.x / chunks;
+    const int o = ((blockIdx.x - (int)r * chunks) * 256 + threadIdx.x) * V;
+    if (o >= n_embd) return;
+    vec acc = (vec)0.0f;
+    for (int j = 0; j < n_used; j++) {
+        const int64_t p = r * n_used + j;
+        const int sl = slots[p];
+        if (sl < 0 || sl >= n_slots) continue;
+        const float w = wts[p] * scale;
+        acc += w * *reinterpret_cast<const vec*>(part + p * n_embd + o);
+    }
+    if (host) acc += *reinterpret_cast<const vec*>(host + r * n_embd + o);
+    *reinterpret_cast<vec*>(out + r * n_embd + o) = acc;
 }
 
 template <uint32_t TY, int RMAX, bool GLU, int STEPS>
@@ -450,7 +476,7 @@ hipError_t kf_launch_rows(uint32_t ty, const void* w, const void* w2, int64_t ex
     const auto* wb = static_cast<const uint8_t*>(w);
     const auto* ub = static_cast<const uint8_t*>(w2);
     // q4_K: the matrix-core form (rows_mma.hip); KF_ROWS_VALU=1 keeps the per-lane dot form (a measurement switch)
-    static const bool valu = getenv("KF_ROWS_VALU") != nullptr;
+    const bool valu = kf_knob_on(KF_KNOB_ROWS_VALU);
     // the activation rows a slot gets on average (grouped: every pair of act_rows x n_used, or one per row)
     const int slots = offsets ? n_slots : 1;
     const int avg_rows = offsets ? (per_slot ? act_rows : act_rows * n_used) / std::max(1, slots) : pairs;
@@ -500,15 +526,23 @@ hipError_t kf_launch_moe_gather_act(const void* src, int src_rows, void* dst, in
 }
 
 hipError_t kf_launch_moe_group(const int32_t* slots, int total, int n_slots, int32_t* order, int32_t* offsets, hipStream_t s) {
-    moe_group_kernel<<<1, 256, (size_t)n_slots * sizeof(int), s>>>(slots, total, n_slots, order, offsets);
+    moe_group_kernel<<<1, 64 * KF_GROUP_WAVES, (size_t)n_slots * KF_GROUP_WAVES * sizeof(int), s>>>(slots, total, n_slots, order, offsets);
     return hipGetLastError();
 }
 
 hipError_t kf_launch_moe_combine(const float* part, const float* wts, const int32_t* slots, const float* host, float* out, int rows, int n_used,
                                  int n_embd, float scale, int n_slots, hipStream_t s) {
-    const int64_t total = (int64_t)rows * n_embd;
-    if (total == 0) return hipSuccess;
-    const int grid = (int)std::min<int64_t>((total + 255) / 256, 4096);
-    moe_combine_kernel<<<grid, 256, 0, s>>>(part, wts, slots, host, out, rows, n_used, n_embd, scale, n_slots);
+    if (rows == 0 || n_embd == 0) return hipSuccess;
+    // float4 columns when every row starts 16-byte aligned, else single columns
+    const bool v4 = n_embd % 4 == 0 && reinterpret_cast<uintptr_t>(part) % 16 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(host) % 16 == 0;
+    const int per = v4 ? 1024 : 256;
+    const int chunks = (n_embd + per - 1) / per;
+    const int64_t blocks = (int64_t)chunks * rows;
+    if (blocks > INT32_MAX) return hipErrorInvalidValue;
+    if (v4)
+        moe_combine_kernel<4><<<(unsigned)blocks, 256, 0, s>>>(part, wts, slots, host, out, n_used, n_embd, scale, n_slots, chunks);
+    else
+        moe_combine_kernel<1><<<(unsigned)blocks, 256, 0, s>>>(part, wts, slots, host, out, n_used, n_embd, scale, n_slots, chunks);
     return hipGetLastError();
 }

@@ -28,6 +28,7 @@
 // rows by DMA, in K phases when all n columns do not fit beside the weight buffers.
 // Measured (Mixtral-style layer, 8 Q4_K experts, 16 tokens top-2): fused gate/up 129 us against 203 us for the
 // per-lane form.
+#include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_host.h"
 
@@ -334,10 +335,7 @@ RmPlan rm_plan(int n, int n_out, int slots, bool glu, int avg_rows) {
         const int nph = (nsb + max_sb - 1) / max_sb;
         pl.kc = ((nsb + nph - 1) / nph) * KF_Q4_K_BLOCK;  // balanced phases
     }
-    static const int forced_nb = [] {  // KF_RM_NB: a measurement knob (2 or 3 buffers)
-        const char* e = getenv("KF_RM_NB");
-        return e ? atoi(e) : 0;
-    }();
+    const int forced_nb = kf_knob_or(KF_KNOB_RM_NB, 0);  // a measurement knob (2 or 3 buffers)
     if (forced_nb == 2) pl.nb = 2;
     if (pl.kc < n) {
         pl.rpb = 16 * RM_WAVES;
@@ -351,10 +349,7 @@ RmPlan rm_plan(int n, int n_out, int slots, bool glu, int avg_rows) {
         // tiles a block: enough that the slots' blocks fill one round, at least one a wave, at most 16 a wave; not
         // necessarily a multiple of the waves (C5: 28 tiles a block, 256 blocks, where whole tiles a wave gave 32 and
         // 224 blocks, leaving 32 CUs idle)
-        static const int whole = [] {  // KF_RM_WHOLE=1: whole tiles a wave (a comparison knob)
-            const char* e = getenv("KF_RM_WHOLE");
-            return e ? atoi(e) : 0;
-        }();
+        const int whole = kf_knob_or(KF_KNOB_RM_WHOLE, 0);  // 1: whole tiles a wave (a comparison knob)
         int tpb = std::max(RM_WAVES, std::min(16 * RM_WAVES, (tiles + want - 1) / want));
         if (whole) tpb = RM_WAVES * std::max(1, std::min(16, (tiles + want * RM_WAVES - 1) / (want * RM_WAVES)));
         pl.rpb = 16 * tpb;
@@ -653,10 +648,7 @@ hipError_t kf_launch_rows_mma_1(uint32_t ty, const void* w, int64_t row_bytes, c
                                 int n_out, int rows, const float* bias, const float* res, float* y, hipStream_t s) {
     if (!kf_rows_mma_1_ok(ty, w, row_bytes, n, n_out, rows)) return hipErrorInvalidValue;
     const int tiles = (n_out + 15) / 16;
-    static const int forced = [] {  // KF_RM1_TILES: a tuning knob (1, 2, 4 or 8 tiles a block)
-        const char* e = getenv("KF_RM1_TILES");
-        return e ? atoi(e) : 0;
-    }();
+    const int forced = kf_knob_or(KF_KNOB_RM1_TILES, 0);  // a tuning knob (1, 2, 4 or 8 tiles a block)
     // a block's two stage buffers per wave hold most of a CU's LDS, so one block runs per CU: the fewest tiles a block
     // whose grid still fits in one round of the CUs (QKV at 4096 x 6144: 192 blocks of two tiles, 8.5 us at 8 rows,
     // against 384 blocks of one tile in two rounds, 10.7 us)

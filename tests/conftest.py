@@ -23,3 +23,37 @@ def cuda():
 
     kungfu_amd.lib()
     return torch.device("cuda:0")
+
+
+class _Knobs:
+    """Launch knobs set through kf_hip_set_knob for one test; each touched knob gets its old value back afterwards."""
+
+    def __init__(self):
+        self.saved = {}
+
+    def setenv(self, name, value):
+        import kungfu_amd
+
+        if name not in self.saved:
+            self.saved[name] = kungfu_amd.get_knob(name)
+        kungfu_amd.set_knob(name, int(value))
+
+    def delenv(self, name, raising=False):
+        import kungfu_amd
+
+        if name not in self.saved:
+            self.saved[name] = kungfu_amd.get_knob(name)
+        kungfu_amd.set_knob(name, None)
+
+    def restore(self):
+        import kungfu_amd
+
+        for name, v in self.saved.items():
+            kungfu_amd.set_knob(name, v)
+
+
+@pytest.fixture
+def knobs():
+    k = _Knobs()
+    yield k
+    k.restore()

@@ -46,22 +46,55 @@ def _routing(rows, n_used, n_exp, seed, drop=0.0):
     return sel, wts
 
 
-@pytest.mark.parametrize("total,n_slots,seed", [(32, 8, 0), (1, 1, 1), (1000, 64, 2), (300, 3, 3), (0, 4, 4)])
+@pytest.mark.parametrize("total,n_slots,seed", [(32, 8, 0), (1, 1, 1), (1000, 64, 2), (300, 3, 3), (0, 4, 4), (63, 5, 5), (257, 7, 6),
+                                                (20000, 4096, 7), (4097, 1, 8), (65, 300, 9)])
 def test_moe_group_is_a_stable_grouping(cuda, total, n_slots, seed):
+    """Stable counting sort against numpy's stable argsort; ids past n_slots and below 0 are skipped. The sizes cover
+    runs shorter than a wave, ragged last windows, one slot, and the slot limit."""
     import torch
 
     rng = np.random.default_rng(seed)
-    slots = rng.integers(-1, n_slots, total).astype(np.int32)
+    slots = rng.integers(-1, n_slots + 2, total).astype(np.int32)
+    slots[slots >= n_slots] = n_slots + 3 if n_slots > 1 else slots[slots >= n_slots]
     order = torch.full((max(total, 1),), -7, dtype=torch.int32, device=cuda)
     offsets = torch.full((n_slots + 1,), -7, dtype=torch.int32, device=cuda)
     kf.moe_group(_t(slots, cuda) if total else None, total, n_slots, order, offsets)
     torch.cuda.synchronize()
-    valid = np.nonzero(slots >= 0)[0]
+    valid = np.nonzero((slots >= 0) & (slots < n_slots))[0]
     want_order = valid[np.argsort(slots[valid], kind="stable")]
     counts = np.bincount(slots[valid], minlength=n_slots)
     want_off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
     assert np.array_equal(offsets.cpu().numpy(), want_off)
     assert np.array_equal(order.cpu().numpy()[: len(valid)], want_order)
+
+
+@pytest.mark.parametrize("rows,n_used,n_embd,host", [(16, 2, 4096, False), (5, 3, 1030, True), (1, 1, 7, True), (3, 2, 2052, False)])
+def test_moe_combine_weighted_pair_sum(cuda, rows, n_used, n_embd, host):
+    """out[r] = sum_j (w_rj scale) part[rj] in j order (+ host[r]), pairs with a slot outside [0, n_slots) skipped:
+    against the same f32 operations in numpy (the kernel's fused multiply-adds round once where numpy's f64 emulation
+    may round twice, so the bar is a few f32 ulps)."""
+    import torch
+
+    rng = np.random.default_rng(rows * 7 + n_embd)
+    pairs = rows * n_used
+    part = rng.normal(0, 1, (pairs, n_embd)).astype(np.float32)
+    sel = rng.integers(-1, 4, pairs).astype(np.int32)
+    wts = rng.uniform(0.1, 1.0, pairs).astype(np.float32)
+    hst = rng.normal(0, 1, (rows, n_embd)).astype(np.float32) if host else None
+    scale = np.float32(0.75)
+    out = torch.full((rows, n_embd), np.nan, device=cuda)
+    kf.moe_combine(_t(part, cuda), _t(wts, cuda), _t(sel, cuda), out, rows, n_used, n_embd, float(scale),
+                   host=_t(hst, cuda) if host else None)
+    torch.cuda.synchronize()
+    want = np.zeros((rows, n_embd), np.float64)
+    for r in range(rows):
+        acc = np.zeros(n_embd, np.float32)
+        for j in range(n_used):
+            p = r * n_used + j
+            if sel[p] >= 0:
+                acc = (np.float64(wts[p] * scale) * part[p].astype(np.float64) + acc).astype(np.float32)
+        want[r] = acc + (hst[r] if host else 0)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=1e-6, atol=1e-6)
 
 
 @pytest.mark.parametrize("ty", [kf.TYPE_Q8_0, kf.TYPE_Q4_K])
@@ -285,12 +318,12 @@ def test_moe_ffn_128_experts_top_8(cuda, rows):
 
 @pytest.mark.parametrize("kq", ["0", "1"])
 @pytest.mark.parametrize("rows,n_exp", [(512, 8), (100, 3)])
-def test_moe_ffn_grouped_gemm_top_2(cuda, monkeypatch, rows, n_exp, kq):
+def test_moe_ffn_grouped_gemm_top_2(cuda, knobs, rows, n_exp, kq):
     """Past 64 routed pairs the q4_K layer runs on the grouped tile GEMM (KF_MOE_KQ: 0 the split-scale kernel, 128-row
     tiles; 1 the one-MFMA-per-group kernel, 64-row tiles): 512 tokens top-2 over eight experts (about 128 pairs an
     expert, several row tiles each), and 100 tokens over three (the last tile of a slot partial), with some pairs
     unused; sampled tokens against the CPU backend stage by stage and the float path."""
-    monkeypatch.setenv("KF_MOE_KQ", kq)
+    knobs.setenv("KF_MOE_KQ", kq)
     n_embd, n_ff, n_used = 1024, 1536, 2
     args, got, stages = _moe_layer(cuda, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows, n_used, 70 + n_exp, drop=0.05)
     assert "gu" in stages
@@ -302,12 +335,12 @@ def test_moe_ffn_grouped_gemm_top_2(cuda, monkeypatch, rows, n_exp, kq):
     assert np.abs(got - flt).max() <= 2e-2 * max(np.abs(flt).mean(), 1e-6)
 
 
-def test_moe_ffn_config_c5_first_tokens(cuda):
-    """Config C5 at full size (8 experts of Q4_K 4096 -> 14336 -> 4096, 16 tokens, top-2): the first two tokens
-    against the CPU backend (every token is independent of the others)."""
+def test_moe_ffn_config_c5_every_token(cuda):
+    """Config C5 at full size (8 experts of Q4_K 4096 -> 14336 -> 4096, 16 tokens, top-2): all 16 tokens against the
+    CPU backend, stage by stage, and the layer against the CPU float path."""
     n_exp, n_embd, n_ff, rows, n_used = 8, 4096, 14336, 16, 2
     args, got, stages = _moe_layer(cuda, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows, n_used, 0)
-    _check_layer(got, stages, args, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, 2)
+    _check_layer(got, stages, args, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows)
 
 
 @pytest.mark.parametrize("ty,n", [(kf.TYPE_Q4_K, 1280), (kf.TYPE_Q4_K, 14336), (kf.TYPE_Q8_0, 1056), (kf.TYPE_Q8_0, 4096)])

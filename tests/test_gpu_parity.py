@@ -231,13 +231,13 @@ def test_backend_mirror_matmul_and_slices(cuda):
 @pytest.mark.parametrize("maxit", ["1", "2", "4"])
 @pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 4096, 1030), (kf.TYPE_Q4_K, 14336, 77), (kf.TYPE_Q8_0, 4096, 777),
                                         (kf.TYPE_Q8_0, 14336, 45), (kf.TYPE_Q4_K, 32768, 9)])
-def test_gemv_launch_variants(cuda, monkeypatch, dma, maxit, ty, n, n_out):
+def test_gemv_launch_variants(cuda, knobs, dma, maxit, ty, n, n_out):
     """Both GEMV kernels (direct-to-LDS and register-staged) at every row-iteration count agree with the CPU backend."""
     import torch
 
-    monkeypatch.setenv("KF_GEMV_MAXIT", maxit)
+    knobs.setenv("KF_GEMV_MAXIT", maxit)
     if not dma:
-        monkeypatch.setenv("KF_GEMV_NO_DMA", "1")
+        knobs.setenv("KF_GEMV_NO_DMA", "1")
     w = _weights(ty, n_out, n, seed=31)
     x = kf.synth_normal(32, 1.0, n).reshape(1, n)
     act = kf.alloc_act(1, n, cuda)
@@ -250,7 +250,7 @@ def test_gemv_launch_variants(cuda, monkeypatch, dma, maxit, ty, n, n_out):
 
 @pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 4096, 1030), (kf.TYPE_Q4_K, 4096, 6144), (kf.TYPE_Q8_0, 4096, 777),
                                         (kf.TYPE_Q4_K, 2304, 9)])
-def test_gemv_one_shot_variant(cuda, monkeypatch, ty, n, n_out):
+def test_gemv_one_shot_variant(cuda, knobs, ty, n, n_out):
     """The one-shot GEMV (every wave's row fetched straight into LDS at launch; KF_GEMV_ONESHOT=1, no longer the
     default for any shape) against the default persistent variant, bit for bit, and the CPU backend."""
     import torch
@@ -262,7 +262,7 @@ def test_gemv_one_shot_variant(cuda, monkeypatch, ty, n, n_out):
     outs = []
     for one_shot in (False, True):
         if one_shot:
-            monkeypatch.setenv("KF_GEMV_ONESHOT", "1")
+            knobs.setenv("KF_GEMV_ONESHOT", "1")
         y = torch.full((1, n_out), float("nan"), device=cuda)
         kf.gemv(ty, w, act, y, 1, n, n_out)
         torch.cuda.synchronize()
@@ -275,7 +275,7 @@ def test_gemv_one_shot_variant(cuda, monkeypatch, ty, n, n_out):
                                         (kf.TYPE_Q4_K, 2304, 777), (kf.TYPE_Q4_K, 14336, 64),
                                         (kf.TYPE_Q8_0, 32, 7), (kf.TYPE_Q8_0, 1056, 300), (kf.TYPE_Q8_0, 4096, 777),
                                         (kf.TYPE_Q8_0, 2080, 45), (kf.TYPE_Q8_0, 4128, 9)])
-def test_matmul_one_row_fused_equals_two_launches(cuda, monkeypatch, ty, n, n_out):
+def test_matmul_one_row_fused_equals_two_launches(cuda, knobs, ty, n, n_out):
     """kf_hip_matmul at one row quantizes inside the GEMV (one launch; up to 4096 columns, past that the two launches):
     the same integers and scales as quant_act, so its outputs equal quant_act + kf_hip_gemv bit for bit, with bias and
     residual, on a row with an all-zero block, ties and a negative maximum; and the CPU backend's within the f32 bar."""
@@ -297,7 +297,7 @@ def test_matmul_one_row_fused_equals_two_launches(cuda, monkeypatch, ty, n, n_ou
     y2 = torch.full((1, n_out), float("nan"), device=cuda)
     kf.quant_act(xt, act, kf.act_kind(ty))
     kf.gemv(ty, wt, act, y2, 1, n, n_out, bias=bt, res=rt)
-    monkeypatch.setenv("KF_MATMUL_NO_FUSE", "1")
+    knobs.setenv("KF_MATMUL_NO_FUSE", "1")
     y3 = torch.full((1, n_out), float("nan"), device=cuda)
     kf.matmul(ty, wt, xt, act, y3, n_out, bias=bt, res=rt)
     torch.cuda.synchronize()
@@ -558,14 +558,14 @@ def test_matmul_q8_0_small_batch_llama_shapes(cuda, shape, rows):
 
 @pytest.mark.parametrize("variant", ["11", "14"])
 @pytest.mark.parametrize("rows,n,n_out", [(49, 256, 40), (53, 4096, 300), (64, 1280, 520), (57, 14336, 96), (64, 768, 4100)])
-def test_gemm_q8_0_all_rows_one_pass_variants(cuda, monkeypatch, variant, rows, n, n_out):
+def test_gemm_q8_0_all_rows_one_pass_variants(cuda, knobs, variant, rows, n, n_out):
     """49..64 Q8_0 rows in one weight pass (activation rows staged in LDS per K chunk), both (waves) variants: ragged
     row counts, a single chunk, K split over waves with a chunk count that is not a multiple of the waves, a last
     weight tile past n_out, against the CPU backend."""
     import torch
 
-    monkeypatch.setenv("KF_GEMM_MR", variant)
-    monkeypatch.setenv("KF_GEMM_SK", "0")  # the split-K form takes these rows first
+    knobs.setenv("KF_GEMM_MR", variant)
+    knobs.setenv("KF_GEMM_SK", "0")  # the split-K form takes these rows first
     rng = np.random.default_rng(rows * 7 + n_out)
     w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n)
     x = (rng.standard_normal((rows, n)) * 3).astype(np.float32)
@@ -585,7 +585,7 @@ def test_gemm_q8_0_all_rows_one_pass_variants(cuda, monkeypatch, variant, rows, 
                                                      (64, 1024, 64, None, None), (24, 1024, 256, 4, None),
                                                      (40, 4096, 1000, None, 43), (64, 14336, 520, 5, 43),
                                                      (20, 4096, 700, None, 83), (64, 2048, 300, None, 162)])
-def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
+def test_gemm_q8_0_split_k(cuda, knobs, rows, n, n_out, splits, var):
     """17..64 Q8_0 rows with K split across blocks (partials summed in split order by the last block of each tile),
     forced on for every size (KF_GEMM_SK=1; by default it takes matrices above 4096 x 4096): ragged rows and output
     tiles, split counts that do not divide the chunks (7 of 56; 4 of 4: one chunk a split), the chunk forms (4, 8, 16
@@ -594,11 +594,11 @@ def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
     scratch-free products (KF_GEMM_SK=0)."""
     import torch
 
-    monkeypatch.setenv("KF_GEMM_SK", "1")
+    knobs.setenv("KF_GEMM_SK", "1")
     if splits:
-        monkeypatch.setenv("KF_GEMM_SK_S", str(splits))
+        knobs.setenv("KF_GEMM_SK_S", str(splits))
     if var:
-        monkeypatch.setenv("KF_GEMM_SK_V", str(var))
+        knobs.setenv("KF_GEMM_SK_V", str(var))
 
     rng = np.random.default_rng(rows * 13 + n + n_out)
     w = _weights(kf.TYPE_Q8_0, n_out, n, seed=rows + n_out)
@@ -618,7 +618,7 @@ def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
         assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
     want = oracle.matmul_slice(kf.TYPE_Q8_0, w, n, n_out, x, bias) + res
     _close(outs[0], want)
-    monkeypatch.setenv("KF_GEMM_SK", "0")
+    knobs.setenv("KF_GEMM_SK", "0")
     y = torch.full((rows, n_out), float("nan"), device=cuda)
     kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt, res=rt)
     torch.cuda.synchronize()
@@ -627,7 +627,7 @@ def test_gemm_q8_0_split_k(cuda, monkeypatch, rows, n, n_out, splits, var):
 
 @pytest.mark.parametrize("kq", ["0", "1"])
 @pytest.mark.parametrize("rows,n,n_out", [(2048, 4096, 14336), (130, 2048, 600), (257, 1024, 300), (96, 14336, 512)])
-def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out, kq):
+def test_gemm_q4_k_tail_halves(cuda, knobs, rows, n, n_out, kq):
     """The q4_K GEMMs' tail split, both kernels (KF_Q4K_KQ: 0 the split-scale kernel, two K halves; 1 the
     one-MFMA-per-group kernel, 2-4 K ranges): tiles of a last round at most half full (all of them when the grid is
     below half the CUs) run over K ranges whose partial tiles the last to arrive adds in order. Against the unsplit
@@ -635,7 +635,7 @@ def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out, kq):
     zero), and the smaller shapes against the CPU backend; 4, 8 and 56 super-blocks a row, ragged tiles."""
     import torch
 
-    monkeypatch.setenv("KF_Q4K_KQ", kq)
+    knobs.setenv("KF_Q4K_KQ", kq)
 
     w = _weights(kf.TYPE_Q4_K, n_out, n, seed=rows + n)
     x = kf.synth_normal(rows + 3, 1.0, rows * n).reshape(rows, n)
@@ -650,7 +650,7 @@ def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out, kq):
         torch.cuda.synchronize()
         outs.append(y.cpu().numpy())
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
-    monkeypatch.setenv("KF_GEMM_NO_TAIL", "1")
+    knobs.setenv("KF_GEMM_NO_TAIL", "1")
     y = torch.full((rows, n_out), float("nan"), device=cuda)
     kf.gemm_i8(kf.TYPE_Q4_K, wt, act, y, rows, n, n_out, bias=bt)
     torch.cuda.synchronize()
@@ -660,7 +660,7 @@ def test_gemm_q4_k_tail_halves(cuda, monkeypatch, rows, n, n_out, kq):
 
 
 @pytest.mark.parametrize("rows,n,n_out", [(2048, 4096, 14336), (300, 1024, 1000), (129, 14336, 600)])
-def test_gemm_q8_0_tail_halves(cuda, monkeypatch, rows, n, n_out):
+def test_gemm_q8_0_tail_halves(cuda, knobs, rows, n, n_out):
     """The q8_0 tile GEMM's tail split (two blocks a CU: a last round at most half full, or a grid below half of
     them, runs its tiles as two K halves added in half order by the second to arrive): against the unsplit kernel
     (KF_GEMM_NO_TAIL) within the f32 bar, bit-identical over two calls, the smaller shapes against the CPU backend."""
@@ -679,7 +679,7 @@ def test_gemm_q8_0_tail_halves(cuda, monkeypatch, rows, n, n_out):
         torch.cuda.synchronize()
         outs.append(y.cpu().numpy())
     assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
-    monkeypatch.setenv("KF_GEMM_NO_TAIL", "1")
+    knobs.setenv("KF_GEMM_NO_TAIL", "1")
     y = torch.full((rows, n_out), float("nan"), device=cuda)
     kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt)
     torch.cuda.synchronize()
@@ -689,7 +689,7 @@ def test_gemm_q8_0_tail_halves(cuda, monkeypatch, rows, n, n_out):
 
 
 @pytest.mark.parametrize("rows,n,n_out", [(96, 14336, 600), (130, 4096, 4096), (250, 14336, 520), (65, 4096, 6144)])
-def test_gemm_q8_0_row_slices(cuda, monkeypatch, rows, n, n_out):
+def test_gemm_q8_0_row_slices(cuda, knobs, rows, n, n_out):
     """65.. q8_0 rows as 64-row slices through the small-batch products (the cost model's pick at down- and O-like
     shapes up to a few hundred rows; KF_GEMM_SLICE forces each form): ragged last slices (2, 58 and 1 rows), bias and
     residual; the sliced and tile forms within the f32 bar of each other, and the auto choice against the CPU backend."""
@@ -705,9 +705,9 @@ def test_gemm_q8_0_row_slices(cuda, monkeypatch, rows, n, n_out):
     outs = {}
     for force in (None, "1", "0"):
         if force is None:
-            monkeypatch.delenv("KF_GEMM_SLICE", raising=False)
+            knobs.delenv("KF_GEMM_SLICE", raising=False)
         else:
-            monkeypatch.setenv("KF_GEMM_SLICE", force)
+            knobs.setenv("KF_GEMM_SLICE", force)
         y = torch.full((rows, n_out), float("nan"), device=cuda)
         kf.gemm_i8(kf.TYPE_Q8_0, wt, act, y, rows, n, n_out, bias=bt, res=rt)
         torch.cuda.synchronize()

@@ -100,7 +100,7 @@ def test_producer_feeds_the_product(cuda):
 @pytest.mark.parametrize("ty", [kf.TYPE_Q4_K, kf.TYPE_Q8_0])
 @pytest.mark.parametrize("rows,n,n_out,affine", [(1, 4096, 520, True), (1, 2048, 300, False), (1, 256, 64, True), (1, 4096, 6144, False),
                                                  (1, 3584, 96, True), (3, 4096, 200, True)])
-def test_rms_norm_matmul(cuda, monkeypatch, ty, rows, n, n_out, affine):
+def test_rms_norm_matmul(cuda, knobs, ty, rows, n, n_out, affine):
     """kf_hip_rms_norm_matmul: at one row the GEMV normalises and quantizes the row in every block (one launch),
     bit-identical to kf_hip_rms_norm_q8 followed by the product (KF_MATMUL_NO_FUSE); both against the CPU backend's
     matmul_slice of its rms_norm. Three rows take the two-launch path. Widths of one to sixteen 256-column chunks
@@ -121,9 +121,9 @@ def test_rms_norm_matmul(cuda, monkeypatch, ty, rows, n, n_out, affine):
     outs = []
     for fuse in (True, False):
         if fuse:
-            monkeypatch.delenv("KF_MATMUL_NO_FUSE", raising=False)
+            knobs.delenv("KF_MATMUL_NO_FUSE", raising=False)
         else:
-            monkeypatch.setenv("KF_MATMUL_NO_FUSE", "1")
+            knobs.setenv("KF_MATMUL_NO_FUSE", "1")
         y = torch.full((rows, n_out), float("nan"), device=cuda)
         kf.rms_norm_matmul(ty, wt, xt, act, y, n_out, wnt, bnt, 1e-5, bias=bt, res=rt)
         torch.cuda.synchronize()

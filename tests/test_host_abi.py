@@ -22,6 +22,30 @@ def test_library_exports_every_declared_symbol():
     assert L.kf_hip_abi_version() == 2
 
 
+def test_knobs_read_once_from_the_environment_then_only_through_the_setter():
+    """The launch knobs come from KF_* variables once per process (a flag knob by presence, a value knob by its
+    integer); later environment changes are not seen, kf_hip_set_knob is. Runs in a fresh process."""
+    import subprocess
+    import sys
+
+    code = (
+        "import os, kungfu_amd as kf\n"
+        "assert kf.get_knob('KF_GEMM_NO_TAIL') == 1 and kf.get_knob('KF_GEMV_MAXIT') == 3\n"
+        "assert kf.get_knob('KF_GEMM_SK') == -1\n"
+        "os.environ['KF_GEMM_SK'] = '1'\n"
+        "assert kf.get_knob('KF_GEMM_SK') == -1\n"
+        "kf.set_knob('KF_GEMM_SK', 0); assert kf.get_knob('KF_GEMM_SK') == 0\n"
+        "kf.set_knob('KF_GEMM_NO_TAIL', None); assert kf.get_knob('KF_GEMM_NO_TAIL') == -1\n"
+        "kf.set_knob('KF_GEMM_NO_TAIL', True); assert kf.get_knob('KF_GEMM_NO_TAIL') == 1\n"
+        "try:\n    kf.set_knob('KF_NOT_A_KNOB', 1)\nexcept kf.KfError:\n    pass\nelse:\n    raise SystemExit(1)\n"
+        "print('ok')\n"
+    )
+    env = dict(os.environ, KF_GEMM_NO_TAIL="0", KF_GEMV_MAXIT="3")
+    env.pop("KF_GEMM_SK", None)
+    r = subprocess.run([sys.executable, "-c", code], env=env, cwd=os.path.dirname(GOLDEN) + "/..", capture_output=True, text=True)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", r.stderr
+
+
 def test_act_layout_sections_are_aligned_and_sized():
     for rows, n in [(1, 4096), (3, 14336), (64, 256), (2048, 4096)]:
         o = kf.act_offsets(rows, n)
