@@ -143,8 +143,10 @@ int kf_hip_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* 
 /* kf_hip_rms_norm_q8 and kf_hip_matmul as one call: y = W . quant(rms_norm(x) * norm_w + norm_b) + bias + res, the
  * normalised rows quantized into `act` as kf_hip_rms_norm_q8 writes them, then the product kf_hip_matmul selects.
  * One row of q8_0 / q4_K (n_in <= 4096, x, norm_w, norm_b and the weights 16-byte aligned) runs as one launch: every
- * block of the GEMV normalises and quantizes the row itself (the same f64 sum of squares, correctly rounded square
- * root and division and unfused multiply-adds, so the same integers) and `act` is left unwritten
+ * block of the GEMV normalises and quantizes the row itself (an f64 sum of squares, correctly rounded square root
+ * and division and unfused multiply-adds, as kf_hip_rms_norm_q8; the f64 partial sums are added in another order, so
+ * a row whose scaled value lies within an f64 rounding of a quantization boundary may get another integer there,
+ * bit-identical on every tested shape) and `act` is left unwritten
  * (KF_MATMUL_NO_FUSE: two launches). Replaces the reference's rms_norm_q8 launch followed by matmul_launch
  * (exec.rs:2439, 2061-2093) for the decode products whose input is a normalised row (QKV, gate/up). */
 int kf_hip_rms_norm_matmul(uint32_t ty, const void* w, int n_in, int n_out, const float* x, int rows, const float* norm_w, const float* norm_b,
@@ -164,6 +166,15 @@ int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n_out, const
 
 /* KF_NOALLOC_SCRATCH_BYTES of the loaded library. No reference counterpart. */
 size_t kf_hip_noalloc_scratch_bytes(void);
+
+/* The split-K products and the tile GEMMs' tail splits keep partial tiles and tickets in a static per-GPU array of
+ * two slots; a slot goes to each (device, stream) on its first such product and stays with it. Launches on one stream
+ * are ordered, so a stream's products never share their slot with a running product. A stream that finds both slots
+ * held by other streams, and any stream under HIP graph capture (a graph could be replayed on another stream or
+ * beside direct launches), runs the scratch-free forms: same results within the bar, no shared state. This call
+ * waits for `stream`'s work and returns its slot for other streams (a no-op if it holds none); call it before
+ * destroying a stream that ran products. No reference counterpart. */
+int kf_hip_release_stream(void* stream);
 
 /* Grouped products sharing one input (Q/K/V, or gate and up stored as separate tensors): up to KF_HIP_MAX_SEGMENTS
  * weight matrices of one type and row width stacked along their output rows. The segment table is the reference's

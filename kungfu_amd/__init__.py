@@ -79,6 +79,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "kf_hip_block_ints": ([U, P, L64, P, I, I, I, P, P], I),
         "kf_hip_stream_read": ([P, S, I, P, P], I),
         "kf_hip_set_knob": ([ctypes.c_char_p, I], I),
+        "kf_hip_release_stream": ([P], I),
         "kf_hip_get_knob": ([ctypes.c_char_p], I),
         "kf_hip_rms_norm_matmul": ([U, P, I, I, P, I, P, P, ctypes.c_float, P, P, P, P, P], I),
         "kf_hip_gemm_i8": ([U, P, L64, P, P, P, P, I, I, I, P], I),
@@ -130,6 +131,11 @@ def check(rc: int) -> int:
     if rc < 0:
         raise KfError(rc, last_error())
     return rc
+
+
+def release_stream(stream) -> None:
+    """Returns the stream's split-K scratch slot (kf_hip_release_stream) after waiting for its work."""
+    check(lib().kf_hip_release_stream(stream))
 
 
 def set_knob(name: str, value) -> None:

@@ -32,6 +32,12 @@
 #include <type_traits>
 #include <cstdlib>
 
+// The split-K fixups rely on gfx9 cache behaviour (system-scope relaxed atomics write through to memory, stores are
+// counted in vmcnt), not on a release/acquire pair: build for gfx950 only.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the split-K fixups assume gfx950's cache and counter behaviour"
+#endif
+
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -1116,8 +1122,8 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
 }
 
 // The split-K launch: S splits of K per weight tile, about BPC blocks a CU (as many as the stages' LDS lets a CU
-// hold, at most two), as many as the scratch holds; hipErrorNotSupported when the scratch cannot be had (a fifth
-// stream)
+// hold, at most two), as many as the scratch holds; hipErrorNotSupported when the scratch cannot be had (a stream
+// under graph capture, or every slot held by other streams)
 template <int TM, int TN, int G, int NS>
 hipError_t gemm_sk_launch(const uint8_t* w, int64_t row_bytes, const int8_t* xq, const float* xd32, const float* bias, const float* res,
                           float* y, int M, int N, int K, hipStream_t s) {

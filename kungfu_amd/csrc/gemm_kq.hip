@@ -27,6 +27,12 @@
 
 #include <type_traits>
 
+// The split-K fixups rely on gfx9 cache behaviour (system-scope relaxed atomics write through to memory, stores are
+// counted in vmcnt), not on a release/acquire pair: build for gfx950 only.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the split-K fixups assume gfx950's cache and counter behaviour"
+#endif
+
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));

@@ -37,13 +37,12 @@ inline int kf_cu_count() {
     return v;
 }
 
-// Device scratch of the split-K products (the few-row q8_0 split-K product, the q4_K GEMM's tail halves): a static
-// __device__ array of KF_SPLIT_SLOTS slots of KF_SPLIT_SCRATCH bytes
-// per GPU (zero at load, never allocated, so graph capture and callers that cannot allocate can use it), one slot per
-// (device, stream) handed out on first use and kept for the process. A slot starts with KF_SPLIT_TICKETS int32
-// tickets, which the kernels leave at zero when they end. Launches on one stream are ordered, so a slot is never used
-// by two running products; a stream that finds every slot taken gets null and its products take their scratch-free
-// form.
+// Device scratch of the split-K products (the few-row q8_0 split-K product, the tile GEMMs' tail splits): a static
+// __device__ array of KF_SPLIT_SLOTS slots of KF_SPLIT_SCRATCH bytes per GPU (zero at load, never allocated), one slot
+// per (device, stream) handed out on first use and held until kf_hip_release_stream. A slot starts with
+// KF_SPLIT_TICKETS int32 tickets, which the kernels leave at zero when they end. Launches on one stream are ordered,
+// so a slot is never used by two running products. Null (and the products take their scratch-free form) for a stream
+// under graph capture, so no graph holds a slot, and for a stream that finds every slot held by other streams.
 constexpr size_t KF_SPLIT_SCRATCH = 40u << 20;
 constexpr int KF_SPLIT_SLOTS = 2;
 constexpr int KF_SPLIT_TICKETS = 1 << 16;

@@ -36,6 +36,7 @@ void* scratch_ptr(int dev) {
         const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !p) {
             kf_set_error("hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+            (void)hipGetLastError();  // the failure is reported here, not by the next launch's error check
             return nullptr;
         }
         ptr[dev] = p;
@@ -73,31 +74,71 @@ extern "C" int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n
 
 // ------------------------------------------------------------------------------------------------ split-K scratch
 // The split-K products' partial tiles and tickets (kf_host.h): static, so nothing is allocated and the addresses never
-// change. Each device has its own copy, found with hipGetSymbolAddress once per device.
+// change. Each device has its own copy, found with hipGetSymbolAddress once per device. Slots go to (device, stream)
+// pairs on first use and come back through kf_hip_release_stream. A stream under graph capture gets none: a captured
+// graph would keep the slot's address and could later be replayed on another stream, or beside direct launches on
+// its own, with both products sharing one slot's tickets and partials; its products take the scratch-free form.
 static __device__ __align__(256) uint8_t split_scratch[KF_SPLIT_SLOTS * KF_SPLIT_SCRATCH];
 
+namespace {
+std::mutex g_split_mu;
+std::map<int, uint8_t*> g_split_base;                       // per device
+std::map<std::pair<int, hipStream_t>, int> g_split_slot;    // per (device, stream)
+std::map<int, unsigned> g_split_free;                       // per device: bit i set when slot i is free
+}  // namespace
+
 void* kf_split_scratch(hipStream_t s) {
-    static std::mutex mu;
-    static std::map<int, uint8_t*> base;                       // per device
-    static std::map<std::pair<int, hipStream_t>, int> slot;    // per (device, stream)
-    static std::map<int, int> used;                            // slots handed out per device
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &cs) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (cs != hipStreamCaptureStatusNone) return nullptr;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> g(mu);
-    auto b = base.find(dev);
-    if (b == base.end()) {
+    if (hipGetDevice(&dev) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> g(g_split_mu);
+    auto b = g_split_base.find(dev);
+    if (b == g_split_base.end()) {
         void* p = nullptr;
         if (hipGetSymbolAddress(&p, HIP_SYMBOL(split_scratch)) != hipSuccess || !p) {
             (void)hipGetLastError();
             return nullptr;
         }
-        b = base.emplace(dev, static_cast<uint8_t*>(p)).first;
+        b = g_split_base.emplace(dev, static_cast<uint8_t*>(p)).first;
+        g_split_free[dev] = (1u << KF_SPLIT_SLOTS) - 1;
     }
-    auto it = slot.find({dev, s});
-    if (it == slot.end()) {
-        int& u = used[dev];
-        if (u >= KF_SPLIT_SLOTS) return nullptr;
-        it = slot.emplace(std::make_pair(dev, s), u++).first;
+    auto it = g_split_slot.find({dev, s});
+    if (it == g_split_slot.end()) {
+        unsigned& fr = g_split_free[dev];
+        if (fr == 0) return nullptr;  // every slot held by another stream: the scratch-free form
+        const int i = __builtin_ctz(fr);
+        fr &= ~(1u << i);
+        it = g_split_slot.emplace(std::make_pair(dev, s), i).first;
     }
     return b->second + (size_t)it->second * KF_SPLIT_SCRATCH;
+}
+
+extern "C" int kf_hip_release_stream(void* stream) {
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) {
+        kf_set_error("hipGetDevice: %s", hipGetErrorString(e));
+        return KF_E_HIP;
+    }
+    std::lock_guard<std::mutex> g(g_split_mu);
+    auto it = g_split_slot.find({dev, s});
+    if (it == g_split_slot.end()) return KF_OK;
+    // the slot is free only once the stream's products that use it have ended
+    e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        kf_set_error("hipStreamSynchronize: %s", hipGetErrorString(e));
+        return KF_E_HIP;
+    }
+    g_split_free[dev] |= 1u << it->second;
+    g_split_slot.erase(it);
+    return KF_OK;
 }
