@@ -168,12 +168,15 @@ int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n_out, const
 size_t kf_hip_noalloc_scratch_bytes(void);
 
 /* The split-K products and the tile GEMMs' tail splits keep partial tiles and tickets in a static per-GPU array of
- * two slots; a slot goes to each (device, stream) on its first such product and stays with it. Launches on one stream
- * are ordered, so a stream's products never share their slot with a running product. A stream that finds both slots
- * held by other streams, and any stream under HIP graph capture (a graph could be replayed on another stream or
- * beside direct launches), runs the scratch-free forms: same results within the bar, no shared state. This call
- * waits for `stream`'s work and returns its slot for other streams (a no-op if it holds none); call it before
- * destroying a stream that ran products. No reference counterpart. */
+ * three slots. Two are stream slots: one goes to each (device, stream) on its first such product and stays with it;
+ * launches on one stream are ordered, so a stream's products never share their slot with a running product. A stream
+ * that finds both stream slots held by other streams runs the scratch-free forms (same results within the bar). The
+ * third is the graph slot: every product recorded under HIP graph capture on that GPU uses it, and direct launches
+ * never do, so a replay (on any stream) never shares tickets or partials with a direct product. Rule: two replays of
+ * graphs that hold such products must not run at the same time on one GPU (serialise them on one stream, or with
+ * events); knob KF_CAPTURE_NO_SPLIT records the scratch-free forms instead. This call waits for `stream`'s work and
+ * returns its stream slot for other streams (a no-op if it holds none); call it before destroying a stream that ran
+ * products. No reference counterpart. */
 int kf_hip_release_stream(void* stream);
 
 /* Grouped products sharing one input (Q/K/V, or gate and up stored as separate tensors): up to KF_HIP_MAX_SEGMENTS

@@ -38,12 +38,16 @@ inline int kf_cu_count() {
 }
 
 // Device scratch of the split-K products (the few-row q8_0 split-K product, the tile GEMMs' tail splits): a static
-// __device__ array of KF_SPLIT_SLOTS slots of KF_SPLIT_SCRATCH bytes per GPU (zero at load, never allocated), one slot
-// per (device, stream) handed out on first use and held until kf_hip_release_stream. A slot starts with
-// KF_SPLIT_TICKETS int32 tickets, which the kernels leave at zero when they end. Launches on one stream are ordered,
-// so a slot is never used by two running products. Null (and the products take their scratch-free form) for a stream
-// under graph capture, so no graph holds a slot, and for a stream that finds every slot held by other streams.
+// __device__ array of KF_SPLIT_SLOTS slots of KF_SPLIT_SCRATCH bytes per GPU (zero at load, never allocated). Slots
+// 0 .. KF_SPLIT_STREAM_SLOTS - 1 go to (device, stream) pairs on first use and are held until kf_hip_release_stream;
+// launches on one stream are ordered, so a slot is never used by two running products. The last slot belongs to
+// products recorded under HIP graph capture (every captured product of a GPU shares it; direct launches never use
+// it), so a replay never meets a direct product's tickets; two replays of graphs holding such products must not run
+// at the same time. A slot starts with KF_SPLIT_TICKETS int32 tickets, which the kernels leave at zero when they end.
+// Null (and the products take their scratch-free form) for a stream that finds every stream slot held by other
+// streams, and under capture when KF_CAPTURE_NO_SPLIT is set.
 constexpr size_t KF_SPLIT_SCRATCH = 40u << 20;
-constexpr int KF_SPLIT_SLOTS = 2;
+constexpr int KF_SPLIT_STREAM_SLOTS = 2;
+constexpr int KF_SPLIT_SLOTS = KF_SPLIT_STREAM_SLOTS + 1;
 constexpr int KF_SPLIT_TICKETS = 1 << 16;
 void* kf_split_scratch(hipStream_t s);

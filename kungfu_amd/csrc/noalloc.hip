@@ -7,6 +7,7 @@
 // device address that hipGetSymbolAddress returns, looked up once per device (with that device current) on the
 // device's first call and kept per device.
 #include "kf_host.h"
+#include "kf_knobs.h"
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -74,10 +75,10 @@ extern "C" int kf_hip_matmul_noalloc(uint32_t ty, const void* w, int n_in, int n
 
 // ------------------------------------------------------------------------------------------------ split-K scratch
 // The split-K products' partial tiles and tickets (kf_host.h): static, so nothing is allocated and the addresses never
-// change. Each device has its own copy, found with hipGetSymbolAddress once per device. Slots go to (device, stream)
-// pairs on first use and come back through kf_hip_release_stream. A stream under graph capture gets none: a captured
-// graph would keep the slot's address and could later be replayed on another stream, or beside direct launches on
-// its own, with both products sharing one slot's tickets and partials; its products take the scratch-free form.
+// change. Each device has its own copy, found with hipGetSymbolAddress once per device. Stream slots go to (device,
+// stream) pairs on first use and come back through kf_hip_release_stream. A stream under graph capture gets the
+// graph slot instead: a captured graph keeps the address it recorded and may be replayed on any stream, so it must
+// never share a slot with direct launches, which hold stream slots only.
 static __device__ __align__(256) uint8_t split_scratch[KF_SPLIT_SLOTS * KF_SPLIT_SCRATCH];
 
 namespace {
@@ -93,7 +94,8 @@ void* kf_split_scratch(hipStream_t s) {
         (void)hipGetLastError();
         return nullptr;
     }
-    if (cs != hipStreamCaptureStatusNone) return nullptr;
+    const bool capturing = cs != hipStreamCaptureStatusNone;
+    if (capturing && kf_knob_on(KF_KNOB_CAPTURE_NO_SPLIT)) return nullptr;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) {
         (void)hipGetLastError();
@@ -108,8 +110,9 @@ void* kf_split_scratch(hipStream_t s) {
             return nullptr;
         }
         b = g_split_base.emplace(dev, static_cast<uint8_t*>(p)).first;
-        g_split_free[dev] = (1u << KF_SPLIT_SLOTS) - 1;
+        g_split_free[dev] = (1u << KF_SPLIT_STREAM_SLOTS) - 1;
     }
+    if (capturing) return b->second + (size_t)KF_SPLIT_STREAM_SLOTS * KF_SPLIT_SCRATCH;
     auto it = g_split_slot.find({dev, s});
     if (it == g_split_slot.end()) {
         unsigned& fr = g_split_free[dev];

@@ -1,8 +1,8 @@
 """Ownership of the split-K scratch across streams and graphs, through the C ABI: two streams running split products at
-once each keep their own slot (every output bit-identical to the one-stream result); a third stream, and any stream
-under graph capture, takes the scratch-free kernels (bit-identical to KF_GEMM_NO_TAIL); kf_hip_release_stream hands
-a slot to the next stream; a captured graph replayed on another stream beside direct calls gives the scratch-free
-result on every replay while the direct calls keep the split result."""
+once each keep their own slot (every output bit-identical to the one-stream result); a third stream takes the
+scratch-free kernels (bit-identical to KF_GEMM_NO_TAIL); kf_hip_release_stream hands a slot to the next stream; a
+captured product uses the graph slot, so a graph replayed on another stream beside direct calls gives the split result
+on every replay, as the direct calls do; with KF_CAPTURE_NO_SPLIT the graph records the scratch-free kernels."""
 import numpy as np
 import pytest
 
@@ -115,21 +115,15 @@ def test_q8_0_split_k_on_two_streams_at_once(cuda, knobs):
         kf.release_stream(b.cuda_stream)
 
 
-def test_graph_replayed_on_another_stream_beside_direct_calls(cuda, case, knobs):
-    """Captured, the product holds no slot (the scratch-free kernel is recorded); five replays on stream d, each beside
-    a direct product on the default stream, with eager work and synchronisation between replays."""
+def _replays(cuda, case, g, y_graph, n=5):
+    """Replays of g on stream d, each beside a direct product on the default stream, with eager work and
+    synchronisation between replays; yields (replay bits, direct bits)."""
     import torch
 
-    split, plain = _refs(cuda, case, knobs)
-    wt, act = case
-    y_graph = torch.full((ROWS, N_OUT), float("nan"), device=cuda)
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        kf.gemm_i8(kf.TYPE_Q4_K, wt, act, y_graph, ROWS, N, N_OUT)
     d = torch.cuda.Stream()
     y_direct_buf = torch.empty((ROWS, N_OUT), device=cuda)
     try:
-        for i in range(5):
+        for i in range(n):
             y_graph.fill_(float("nan"))
             y_direct_buf.fill_(float("nan"))
             torch.cuda.synchronize()
@@ -138,7 +132,38 @@ def test_graph_replayed_on_another_stream_beside_direct_calls(cuda, case, knobs)
                 g.replay()
             y_direct = _run(cuda, case, y=y_direct_buf)
             torch.cuda.synchronize()
-            assert np.array_equal(_bits(y_graph), plain), f"replay {i}"
-            assert np.array_equal(_bits(y_direct), split), f"direct call {i}"
+            yield i, _bits(y_graph), _bits(y_direct)
     finally:
         kf.release_stream(d.cuda_stream)
+
+
+def _capture(cuda, case):
+    import torch
+
+    wt, act = case
+    y_graph = torch.full((ROWS, N_OUT), float("nan"), device=cuda)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        kf.gemm_i8(kf.TYPE_Q4_K, wt, act, y_graph, ROWS, N, N_OUT)
+    return g, y_graph
+
+
+def test_graph_replayed_on_another_stream_beside_direct_calls(cuda, case, knobs):
+    """Captured, the product takes the graph slot (the split kernel is recorded); five replays on stream d, each
+    beside a direct product on the default stream (its stream slot): both give the split result every time."""
+    split, plain = _refs(cuda, case, knobs)
+    g, y_graph = _capture(cuda, case)
+    for i, yg, yd in _replays(cuda, case, g, y_graph):
+        assert np.array_equal(yg, split), f"replay {i}"
+        assert np.array_equal(yd, split), f"direct call {i}"
+
+
+def test_graph_capture_without_split(cuda, case, knobs):
+    """KF_CAPTURE_NO_SPLIT: the graph records the scratch-free kernel (the KF_GEMM_NO_TAIL result on every replay)."""
+    split, plain = _refs(cuda, case, knobs)
+    knobs.setenv("KF_CAPTURE_NO_SPLIT", "1")
+    g, y_graph = _capture(cuda, case)
+    knobs.delenv("KF_CAPTURE_NO_SPLIT")
+    for i, yg, yd in _replays(cuda, case, g, y_graph, n=3):
+        assert np.array_equal(yg, plain), f"replay {i}"
+        assert np.array_equal(yd, split), f"direct call {i}"
