@@ -452,6 +452,17 @@ def read_probe(gate_up, dev):
     return {"peak_measured": round(best_big, 1), "ceiling_same_bytes": round(best_same, 1)}
 
 
+def same_bytes_ceiling(ws, dev):
+    """Per-launch ceiling of a GEMV shape: the streaming-read probe over the shape's own weight copies, in the GEMV's
+    rotation, best of 4, 8 and 16 pieces a thread (us a launch: launch, ramp and tail included)."""
+    import torch
+
+    import kungfu_amd as kf
+
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    return min(time_launches(lambda i: kf.stream_read(ws[i % len(ws)], sink, p), 200) for p in (4, 8, 16))
+
+
 def read_traffic():
     """HBM bytes per gate+up GEMV launch from the committed counter summary (null when it is absent)."""
     try:
@@ -561,8 +572,10 @@ def main():
     for sh in shapes:
         us = time_launches(sh.gemv, 200)
         us_mm = time_launches(sh.matmul, 200)
+        ceil_us = same_bytes_ceiling(sh.w, dev)
         per[sh.name] = {"n_in": sh.n, "n_out": sh.n_out, "us": round(us, 3), "GBs": round(sh.bytes / us / 1e3, 1),
-                        "frac": round(sh.bytes / us / 1e3 / HBM_PEAK_GBS, 4), "us_with_quant": round(us_mm, 3)}
+                        "frac": round(sh.bytes / us / 1e3 / HBM_PEAK_GBS, 4), "us_with_quant": round(us_mm, 3),
+                        "ceiling_us": round(ceil_us, 3), "frac_of_ceiling": round(ceil_us / us, 4)}
         if sh.name == "gate_up":  # gemv_pipe_kernel<q4_K, one wave a row>, the largest share of the step
             k1_bytes += sh.bytes
             k1_us += us
@@ -572,6 +585,7 @@ def main():
     # Q8_0 GEMV of configs[0] (4096x4096) on the GPU, rotating copies
     q8 = Shape("q8_0", kf.TYPE_Q8_0, 4096, 4096, max(2, -(-2 * MALL_BYTES // (kf.row_bytes(8, 4096) * 4096)) + 1), dev)
     us_q8 = time_launches(q8.gemv, 200)
+    ceil_q8 = same_bytes_ceiling(q8.w, dev)
     del q8
 
     out = {
@@ -599,7 +613,9 @@ def main():
                      "ceiling_same_bytes": probe["ceiling_same_bytes"],
                      "frac_of_ceiling": round(achieved / probe["ceiling_same_bytes"], 4)},
         "shapes": per,
-        "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1)},
+        "q8_0_gemv_4096": {"us": round(us_q8, 3), "GBs": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3, 1),
+                           "frac": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3 / HBM_PEAK_GBS, 4),
+                           "ceiling_us": round(ceil_q8, 3), "frac_of_ceiling": round(ceil_q8 / us_q8, 4)},
     }
     out["int8_gemm"] = gemm_section(dev)
     out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
