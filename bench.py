@@ -522,6 +522,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=5.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--decode-only", action="store_true", help="the decode layer and per-shape GEMV figures alone (no side sections, no CPU leg)")
     ap.add_argument("--only", choices=["gemm", "gemm_q4_k", "gemm_kq", "small", "small_q4_k", "moe", "moe_prefill", "fused", "kquant", "group", "traffic"], help="run one side section alone (no JSON contract line)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -617,6 +618,9 @@ def main():
                            "frac": round(gemv_bytes(8, 4096, 4096) / us_q8 / 1e3 / HBM_PEAK_GBS, 4),
                            "ceiling_us": round(ceil_q8, 3), "frac_of_ceiling": round(ceil_q8 / us_q8, 4)},
     }
+    if args.decode_only:
+        print(json.dumps(out), flush=True)
+        return
     out["int8_gemm"] = gemm_section(dev)
     out["int8_gemm_tops"] = min(v["TOPS"] for v in out["int8_gemm"].values())
     out["int8_gemm_q4_k"] = gemm_q4_k_section(dev)

@@ -739,6 +739,27 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
             xdx = sd[bb];
         }
     };
+    uint4 ring[D][GV_PIECES];
+    // Two schedules, both measured (one A/B session, us a launch):
+    //   * split rows (WPR > 1): every load of the ring is unconditional, so the compiler's wait counts are exact and D
+    //     rows stay in flight (a load skipped on some path makes the waits hold, on every path, for the fewest loads
+    //     in flight). Rows past the wave's own read the activation row instead (small and cache-resident: no HBM
+    //     traffic, never stored). Down: 7.6 against 7.8;
+    //   * one wave a row: loads past the wave's rows are skipped and the store reads bias and residual itself; the
+    //     compiler then waits at the store for every load in flight and, at the second row of the ring, for the row
+    //     just requested, so a wave alternates between one row and none in flight. That measured faster than exact
+    //     waits with two rows in flight (gate+up 13.1 against 13.6, QKV 5.0 against 5.05, O 4.2 against 4.26) and
+    //     than exactly one row in flight behind an explicit wait (15.2).
+    const uint8_t* spare = QX > 0 ? reinterpret_cast<const uint8_t*>(xf) : reinterpret_cast<const uint8_t*>(xq);
+    const int spare_len = QX > 0 ? 4 * n : n;
+    auto load_row = [&](int k, int it2) {
+        if constexpr (WPR == 1) {
+            if (it2 < iw) gv_load_step<TY>(ring[k], row_ptr(it2), len, ln);
+        } else {
+            const bool own = it2 < iw;
+            gv_load_step<TY>(ring[k], own ? row_ptr(it2) : spare, own ? len : spare_len, ln);
+        }
+    };
     auto process = [&](const uint4* v, int it) {
         if (!(KF_GV_ABLATE & 4)) gv_park<TY>(wb, v, len, ln);
         __builtin_amdgcn_wave_barrier();
@@ -755,16 +776,22 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         acc = kf_wave_sum_dpp(acc);
         const int o = (it * B + (int)blockIdx.x) * RPB + rg;
         if (lane == 0 && o < n_out) {
-            if (WPR == 1) gv_store(sg, y, bias, res, o, acc);
-            else part[it * GV_WAVES + wave] = acc;
+            if constexpr (WPR == 1)
+                gv_store(sg, y, bias, res, o, acc);
+            else
+                part[it * GV_WAVES + wave] = acc;
         }
     };
 
     // the first D rows' weights go out before the block waits on its activation row; vmcnt counts loads in issue
     // order, so waiting until only those weight loads are outstanding means the activation loads have landed
-    uint4 ring[D][GV_PIECES];
 #pragma unroll
-    for (int k = 0; k < D; k++) gv_load_step<TY>(ring[k], row_ptr(k), len, ln);
+    for (int k = 0; k < D; k++) {
+        if constexpr (WPR == 1)
+            gv_load_step<TY>(ring[k], row_ptr(k), len, ln);  // rows past the wave's own reload its last row
+        else
+            load_row(k, k);
+    }
     if constexpr (QX > 0) {
         __builtin_amdgcn_sched_barrier(0);
         if constexpr (NM) {
@@ -786,8 +813,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
 #pragma unroll
         for (int k = 0; k < D; k++) {
             process(ring[k], it + k);
-            // only rows this wave owns: a reload past them would fetch its last row again (a uniform branch)
-            if (it + k + D < iw) gv_load_step<TY>(ring[k], row_ptr(it + k + D), len, ln);
+            load_row(k, it + k + D);
         }
     }
     KF_GV_STAMP(2)

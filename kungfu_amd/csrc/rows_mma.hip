@@ -128,9 +128,8 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
     extern __shared__ __align__(16) uint8_t smem[];
     // a wave's super-blocks of weights land whole in its LDS buffers (NB of them, in rotation), rows contiguous
     constexpr int NW = GLU ? 2 : 1;
-    __shared__ __align__(16) uint8_t pk0[RM_WAVES * NW * RM_TILE_BYTES];
-    __shared__ __align__(16) uint8_t pk1[RM_WAVES * NW * RM_TILE_BYTES];
-    __shared__ __align__(16) uint8_t pk2[NB > 2 ? RM_WAVES * NW * RM_TILE_BYTES : 16];
+    static_assert(NB >= 2 && NB <= 5, "two to five weight buffers");
+    __shared__ __align__(16) uint8_t pk[NB][RM_WAVES * NW * RM_TILE_BYTES];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slot = blockIdx.y;
@@ -204,9 +203,9 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
             const int items = my_tiles * nsbp;
             const bool last_phase = ph == nph - 1;
             // the first NB super-blocks of weights go out before the phase's activations are staged
-            if (items > 0) park(sb0, nsbp, 0, pk0);
-            if (items > 1) park(sb0, nsbp, 1, pk1);
-            if (NB > 2 && items > 2) park(sb0, nsbp, 2, pk2);
+#pragma unroll
+            for (int b = 0; b < NB; b++)
+                if (items > b) park(sb0, nsbp, b, pk[b]);
             // stage: A operands by DMA (instruction i fills LDS bytes [1024 i, +1024): slot s = 64 i + lane of 16
             // bytes is group s / (2 RT) of the phase, row (s / 2) % RT, half s % 2), rows past R repeat row R - 1
             {
@@ -278,7 +277,11 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
             constexpr int NI = 3 * NW;
             auto step = [&](uint8_t* buf, int j) {
                 const int ahead = min(NB - 1, items - 1 - j);
-                if (ahead >= 2)
+                if (NB > 4 && ahead >= 4)
+                    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(4 * NI));
+                else if (NB > 3 && ahead == 3)
+                    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(3 * NI));
+                else if (ahead == 2)
                     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(2 * NI));
                 else if (ahead == 1)
                     __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(NI));
@@ -294,9 +297,9 @@ __global__ void __launch_bounds__(RM_THREADS) rows_mma_kernel(const uint8_t* __r
                 }
             };
             for (int it = 0; it < items; it += NB) {
-                step(pk0, it);
-                if (it + 1 < items) step(pk1, it + 1);
-                if (NB > 2 && it + 2 < items) step(pk2, it + 2);
+#pragma unroll
+                for (int b = 0; b < NB; b++)
+                    if (it + b < items) step(pk[b], it + b);
             }
             __syncthreads();  // before the next phase or chunk restages
         }
@@ -328,15 +331,25 @@ RmPlan rm_plan(int n, int n_out, int slots, bool glu, int avg_rows) {
     else if (fits(8, 2))
         pl = RmPlan{8, 2, n, 0};
     else {
-        pl = RmPlan{8, 3, n, 0};
+        // the fewest phases three buffers allow; then, without GLU, as many buffers (up to five) as fit beside a
+        // phase of that width, so more weight bytes stay in flight (C5 down: 8 rows of 7168 columns and five buffers)
         const int nsb = n / KF_Q4_K_BLOCK;
-        int max_sb = nsb;
-        while (max_sb > 1 && rm_lds(max_sb * KF_Q4_K_BLOCK, 8).total + 3 * buf > RM_LDS_MAX) max_sb--;
-        const int nph = (nsb + max_sb - 1) / max_sb;
-        pl.kc = ((nsb + nph - 1) / nph) * KF_Q4_K_BLOCK;  // balanced phases
+        auto phases = [&](int nb) {
+            int max_sb = nsb;
+            while (max_sb > 1 && rm_lds(max_sb * KF_Q4_K_BLOCK, 8).total + nb * buf > RM_LDS_MAX) max_sb--;
+            return (nsb + max_sb - 1) / max_sb;
+        };
+        const int nph = phases(3);
+        pl = RmPlan{8, 3, ((nsb + nph - 1) / nph) * KF_Q4_K_BLOCK, 0};  // balanced phases
+        if (!glu)
+            for (int nb = 5; nb > 3; nb--)
+                if (rm_lds(pl.kc, 8).total + nb * buf <= RM_LDS_MAX) {
+                    pl.nb = nb;
+                    break;
+                }
     }
-    const int forced_nb = kf_knob_or(KF_KNOB_RM_NB, 0);  // a measurement knob (2 or 3 buffers)
-    if (forced_nb == 2) pl.nb = 2;
+    const int forced_nb = kf_knob_or(KF_KNOB_RM_NB, 0);  // a measurement knob: fewer buffers (2 to 4)
+    if (forced_nb >= 2 && forced_nb < pl.nb) pl.nb = forced_nb;
     if (pl.kc < n) {
         pl.rpb = 16 * RM_WAVES;
     } else {
@@ -627,6 +640,8 @@ hipError_t kf_launch_rows_mma(const void* w, const void* w2, int64_t expert_byte
         KF_RM_NB(true, 8);
     }
     if (pl.rt == 16) { KF_RM_NB(false, 16); }
+    if (pl.nb == 5) KF_RM(false, 8, 5);
+    if (pl.nb == 4) KF_RM(false, 8, 4);
     KF_RM_NB(false, 8);
 #undef KF_RM_NB
 #undef KF_RM
