@@ -941,6 +941,12 @@ __device__ __forceinline__ void sk_wait(int rem) {
     }
 }
 
+// Ablation switch for measurement builds only (0 in the product): bit 1 drops the MFMA / VALU work of a chunk, bit 2
+// the split epilogue (partials, ticket and fixup: each block stores its own tile)
+#ifndef SK_ABL
+#define SK_ABL 0
+#endif
+
 template <int TM, int TN, int G, int NS>
 __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
                                                            const float* __restrict__ xd32, const float* __restrict__ bias,
@@ -1047,7 +1053,7 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
         sk_wait<Geo::NI, NS - 2>(min(nch - 1 - i, NS - 2));
         __syncthreads();
         if (i + NS - 1 < nch) issue(std::integral_constant<int, (B + NS - 1) % NS>{}, i + NS - 1);
-        compute(kb);
+        if (!(SK_ABL & 1)) compute(kb);
     };
     static_assert(NS >= 2 && NS <= 4, "two to four stages");
     issue(std::integral_constant<int, 0>{}, 0);  // nch >= 1: the launcher gives every split a chunk
@@ -1074,6 +1080,18 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
     // memory, so the blocks of a tile on different XCDs (each with its own L2) see each other's partials without an L2
     // write-back (a __threadfence here, one per block, cost more than the product). Every lane waits for its partial
     // stores to complete before the barrier, and the ticket is taken after it.
+    if (SK_ABL & 2) {
+#pragma unroll
+        for (int t = 0; t < TM; t++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const int m = 16 * t + 4 * q + k, n = n0 + 16 * (TN * wave + j) + c;
+                    if (m < M && n < N) y[(int64_t)m * N + n] = acc[t][j][k];
+                }
+        return;
+    }
     float* pt = part + (size_t)blockIdx.x * Geo::TILE;
 #pragma unroll
     for (int t = 0; t < TM; t++)

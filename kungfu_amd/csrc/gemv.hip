@@ -836,6 +836,139 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     }
 }
 
+// ------------------------------------------------------------------------------------------------ burst variant
+// Every wave requests all R of its rows at launch (the pattern of the streaming-read probe, which reaches the chip's
+// read rate: 10.4 us over the 66 MB gate+up rotation, one-shot) and multiplies them in order as they land. No block
+// barrier: each lane loads its own activation operands (its four 16-byte pieces, two sub-block sums and a scale, or a
+// q8_0 block's two pieces and scale) straight from global memory, where every block reads the same small row. A row
+// travels as two 16-byte pieces and one dword a lane (2304 bytes: 1 KB, 1 KB and 256 B a wave instruction; q8_0's
+// 2176-byte step the same with lanes past 32 reading a duplicate dword) and is parked in the wave's LDS buffer for the
+// per-block lanes. Every load is unconditional (rows past the wave's own, absent bias and residual values read the
+// activation row instead), so the compiler's wait before a row counts exactly the loads behind it.
+template <uint32_t TY, int WPR, int R>
+__global__ void __launch_bounds__(GV_THREADS) gemv_burst_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
+                                                                const int32_t* __restrict__ xs32, const float* __restrict__ xd32,
+                                                                const float* __restrict__ bias, const float* __restrict__ res,
+                                                                float* __restrict__ y, int n, int n_out, int iters, const KfSegs sg,
+                                                                const float* __restrict__, const GvNorm) {
+    constexpr int RPB = GV_WAVES / WPR;
+    constexpr int STEP = TY == KF_TYPE_Q4_K ? 2304 : 2176;
+    constexpr int PER_STEP = TY == KF_TYPE_Q4_K ? 16 : 64;
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rg = wave / WPR, sp = wave % WPR;
+    const int nblk = TY == KF_TYPE_Q4_K ? n >> 8 : n >> 5;
+    const int B = gridDim.x;
+    const int steps = TY == KF_TYPE_Q4_K ? (nblk + 15) / 16 : (nblk + 63) / 64;
+    const int64_t at = (int64_t)min(sp, steps - 1) * STEP;  // the wave's step of every row
+    const int len = (int)min((int64_t)STEP, row_bytes - at);
+    const bool has_step = sp < steps;
+    const int j = lane & 3;
+    const int blk = sp * PER_STEP + (TY == KF_TYPE_Q4_K ? (lane >> 2) : lane);
+    const int bb = min(blk, nblk - 1);
+    uint8_t* wb = smem + (size_t)wave * GV_STEP_BYTES;
+    const uint8_t* wl = TY == KF_TYPE_Q4_K ? wb + (lane >> 2) * KF_Q4_K_BYTES : wb + 34 * lane;
+    float* part = reinterpret_cast<float*>(smem + (size_t)GV_WAVES * GV_STEP_BYTES);
+    int iw = iters;  // iterations whose row exists for this wave
+    while (iw > 0 && ((iw - 1) * B + (int)blockIdx.x) * RPB + rg >= n_out) iw--;
+    const uint8_t* spare = reinterpret_cast<const uint8_t*>(xq);
+
+    // 1. the lane's activation operands, then the rows' bias and residual values
+    uint4 xa4[4];
+    int2 xbs = make_int2(0, 0);
+    float xdx;
+    if (KF_GV_ABLATE & 8) {
+        xa4[0] = xa4[1] = xa4[2] = xa4[3] = make_uint4(lane, 1u, 2u, 3u);
+        xdx = 1.0f;
+    } else if constexpr (TY == KF_TYPE_Q4_K) {
+        const uint4* xp = reinterpret_cast<const uint4*>(xq + (size_t)bb * 256 + 64 * j);
+#pragma unroll
+        for (int k = 0; k < 4; k++) xa4[k] = xp[k];
+        xbs = *reinterpret_cast<const int2*>(xs32 + bb * 8 + 2 * j);
+        xdx = xd32[bb * 8];
+    } else {
+        const uint4* xp = reinterpret_cast<const uint4*>(xq + (size_t)bb * 32);
+        xa4[0] = xp[0];
+        xa4[1] = xp[1];
+        xa4[2] = xa4[3] = make_uint4(0u, 0u, 0u, 0u);
+        xdx = xd32[bb];
+    }
+    auto row_of = [&](int it) { return min((min(it, max(iw, 1) - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1); };
+    float rb[R], rr[R];
+    if constexpr (WPR == 1) {
+#pragma unroll
+        for (int it = 0; it < R; it++) {
+            const GvRow r = gv_row(sg, nullptr, y, bias, res, row_of(it));
+            rb[it] = *(r.bias ? r.bias + r.o : reinterpret_cast<const float*>(spare));
+            rr[it] = *(r.res ? r.res + r.o : reinterpret_cast<const float*>(spare));
+        }
+    }
+    // 2. every row of the wave
+    uint4 va[R], vb[R];
+    uint32_t vc[R];
+    const uint32_t oa = min(16u * (uint32_t)lane, (uint32_t)len - 16u), ob = min(1024u + 16u * (uint32_t)lane, (uint32_t)len - 16u);
+    const uint32_t oc = min(2048u + 4u * (uint32_t)lane, (uint32_t)len - 4u);
+#pragma unroll
+    for (int it = 0; it < R; it++) {
+        const bool own = it < iw;
+        const uint8_t* src = own ? gv_row_ptr(sg, w, row_bytes, row_of(it)) + at : spare;
+        const uint32_t cap = own ? 0xffffffffu : (uint32_t)n - 16u;  // the activation row holds n bytes
+        if constexpr (TY == KF_TYPE_Q4_K) {
+            va[it] = kf_load_stream_u4(src + min(oa, cap));
+            vb[it] = kf_load_stream_u4(src + min(ob, cap));
+        } else {
+            va[it] = kf_load_stream_u4_unaligned(src + min(oa, cap));
+            vb[it] = kf_load_stream_u4_unaligned(src + min(ob, cap));
+        }
+        vc[it] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(src + min(oc, cap)));
+    }
+    // 3. the rows in order as they land
+#pragma unroll
+    for (int it = 0; it < R; it++) {
+        if (it < iters) {
+            if (!(KF_GV_ABLATE & 4)) {
+                *reinterpret_cast<uint4*>(wb + oa) = va[it];
+                *reinterpret_cast<uint4*>(wb + ob) = vb[it];
+                *reinterpret_cast<uint32_t*>(wb + oc) = vc[it];
+            }
+            __builtin_amdgcn_wave_barrier();
+            float acc = 0.0f;
+            if (KF_GV_ABLATE & 2) {
+                acc = (KF_GV_ABLATE & 4) ? (float)(va[it].x ^ vb[it].y ^ vc[it]) : (float)(*reinterpret_cast<const uint32_t*>(wl) ^ xa4[0].x);
+            } else if (has_step && blk < nblk) {
+                if constexpr (TY == KF_TYPE_Q4_K)
+                    acc = gv_q4k_lane_r(wl, xa4[0], xa4[1], xa4[2], xa4[3], xbs, xdx, j);
+                else
+                    acc = gv_q8_0_lane_r(wl, xa4[0], xa4[1], xdx);
+            }
+            __builtin_amdgcn_wave_barrier();
+            acc = kf_wave_sum_dpp(acc);
+            const int o = (it * B + (int)blockIdx.x) * RPB + rg;
+            if (lane == 0 && o < n_out) {
+                if constexpr (WPR == 1) {
+                    const GvRow r = gv_row(sg, nullptr, y, bias, res, o);
+                    r.y[r.o] = acc + (r.bias ? rb[it] : 0.0f) + (r.res ? rr[it] : 0.0f);
+                } else {
+                    part[it * GV_WAVES + wave] = acc;
+                }
+            }
+        }
+    }
+    if constexpr (WPR > 1) {
+        __syncthreads();
+        for (int t = threadIdx.x; t < iters * RPB; t += GV_THREADS) {
+            const int it2 = t / RPB, g = t % RPB;
+            const int o = (it2 * B + (int)blockIdx.x) * RPB + g;
+            if (o >= n_out) continue;
+            float acc = 0.0f;
+#pragma unroll
+            for (int q = 0; q < WPR; q++) acc += part[it2 * GV_WAVES + g * WPR + q];
+            gv_store(sg, y, bias, res, o, acc);
+        }
+    }
+}
+
 // The unit loads of the per-block integer check: a q8_0 block read as its f16 scale and two unaligned 16-byte loads
 struct Q8Unit {
     uint32_t dbits;
@@ -985,6 +1118,29 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
         GvKernel k = gemv_dma_kernel<TY, 1, WPR, 1>;
         if (groups <= cu_count() * resident_blocks(k, smem) && smem <= 65536) {
             k<<<groups, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, 1, sg, xf, nm);
+            return hipGetLastError();
+        }
+    }
+    // the burst variant where every wave of a grid of two blocks a CU has one row (O at 4096 x 4096: 3.9 against
+    // 4.2 us for the pipelined kernel, which waits for its block's activation row first). With more rows a wave it
+    // measured slower than the pipelined kernel (gate+up, 7 rows a wave: 14.4 against 13.1 us; 12.6 even without
+    // the arithmetic), so it takes one-row grids only; KF_GEMV_BURST=n forces it up to n rows a wave (1, 2, 4, 7, 8)
+    const int burst_rows = kf_knob_on(KF_KNOB_GEMV_BURST) ? kf_knob(KF_KNOB_GEMV_BURST) : 1;
+    if (!fused && SPW == 1 && dma && maxit_env == 0 && !kf_knob_on(KF_KNOB_GEMV_NO_PIPE)) {
+        const int bpc = kf_knob(KF_KNOB_GEMV_BPC);
+        int grid = cu_count() * (bpc > 0 ? bpc : 2);
+        if (grid > groups) grid = groups;
+        const int iters = (groups + grid - 1) / grid;
+        const size_t smem = (size_t)GV_WAVES * GV_STEP_BYTES + (WPR > 1 ? (size_t)iters * GV_WAVES * 4 : 0);
+        GvKernel k = iters > burst_rows ? nullptr
+                     : iters == 1 ? gemv_burst_kernel<TY, WPR, 1>
+                     : iters == 2 ? gemv_burst_kernel<TY, WPR, 2>
+                     : iters <= 4 ? gemv_burst_kernel<TY, WPR, 4>
+                     : iters == 7 ? gemv_burst_kernel<TY, WPR, 7>
+                     : iters <= 8 ? gemv_burst_kernel<TY, WPR, 8>
+                                  : nullptr;
+        if (k && (int64_t)n <= 16 * 1024 * 1024) {
+            k<<<grid, GV_THREADS, smem, s>>>(w, row_bytes, xq, xs32, xd32, bias, res, y, n, n_out, iters, sg, nullptr, nm);
             return hipGetLastError();
         }
     }

@@ -31,6 +31,7 @@ enum KfKnob : int {
     KF_KNOB_GEMM_SMALL_W,    // value: waves per block of the small-batch kernel
     KF_KNOB_GEMM_SMALL_TN,   // value: 16-column tiles a wave of the small-batch kernel
     KF_KNOB_CAPTURE_NO_SPLIT,  // flag: products under graph capture take the scratch-free forms
+    KF_KNOB_GEMV_BURST,      // value: the burst GEMV takes grids of up to this many rows a wave (0: none; default 1)
     KF_KNOB_COUNT
 };
 

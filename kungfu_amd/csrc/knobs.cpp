@@ -20,7 +20,7 @@ constexpr KnobName kNames[KF_KNOB_COUNT] = {
     {"KF_KQ_GEMM", false},     {"KF_MOE_KQ", false},      {"KF_GEMM_NO_TAIL", true}, {"KF_GEMM_TILE", true},
     {"KF_GEMM_SLICE", false},  {"KF_GEMM_SK", false},     {"KF_GEMM_SK_S", false},   {"KF_GEMM_SK_V", false},
     {"KF_GEMM_NO_MR", true},   {"KF_GEMM_MR", false},     {"KF_GEMM_SMALL_W", false}, {"KF_GEMM_SMALL_TN", false},
-    {"KF_CAPTURE_NO_SPLIT", true},
+    {"KF_CAPTURE_NO_SPLIT", true}, {"KF_GEMV_BURST", false},
 };
 std::atomic<int> g_knob[KF_KNOB_COUNT];
 std::once_flag g_once;

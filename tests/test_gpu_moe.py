@@ -335,6 +335,32 @@ def test_moe_ffn_grouped_gemm_top_2(cuda, knobs, rows, n_exp, kq):
     assert np.abs(got - flt).max() <= 2e-2 * max(np.abs(flt).mean(), 1e-6)
 
 
+def test_grouped_gemm_partial_row_tiles(cuda):
+    """Slots whose rows end just past a 128-row tile (1, 17 or 32 rows in the last tile), slots of 5, 32 and 33 rows,
+    an empty slot: the tiles holding at most 32 rows run the one-tile K loop, the others the full one; every row of
+    every slot against the CPU backend's integer product for its expert."""
+    import torch
+
+    ty, n, n_out = kf.TYPE_Q4_K, 1024, 768
+    sizes = [129, 145, 32, 33, 5, 0, 160]
+    n_exp = len(sizes)
+    offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
+    pairs = int(offs[-1])
+    w = _experts(ty, n_exp, n_out, n, 90)
+    x = kf.synth_normal(91, 1.0, pairs * n).reshape(pairs, n)
+    act = kf.alloc_act(pairs, n, cuda)
+    kf.quant_act(_t(x, cuda), act, kf.act_kind(ty))
+    y = torch.full((pairs, n_out), float("nan"), device=cuda)
+    eb = n_out * kf.row_bytes(ty, n)
+    kf.moe_gemm(ty, _t(w, cuda), act, pairs, n, n_out, _t(offs, cuda), n_exp, y, eb)
+    got = y.cpu().numpy()
+    wr = w.reshape(n_exp, -1)
+    for s in range(n_exp):
+        r0, r1 = offs[s], offs[s + 1]
+        if r1 > r0:
+            _close(got[r0:r1], oracle.matmul_i8(ty, wr[s], n, n_out, x[r0:r1]))
+
+
 def test_moe_ffn_config_c5_every_token(cuda):
     """Config C5 at full size (8 experts of Q4_K 4096 -> 14336 -> 4096, 16 tokens, top-2): all 16 tokens against the
     CPU backend, stage by stage, and the layer against the CPU float path."""

@@ -271,6 +271,33 @@ def test_gemv_one_shot_variant(cuda, knobs, ty, n, n_out):
     _close(outs[1], oracle.matmul_slice(ty, w.cpu().numpy(), n, n_out, x))
 
 
+@pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 4096, 4096), (kf.TYPE_Q4_K, 4096, 6144), (kf.TYPE_Q4_K, 4096, 28672),
+                                        (kf.TYPE_Q4_K, 4096, 30000), (kf.TYPE_Q4_K, 14336, 4096), (kf.TYPE_Q4_K, 2304, 9),
+                                        (kf.TYPE_Q8_0, 4096, 4096), (kf.TYPE_Q8_0, 14336, 1030), (kf.TYPE_Q8_0, 4128, 77)])
+def test_gemv_burst_variant(cuda, knobs, ty, n, n_out):
+    """The burst GEMV (every wave's rows requested at launch, activation operands loaded per lane) forced at one to
+    eight rows a wave and one to eight waves a row (KF_GEMV_BURST=8) against the pipelined kernel (KF_GEMV_BURST=0),
+    bit for bit with bias and residual, and the CPU backend within the f32 bar."""
+    import torch
+
+    w = _tensor(_weights(ty, n_out, n, seed=47), cuda)
+    x = kf.synth_normal(48, 1.0, n).reshape(1, n)
+    bias = _tensor(kf.synth_normal(49, 1.0, n_out), cuda)
+    res = _tensor(kf.synth_normal(50, 1.0, n_out).reshape(1, n_out), cuda)
+    act = kf.alloc_act(1, n, cuda)
+    kf.quant_act(_tensor(x, cuda), act, kf.act_kind(ty))
+    outs = []
+    for rows in ("0", "8"):
+        knobs.setenv("KF_GEMV_BURST", rows)
+        y = torch.full((1, n_out), float("nan"), device=cuda)
+        kf.gemv(ty, w, act, y, 1, n, n_out, bias=bias, res=res)
+        torch.cuda.synchronize()
+        outs.append(y.cpu().numpy())
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    want = oracle.matmul_slice(ty, w.cpu().numpy(), n, n_out, x) + bias.cpu().numpy() + res.cpu().numpy()
+    _close(outs[1], want)
+
+
 @pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 256, 40), (kf.TYPE_Q4_K, 1280, 300), (kf.TYPE_Q4_K, 4096, 1030),
                                         (kf.TYPE_Q4_K, 2304, 777), (kf.TYPE_Q4_K, 14336, 64),
                                         (kf.TYPE_Q8_0, 32, 7), (kf.TYPE_Q8_0, 1056, 300), (kf.TYPE_Q8_0, 4096, 777),
