@@ -208,12 +208,13 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
             const uint32_t qhv[4] = {qh.x, qh.y, qh.z, qh.w};
             const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
             uint4 raw[4];
-            uint32_t sc2[4];
+            uint32_t sc2[4], scv[2], mnv[2];
+            kf_q4k_scales8(hd.y, hd.z, hd.w, scv, mnv);
 #pragma unroll
             for (int p = 0; p < 4; p++) {
                 raw[p] = *reinterpret_cast<const uint4*>(wr + G::QS + 32 * p + 16 * half);
-                uint32_t m2;
-                kf_q4k_scales(hd.y, hd.z, hd.w, p, sc2[p], m2);
+                sc2[p] = kf_pair(scv, p);
+                const uint32_t m2 = kf_pair(mnv, p);
                 mo[2 * p] = (_Float16)(float)((half ? 1u : 64u) * (m2 & 0xffu));
                 mo[2 * p + 1] = (_Float16)(float)((half ? 1u : 64u) * (m2 >> 8));
             }

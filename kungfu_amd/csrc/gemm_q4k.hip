@@ -239,11 +239,12 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
     // The super-block's four sub-block pairs into the S chains
     auto mfma_sb = [&](const uint8_t* buf) __attribute__((always_inline)) {
         const uint4 hd = *reinterpret_cast<const uint4*>(buf + G4_W + wrow);
+        uint32_t scv[2], mnv[2];
+        kf_q4k_scales8(hd.y, hd.z, hd.w, scv, mnv);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
             const uint4 raw = *reinterpret_cast<const uint4*>(buf + G4_W + wrow + 16 + 32 * p + 16 * half);
-            uint32_t sc2, m2;
-            kf_q4k_scales(hd.y, hd.z, hd.w, p, sc2, m2);
+            const uint32_t sc2 = kf_pair(scv, p);
             const uint32_t s0 = sc2 & 0xffu, s1 = sc2 >> 8;
             const uint32_t l0 = s0 & 7u, u0 = s0 >> 3, l1 = s1 & 7u, u1 = s1 >> 3;
             const uint32_t m4 = 0x0f0f0f0fu;
@@ -298,10 +299,11 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
             return;
         }
         v8h mo;
+        uint32_t scv[2], mnv[2];
+        kf_q4k_scales8(hd.y, hd.z, hd.w, scv, mnv);
 #pragma unroll
         for (int pj = 0; pj < 4; pj++) {
-            uint32_t sc2, m2;
-            kf_q4k_scales(hd.y, hd.z, hd.w, pj, sc2, m2);
+            const uint32_t m2 = kf_pair(mnv, pj);
             const uint32_t f = half ? 1u : 64u;
             mo[2 * pj] = (_Float16)(float)(f * (m2 & 0xffu));
             mo[2 * pj + 1] = (_Float16)(float)(f * (m2 >> 8));

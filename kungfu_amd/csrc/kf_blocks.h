@@ -28,6 +28,18 @@ __device__ __forceinline__ void kf_q4k_scales(uint32_t hy, uint32_t hz, uint32_t
     }
 }
 
+// All eight scale/min pairs of a q4_K / q5_K header at once (scale_min_k4 for every group): byte g of sc[g >> 2] and
+// mn[g >> 2] is group g's 6-bit scale and min. Pair j's two bytes, as kf_q4k_scales returns them, are
+// kf_pair(sc, j) and kf_pair(mn, j).
+__device__ __forceinline__ void kf_q4k_scales8(uint32_t hy, uint32_t hz, uint32_t hw, uint32_t (&sc)[2], uint32_t (&mn)[2]) {
+    sc[0] = hy & 0x3f3f3f3fu;
+    sc[1] = (hw & 0x0f0f0f0fu) | ((hy >> 2) & 0x30303030u);
+    mn[0] = hz & 0x3f3f3f3fu;
+    mn[1] = ((hw >> 4) & 0x0f0f0f0fu) | ((hz >> 2) & 0x30303030u);
+}
+
+__device__ __forceinline__ uint32_t kf_pair(const uint32_t (&v)[2], int j) { return (v[j >> 1] >> (16 * (j & 1))) & 0xffffu; }
+
 // Integer dot of sub-block pair j: qa = nibble bytes 32j..32j+15, qb = 32j+16..32j+31; x0..x3 the 64 activation bytes
 // 64j..64j+63 of the super-block as four 16-byte pieces.
 __device__ __forceinline__ void kf_q4k_pair_dots(const uint4 qa, const uint4 qb, const uint4 x0, const uint4 x1, const uint4 x2,

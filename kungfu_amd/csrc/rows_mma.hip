@@ -77,15 +77,14 @@ template <bool Q5 = false>
 __device__ __forceinline__ void rm_block(const RmW& v, const uint8_t* a_at, int a_gstride, rm_v4h xo, int q, rm_v4i& S, rm_v4f& mins) {
     const uint32_t m4 = 0x0f0f0f0fu, m1 = 0x01010101u;
     S = rm_v4i{0, 0, 0, 0};
-    // the eight 6-bit scales and mins at once (scale_min_k4 for every group, crates/kf-quant/src/types/mod.rs:86-94):
-    // byte g of sc[g / 4] / mn[g / 4] is group g's
-    const uint32_t sc[2] = {v.hd.y & 0x3f3f3f3fu, (v.hd.w & m4) | ((v.hd.y >> 2) & 0x30303030u)};
-    const uint32_t mn[2] = {v.hd.z & 0x3f3f3f3fu, ((v.hd.w >> 4) & m4) | ((v.hd.z >> 2) & 0x30303030u)};
-    // the lane's quarter q: groups 2q and 2q+1
-    const uint32_t mq = ((q < 2 ? mn[0] : mn[1]) >> (16 * (q & 1))) & 0xffffu;
+    // the eight 6-bit scales and mins at once (crates/kf-quant/src/types/mod.rs:86-94); mq: the lane's quarter q,
+    // groups 2q and 2q+1
+    uint32_t sc[2], mn[2];
+    kf_q4k_scales8(v.hd.y, v.hd.z, v.hd.w, sc, mn);
+    const uint32_t mq = kf_pair(mn, q);
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        const uint32_t sc2 = (sc[p >> 1] >> (16 * (p & 1))) & 0xffffu;
+        const uint32_t sc2 = kf_pair(sc, p);
         uint32_t l0 = v.q[p].x & m4, l1 = v.q[p].y & m4, h0 = (v.q[p].x >> 4) & m4, h1 = (v.q[p].y >> 4) & m4;
         if constexpr (Q5) {  // the fifth bit of group g is bit g of the column's qh byte (q5_k.rs:7-60)
             l0 |= ((v.qh.x >> (2 * p)) & m1) << 4;
