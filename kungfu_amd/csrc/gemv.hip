@@ -1121,14 +1121,17 @@ hipError_t launch_gemv(const uint8_t* w, int64_t row_bytes, const int8_t* xq, co
             return hipGetLastError();
         }
     }
-    // the burst variant where every wave of a grid of two blocks a CU has one row (O at 4096 x 4096: 3.9 against
-    // 4.2 us for the pipelined kernel, which waits for its block's activation row first). With more rows a wave it
-    // measured slower than the pipelined kernel (gate+up, 7 rows a wave: 14.4 against 13.1 us; 12.6 even without
-    // the arithmetic), so it takes one-row grids only; KF_GEMV_BURST=n forces it up to n rows a wave (1, 2, 4, 7, 8)
+    // the burst variant where every wave has one row, in a grid of at most four blocks a CU (O at 4096 x 4096, two
+    // blocks a CU: 3.9 against 4.2 us for the pipelined kernel, which waits for its block's activation row first;
+    // QKV at 4096 x 6144, three blocks a CU: 4.65 against 4.95; q8_0 at 4096 x 4096, two waves a row, four blocks a
+    // CU: 5.04 against 5.11). With more rows a wave it measured slower than the pipelined kernel (gate+up, 7 rows a
+    // wave: 14.4 against 13.1 us; 12.6 even without the arithmetic), so it takes one-row grids only;
+    // KF_GEMV_BURST=n forces it up to n rows a wave (1, 2, 4, 7, 8) on a grid of two blocks a CU
     const int burst_rows = kf_knob_on(KF_KNOB_GEMV_BURST) ? kf_knob(KF_KNOB_GEMV_BURST) : 1;
     if (!fused && SPW == 1 && dma && maxit_env == 0 && !kf_knob_on(KF_KNOB_GEMV_NO_PIPE)) {
         const int bpc = kf_knob(KF_KNOB_GEMV_BPC);
         int grid = cu_count() * (bpc > 0 ? bpc : 2);
+        if (!kf_knob_on(KF_KNOB_GEMV_BURST) && bpc <= 0 && groups <= 4 * cu_count()) grid = groups;  // one row a wave
         if (grid > groups) grid = groups;
         const int iters = (groups + grid - 1) / grid;
         const size_t smem = (size_t)GV_WAVES * GV_STEP_BYTES + (WPR > 1 ? (size_t)iters * GV_WAVES * 4 : 0);
