@@ -942,10 +942,12 @@ __device__ __forceinline__ void sk_wait(int rem) {
 }
 
 // Ablation switch for measurement builds only (0 in the product): bit 1 drops the MFMA / VALU work of a chunk, bit 2
-// the split epilogue (partials, ticket and fixup: each block stores its own tile)
+// the split epilogue (partials, ticket and fixup: each block stores its own tile), bit 4 the chunks' DMA (the compute
+// reads whatever the LDS holds)
 #ifndef SK_ABL
 #define SK_ABL 0
 #endif
+
 
 template <int TM, int TN, int G, int NS>
 __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __restrict__ w, int64_t row_bytes, const int8_t* __restrict__ xq,
@@ -990,6 +992,7 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
         vw[i] = r * (int)row_bytes + (e - r * Geo::WCH);
     }
     auto issue = [&](auto kb, int ch) __attribute__((always_inline)) {
+        if (SK_ABL & 4) return;
         uint8_t* b = sk_ring + decltype(kb)::value * Geo::STAGE;
         const int cc = ch0 + ch;
 #pragma unroll
@@ -1042,7 +1045,6 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
                     for (int k = 0; k < 4; k++) acc[t][j][k] = fmaf((float)ci[k], sc[k], acc[t][j][k]);
                 }
             }
-            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // chunk i: wait for this wave's share of it (loads complete in issue order; the chunks after it, up to NS - 2,
