@@ -896,7 +896,7 @@ __global__ void __launch_bounds__(64 * W) gemm_q8_0_mr_kernel(const uint8_t* __r
 }
 
 // ------------------------------------------------------------------------------------------------ split K
-// 17..64 rows with K split across blocks. A block of four waves owns 64 TN weight rows (16 TN a wave) and all TM x 16
+// 1..64 rows with K split across blocks. A block of four waves owns 64 TN weight rows (16 TN a wave) and all TM x 16
 // activation rows, over its share of K in chunks of G groups: the activation chunk (TM x 16 rows x 32 G columns and
 // their group scales, 16-byte piece s of row r staged in slot s ^ (r % 2G) for bank-spread operand reads) is DMA'd
 // once per block and read by all four waves, so the activation bytes moved are about M / (64 TN) times the weight
@@ -1264,19 +1264,25 @@ static bool q8_0_slices_pay(int M, int N, int K, int64_t row_bytes) {
 // none takes the shape
 static hipError_t small_q8_0(const uint8_t* wb, int64_t row_bytes, const int8_t* xq, const float* xd, const float* bias, const float* res,
                              float* y, int M, int N, int K, hipStream_t s) {
-    // 17..64 rows with K split across blocks, for matrices above 4096 x 4096 (MI355X, Llama-3-8B shapes, 32 / 64
+    // 1..64 rows with K split across blocks, for matrices above 4096 x 4096 (MI355X, Llama-3-8B shapes, 32 / 64
     // rows: QKV 17.0 / 23.4 against 21.1 / 28.4 us, gate 26.4 / 38.2 against 35.6 / 50.0, down 27.8 / 38.9
     // against 31.4 / 48.0; O at 4096 x 4096 15.2 / 20.5 against 12.1 / 18.4, so not there). KF_GEMM_SK=0 turns
     // it off, KF_GEMM_SK=1 on for every size (comparison knobs)
     const bool sk = kf_knob_on(KF_KNOB_GEMM_SK) ? kf_knob(KF_KNOB_GEMM_SK) != 0 : (int64_t)N * K > (1ll << 24);
-    if (M > 16 && M <= 64 && K % 128 == 0 && (K / 32) % 2 == 0 && sk) {
+    if (M <= 64 && K % 128 == 0 && (K / 32) % 2 == 0 && sk) {
         const int var = kf_knob_or(KF_KNOB_GEMM_SK_V, 0);  // 10 G + NS (groups a chunk, ring stages): a tuning knob
         // 8-group chunks in two stages where K allows (MI355X, Llama-3-8B shapes at 32 / 64 rows: gate 25.1 / 37.2
         // against 26.0 / 38.3 us with 4-group chunks in three, down 24.5 / 37.4 against 25.3 / 39.3)
         const int v = var ? var : K % 256 == 0 ? 82 : 43;
         hipError_t e = hipErrorNotSupported;
         if (K % (32 * (v / 10)) == 0) {
-            if (M <= 32)
+            // 1..16 rows: one staged 16-row tile (MI355X, Llama-3-8B shapes at 8 / 16 rows: QKV 11.0 / 11.4 against
+            // 12.1 / 12.9 us for the small-batch kernel, gate 17.9 / 19.0 against 21.3 / 21.9, down 18.0 / 18.2
+            // against 19.4 / 23.1: that kernel fills fewer than one wave a SIMD on these grids); 8-group chunks only
+            // (a 16-row tile of 4-group chunks is not whole DMA instructions)
+            if (M <= 16) {
+                if (K % 256 == 0) e = gemm_sk_launch<1, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s);
+            } else if (M <= 32)
                 e = v == 83    ? gemm_sk_launch<2, 1, 8, 3>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
                     : v == 82  ? gemm_sk_launch<2, 1, 8, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)
                     : v == 162 ? gemm_sk_launch<2, 1, 16, 2>(wb, row_bytes, xq, xd, bias, res, y, M, N, K, s)

@@ -611,14 +611,17 @@ def test_gemm_q8_0_all_rows_one_pass_variants(cuda, knobs, variant, rows, n, n_o
                                                      (64, 4096, 14336, None, None), (50, 384, 200, None, None),
                                                      (64, 1024, 64, None, None), (24, 1024, 256, 4, None),
                                                      (40, 4096, 1000, None, 43), (64, 14336, 520, 5, 43),
-                                                     (20, 4096, 700, None, 83), (64, 2048, 300, None, 162)])
+                                                     (20, 4096, 700, None, 83), (64, 2048, 300, None, 162),
+                                                     (1, 4096, 6144, None, None), (8, 4096, 14336, None, None),
+                                                     (16, 14336, 4096, None, None), (5, 1024, 200, 3, None),
+                                                     (13, 4096, 520, None, 162)])
 def test_gemm_q8_0_split_k(cuda, knobs, rows, n, n_out, splits, var):
-    """17..64 Q8_0 rows with K split across blocks (partials summed in split order by the last block of each tile),
+    """1..64 Q8_0 rows with K split across blocks (partials summed in split order by the last block of each tile),
     forced on for every size (KF_GEMM_SK=1; by default it takes matrices above 4096 x 4096): ragged rows and output
-    tiles, split counts that do not divide the chunks (7 of 56; 4 of 4: one chunk a split), the chunk forms (4, 8, 16
-    groups; two or three stages: KF_GEMM_SK_V), three calls in a row on one stream (the tickets return to zero), bias
-    and residual; against the CPU backend, bit-identical between calls (deterministic), and within the f32 bar of the
-    scratch-free products (KF_GEMM_SK=0)."""
+    tiles (one to sixteen rows in one staged 16-row tile), split counts that do not divide the chunks (7 of 56; 4 of
+    4: one chunk a split), the chunk forms (4, 8, 16 groups; two or three stages: KF_GEMM_SK_V), three calls in a row
+    on one stream (the tickets return to zero), bias and residual; against the CPU backend, bit-identical between
+    calls (deterministic), and within the f32 bar of the scratch-free products (KF_GEMM_SK=0)."""
     import torch
 
     knobs.setenv("KF_GEMM_SK", "1")
