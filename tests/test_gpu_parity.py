@@ -404,10 +404,15 @@ def test_gemm_q4_k_random_blocks_and_extreme_sums(cuda):
     _close(y.cpu().numpy(), oracle.matmul_slice(kf.TYPE_Q4_K, w, n, n_out, x))
 
 
+# Rows of the full-size prefill checks: every 97th row, the rows either side of the 64- and 128-row tile edges at both
+# ends, and the last rows (whole rows, so every column tile, the tail-split ones included)
+PREFILL_ROWS = sorted(set(range(0, 2048, 97)) | {63, 64, 127, 128, 1919, 1920, 1983, 1984, 2046, 2047})
+
+
 @pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
 def test_gemm_q4_k_prefill_shapes_match_gemv(cuda, n, n_out):
-    """Q4_K at the Llama-3-8B shapes and M = 2048: every 97th row of the GEMM against the GEMV of that row on the same
-    quantized activations, and the sampled rows against the CPU backend's matmul_slice (rows are independent)."""
+    """Q4_K at the Llama-3-8B shapes and M = 2048: the PREFILL_ROWS rows of the GEMM against the GEMV of that row on
+    the same quantized activations, and against the CPU backend's matmul_slice (rows are independent)."""
     import torch
 
     rows = 2048
@@ -421,14 +426,14 @@ def test_gemm_q4_k_prefill_shapes_match_gemv(cuda, n, n_out):
     one = kf.alloc_act(1, n, cuda)
     oviews = kf.act_views(one, 1, n)
     yr = torch.empty((1, n_out), device=cuda)
-    for r in range(0, rows, 97):
+    for r in PREFILL_ROWS:
         for src, dst in zip(views, oviews):
             dst.copy_(src[r : r + 1])
         kf.gemv(kf.TYPE_Q4_K, w, one, yr, 1, n, n_out)
         torch.cuda.synchronize()
         _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())
     # rows are independent: the sampled rows against the CPU backend itself
-    sample = list(range(0, rows, 97))
+    sample = PREFILL_ROWS
     want = oracle.matmul_slice(kf.TYPE_Q4_K, w.cpu().numpy(), n, n_out, x[sample].cpu().numpy())
     _close(y[sample].cpu().numpy(), want)
 
@@ -451,8 +456,8 @@ def test_matmul_q4_k_many_rows(cuda, rows, n_out):
 
 @pytest.mark.parametrize("n,n_out", [(4096, 14336), (14336, 4096)])
 def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
-    """Config C4 at full size (M = 2048): every 97th row of the GEMM against the GEMV of that row on the same
-    quantized activations, and the sampled rows against the CPU backend's matmul_slice (rows are independent)."""
+    """Config C4 at full size (M = 2048): the PREFILL_ROWS rows of the GEMM against the GEMV of that row on the same
+    quantized activations, and against the CPU backend's matmul_slice (rows are independent)."""
     import torch
 
     rows = 2048
@@ -466,14 +471,14 @@ def test_gemm_prefill_shapes_match_gemv(cuda, n, n_out):
     one = kf.alloc_act(1, n, cuda)
     oq, od16, os16, od32, os32 = kf.act_views(one, 1, n)
     yr = torch.empty((1, n_out), device=cuda)
-    for r in range(0, rows, 97):
+    for r in PREFILL_ROWS:
         for src, dst in ((q, oq), (d16, od16), (s16, os16), (d32, od32), (s32, os32)):
             dst.copy_(src[r : r + 1])
         kf.gemv(kf.TYPE_Q8_0, w, one, yr, 1, n, n_out)
         torch.cuda.synchronize()
         _close(y[r : r + 1].cpu().numpy(), yr.cpu().numpy())
     # rows are independent: the sampled rows against the CPU backend itself
-    sample = list(range(0, rows, 97))
+    sample = PREFILL_ROWS
     want = oracle.matmul_slice(kf.TYPE_Q8_0, w.cpu().numpy(), n, n_out, x[sample].cpu().numpy())
     _close(y[sample].cpu().numpy(), want)
 
