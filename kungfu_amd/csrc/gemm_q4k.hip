@@ -31,9 +31,10 @@
 //   * staging is buffer_load ... lds DMA over buffer resources based at the tile's first rows; rows past M or N read
 //     as zeros through the hardware range check. Blocks run in XCD order (each XCD a contiguous range of tiles, M
 //     fastest), so the blocks in flight on an XCD share their weight tiles in its L2.
-// Measured at M = 2048 (ablation builds, us): gate/up 333 in all (MFMA with its LDS operand reads alone 147, the
-// staging alone 91), each of the staging, the plane expansion and the rescale adding 50-60 us: the matrix core and the
-// VALU of one wave still mostly take turns, which is what bounds the kernel.
+// Measured at M = 2048 (ablation builds, gate / down, us): 305-314 / 271-278 in all; the MFMA phase alone (no DMA,
+// rescale or plane expansion) 218-225 / 186-189, with the plane expansion 225 / 186, with the rescale 265 / 229,
+// with the DMA 245 / 216. The MFMA phase itself keeps the matrix cores about half busy, and the rescale and the DMA
+// add to it.
 #include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_device.h"
@@ -251,7 +252,10 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
             const uint32_t v[4] = {raw.x, raw.y, raw.z, raw.w};
             v4i bl[2], bh[2];
             if (G4_ABL & 4) {
-                bl[0] = bh[0] = bl[1] = bh[1] = v4i{(int)raw.x, (int)raw.y, (int)raw.z, (int)raw.w};
+                // the high plane a permutation of the low one: identical operands let the compiler merge the two
+                // MFMAs of a tile and group, halving the matrix-core work the ablation measures
+                bl[0] = bl[1] = v4i{(int)raw.x, (int)raw.y, (int)raw.z, (int)raw.w};
+                bh[0] = bh[1] = v4i{(int)raw.y, (int)raw.z, (int)raw.w, (int)raw.x};
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
