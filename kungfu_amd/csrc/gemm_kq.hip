@@ -101,7 +101,9 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
                                                                  const float* __restrict__ xd32, const float* __restrict__ bias,
                                                                  const float* __restrict__ res, float* __restrict__ y, int M, int N, int K,
                                                                  KqTail tail_arg, KqMoe moe) {
-    const KqTail tail = MOE ? KqTail{nullptr, nullptr, 0, 1} : tail_arg;  // the grouped form never splits
+    const KqTail tail = MOE ? KqTail{nullptr, nullptr, 0, 1} : tail_arg;  // the dense form's tail split
+    // the grouped form splits K in two over every tile when its launcher passes the scratch (msplit)
+    const bool msplit = MOE && tail_arg.part != nullptr;
     using G = KqGeo<TY>;
     __shared__ __align__(16) uint8_t buf0[G::STAGE];
     __shared__ __align__(16) uint8_t buf1[G::STAGE];
@@ -123,6 +125,21 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
         tm = t - tn * mt;
         s0 = nsb * sp / tail.S;
         s1 = nsb * (sp + 1) / tail.S;
+    } else if (msplit) {
+        // the two K halves of tile tt, in XCD order: XCD x (blocks go to the eight XCDs round-robin) takes a contiguous
+        // range of tiles, both halves of each, so the blocks of an expert's weight tiles share them in its L2
+        const int T = ((N + KQ_BN - 1) / KQ_BN) * mt, b = blockIdx.x;
+        if ((T & 7) == 0) {
+            tt = (b & 7) * (T >> 3) + (b >> 4);
+            sp = (b >> 3) & 1;
+        } else {
+            tt = b >> 1;
+            sp = b & 1;
+        }
+        tn = tt / mt;
+        tm = tt - tn * mt;
+        s0 = nsb * sp / 2;
+        s1 = nsb * (sp + 1) / 2;
     } else {
         kq_tile(tail.part ? tail.full : ((N + KQ_BN - 1) / KQ_BN) * mt, mt, blockIdx.x, tm, tn);
     }
@@ -383,6 +400,60 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
     }
 
     const int n = n0 + wave * 32 + r32;
+    if (MOE && msplit) {
+        // The two K halves of a grouped tile. The first half leaves its partial in y (the tile's output rows) and the
+        // second in the scratch, each with system-scope stores, which write through to memory, then each takes the
+        // tile's ticket; the second to arrive reads the other's partial from its place and stores the sum. A sum of
+        // two is the same in either order, so the result does not depend on which half arrives last.
+        constexpr int R = KQ_TM * 16;
+        float* pp = tail_arg.part + (size_t)tt * R * KQ_THREADS + tid;
+        auto yo = [&](int i, int r) __attribute__((always_inline)) {
+            const int m = m0 + i * 32 + (r & 3) + 8 * (r >> 2) + 4 * half;
+            return m >= m_end ? (int64_t)-1 : (int64_t)(moe.out_rows ? moe.out_rows[m] : m) * N + n;
+        };
+        if (sp == 1) {
+#pragma unroll
+            for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) __hip_atomic_store(pp + (i * 16 + r) * KQ_THREADS, acc[i][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        } else if (n < N) {
+#pragma unroll
+            for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t o = yo(i, r);
+                    if (o >= 0) __hip_atomic_store(y + o, acc[i][r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+        __syncthreads();
+        if (tid == 0) last = __hip_atomic_fetch_add(&tail_arg.tickets[tt], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) == 1;
+        __syncthreads();
+        if (!last) return;
+        if (sp == 0) {
+            float other[R];
+#pragma unroll
+            for (int e = 0; e < R; e++) other[e] = __hip_atomic_load(pp + e * KQ_THREADS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+            for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][r] = acc[i][r] + other[i * 16 + r];
+        } else if (n < N) {
+            float other[R];
+#pragma unroll
+            for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int64_t o = yo(i, r);
+                    other[i * 16 + r] = o >= 0 ? __hip_atomic_load(y + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) : 0.0f;
+                }
+#pragma unroll
+            for (int i = 0; i < KQ_TM; i++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[i][r] = other[i * 16 + r] + acc[i][r];
+        }
+        if (tid == 0) __hip_atomic_store(&tail_arg.tickets[tt], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
     if (n < N) {
         const float bn = bias ? bias[n] : 0.0f;
 #pragma unroll
@@ -468,8 +539,21 @@ hipError_t kf_launch_gemm_kq_moe(const void* w, const void* w2, int64_t expert_b
     // row tiles over all slots: each slot adds at most one partial tile
     const int mt = (pairs + KQ_BM - 1) / KQ_BM + n_slots;
     const KqMoe moe{offsets, out_rows, static_cast<const uint8_t*>(w2), expert_bytes, n_slots, n_split};
-    gemm_kq_kernel<KF_TYPE_Q4_K, true><<<((N + KQ_BN - 1) / KQ_BN) * mt, KQ_THREADS, 0, s>>>(
+    // Grids of at most two rounds of the CUs (by the tile bound; down at 512 tokens top-2: 384 tiles, about 320 live)
+    // run every tile as two K halves: a second round a quarter full would otherwise take as long as a full one. It
+    // needs the split scratch, one partial tile per tile (KF_GEMM_NO_TAIL turns it off, a comparison knob)
+    const int T = ((N + KQ_BN - 1) / KQ_BN) * mt;
+    KqTail split{nullptr, nullptr, 0, 1};
+    int blocks = T;
+    if (T <= 2 * kf_cu_count() && K / 256 >= 4 && T <= KF_SPLIT_TICKETS &&
+        (size_t)T * KQ_TM * 16 * KQ_THREADS * 4 <= KF_SPLIT_SCRATCH - (size_t)KF_SPLIT_TICKETS * 4 && !kf_knob_on(KF_KNOB_GEMM_NO_TAIL)) {
+        if (char* scr = static_cast<char*>(kf_split_scratch(s))) {
+            split = KqTail{reinterpret_cast<float*>(scr + (size_t)KF_SPLIT_TICKETS * 4), reinterpret_cast<int*>(scr), 0, 2};
+            blocks = 2 * T;
+        }
+    }
+    gemm_kq_kernel<KF_TYPE_Q4_K, true><<<blocks, KQ_THREADS, 0, s>>>(
         static_cast<const uint8_t*>(w), row_bytes, reinterpret_cast<const int8_t*>(base + o.q), reinterpret_cast<const _Float16*>(base + o.xa),
-        reinterpret_cast<const float*>(base + o.d32), nullptr, nullptr, y, mt * KQ_BM, N, K, KqTail{nullptr, nullptr, 0, 1}, moe);
+        reinterpret_cast<const float*>(base + o.d32), nullptr, nullptr, y, mt * KQ_BM, N, K, split, moe);
     return hipGetLastError();
 }

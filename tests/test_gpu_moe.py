@@ -316,14 +316,19 @@ def test_moe_ffn_128_experts_top_8(cuda, rows):
     _check_layer(got, stages, args, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows)
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("kq", ["0", "1"])
 @pytest.mark.parametrize("rows,n_exp", [(512, 8), (100, 3)])
-def test_moe_ffn_grouped_gemm_top_2(cuda, knobs, rows, n_exp, kq):
+def test_moe_ffn_grouped_gemm_top_2(cuda, knobs, rows, n_exp, kq, split):
     """Past 64 routed pairs the q4_K layer runs on the grouped tile GEMM (KF_MOE_KQ: 0 the split-scale kernel, 128-row
     tiles; 1 the one-MFMA-per-group kernel, 64-row tiles): 512 tokens top-2 over eight experts (about 128 pairs an
     expert, several row tiles each), and 100 tokens over three (the last tile of a slot partial), with some pairs
-    unused; sampled tokens against the CPU backend stage by stage and the float path."""
+    unused; sampled tokens against the CPU backend stage by stage and the float path. The one-MFMA-per-group kernel
+    runs grids of at most two rounds as two K halves a tile (these layers' launches all are); KF_GEMM_NO_TAIL runs
+    them whole."""
     knobs.setenv("KF_MOE_KQ", kq)
+    if not split:
+        knobs.setenv("KF_GEMM_NO_TAIL", "1")
     n_embd, n_ff, n_used = 1024, 1536, 2
     args, got, stages = _moe_layer(cuda, kf.TYPE_Q4_K, n_exp, n_embd, n_ff, rows, n_used, 70 + n_exp, drop=0.05)
     assert "gu" in stages
