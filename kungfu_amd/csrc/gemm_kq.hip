@@ -210,10 +210,12 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
         return *reinterpret_cast<const v4i*>(cur + G::A + (i * 32 + r32) * 256 + 16 * ((2 * g + half) ^ sw));
     };
 
-    auto stage = [&](const uint8_t* cur, int sb) __attribute__((always_inline)) {
+    // TLC: the 32-row tiles of the block that hold rows (a grouped tile with at most 32 rows skips its second)
+    auto stage = [&](auto tlc, const uint8_t* cur, int sb) __attribute__((always_inline)) {
+        constexpr int TL = decltype(tlc)::value;
         v16i S[KQ_TM];
 #pragma unroll
-        for (int i = 0; i < KQ_TM; i++) S[i] = v16i{};
+        for (int i = 0; i < TL; i++) S[i] = v16i{};
         float d, dm = 0.0f;
         v8h mo;
         if constexpr (!G::Q6) {
@@ -243,7 +245,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
 #pragma unroll
                 for (int e = 0; e < 4; e++) b[e] = (int)((((g & 1) ? v[e] >> 4 : v[e]) & m4) | (((qhv[e] >> g) & m1) << 4));
 #pragma unroll
-                for (int i = 0; i < KQ_TM; i++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop(cur, g, i), b, v16i{}, 0, 0, 0);
+                for (int i = 0; i < TL; i++) I[i] = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop(cur, g, i), b, v16i{}, 0, 0, 0);
             };
             // Software-pipelined by one group: group g + 1's MFMAs are issued before group g's multiply-adds, which
             // depend on none of them, so the adds run while the matrix core works. The running sums are
@@ -253,11 +255,11 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
             auto mads = [&](int g, const v16i (&I)[KQ_TM]) __attribute__((always_inline)) {
                 const int sc = (int)((g & 1) ? sc2[g / 2] >> 8 : sc2[g / 2] & 0xffu);
 #pragma unroll
-                for (int i = 0; i < KQ_TM; i++)
+                for (int i = 0; i < TL; i++)
 #pragma unroll
                     for (int r = 0; r < 16; r++) S[i][r] += __mul24(sc, I[i][r]);  // |sc I| < 2^22
 #pragma unroll
-                for (int i = 0; i < KQ_TM; i++) __asm__ volatile("" : "+v"(S[i]));
+                for (int i = 0; i < TL; i++) __asm__ volatile("" : "+v"(S[i]));
             };
             issue(std::integral_constant<int, 0>{}, Ia);
             __builtin_amdgcn_sched_barrier(0);
@@ -315,7 +317,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
                     const int s0 = (int)(int8_t)(uint8_t)(scw[si >> 2] >> (8 * (si & 3)));
                     const int s1 = (int)(int8_t)(uint8_t)(scw[(si + 1) >> 2] >> (8 * ((si + 1) & 3)));
 #pragma unroll
-                    for (int i = 0; i < KQ_TM; i++) {
+                    for (int i = 0; i < TL; i++) {
                         const v4i a = aop(cur, 4 * h + gg, i);
                         const v16i I0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b0, v16i{}, 0, 0, 0);
                         const v16i I1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b1, v16i{}, 0, 0, 0);
@@ -324,7 +326,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
                         for (int r = 0; r < 16; r++) S[i][r] += __mul24(s0, I0[r]) + __mul24(s1, I1[r]);
                     }
 #pragma unroll
-                    for (int i = 0; i < KQ_TM; i++) __asm__ volatile("" : "+v"(S[i]));
+                    for (int i = 0; i < TL; i++) __asm__ volatile("" : "+v"(S[i]));
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }
@@ -332,7 +334,7 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
         }
         // acc += dx (d S - dmin mins); accumulator register r holds row (r % 4) + 8 (r / 4) + 4 (lane / 32)
 #pragma unroll
-        for (int i = 0; i < KQ_TM; i++) {
+        for (int i = 0; i < TL; i++) {
             v16f mins = v16f{};
             if constexpr (!G::Q6) {
                 const v8h xo = *reinterpret_cast<const v8h*>(cur + G::XS + (i * 32 + r32) * 32 + half * 16);
@@ -353,22 +355,30 @@ __global__ void __launch_bounds__(KQ_THREADS, 1) gemm_kq_kernel(const uint8_t* _
     };
 
     // stage sb multiplies one buffer while sb + 1 lands in the other; every DMA wait is explicit
-    dma(buf0, s0);
-    __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
-    __syncthreads();
-#pragma unroll 1
-    for (int sb = s0; sb < s1; sb += 2) {
-        if (sb + 1 < s1) dma(buf1, sb + 1);
-        stage(buf0, sb);
+    auto kloop = [&](auto tlc) __attribute__((always_inline)) {
+        dma(buf0, s0);
         __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
         __syncthreads();
-        if (sb + 1 < s1) {
-            if (sb + 2 < s1) dma(buf0, sb + 2);
-            stage(buf1, sb + 1);
+#pragma unroll 1
+        for (int sb = s0; sb < s1; sb += 2) {
+            if (sb + 1 < s1) dma(buf1, sb + 1);
+            stage(tlc, buf0, sb);
             __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
             __syncthreads();
+            if (sb + 1 < s1) {
+                if (sb + 2 < s1) dma(buf0, sb + 2);
+                stage(tlc, buf1, sb + 1);
+                __builtin_amdgcn_s_waitcnt(KF_WAITCNT_VM(0));
+                __syncthreads();
+            }
         }
-    }
+    };
+    // a grouped slot's last tile often holds a few rows: with at most 32 the second 32-row tile's MFMAs, adds and
+    // rescale are skipped (its accumulators stay zero and its rows are not stored)
+    if (MOE && m_end - m0 <= 32)
+        kloop(std::integral_constant<int, 1>{});
+    else
+        kloop(std::integral_constant<int, KQ_TM>{});
 
     if (!MOE && sp >= 0) {
         // a split: its partial tile through system-scope stores (they write through to memory, so the other splits'
