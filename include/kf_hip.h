@@ -224,7 +224,9 @@ int kf_hip_moe_gemv(uint32_t ty, const void* w, const void* w_up, int64_t expert
  * from w + s * expert_bytes and columns n_split.. from w2 + s * expert_bytes (gate and up as one product). Output row p
  * of the group order is written to y row out_rows[p] (device, nullable: row p); y is [*][n_out]. Rows of act past
  * offsets[n_slots] are not read. Replaces kf8_gemm_moe (crates/kf-backend-cuda/src/kernels/kf8.cu:400-416) without the
- * KF8 unpack; kf_hip_moe_ffn takes it past 64 routed pairs, as expert_gemm_chunks (exec.rs:2196-2237). */
+ * KF8 unpack; kf_hip_moe_ffn takes it past 64 routed pairs, as expert_gemm_chunks (exec.rs:2196-2237). A grid of at
+ * most two rounds of the CUs runs each tile as two K halves through the split scratch (the stream's slot); the first
+ * half's partial passes through the tile's rows of y before the sum lands there. */
 int kf_hip_moe_gemm(uint32_t ty, const void* w, const void* w2, int64_t expert_bytes, int64_t row_bytes, int n_split, const void* act,
                     int pairs, int n, int n_out, const int32_t* offsets, int n_slots, const int32_t* out_rows, float* y, void* stream);
 
