@@ -495,8 +495,10 @@ struct GmTail {
 //     stage's data at offset (136 st) % 16), so the DMA needs only aligned pieces. Rows are 16-byte aligned when
 //     K % 256 == 0, and the last stage (st odd) ends exactly at the row's end;
 //   * activation scales: [row][4] f32 per stage.
-// The two stage buffers (36 KB each) are distinct static LDS arrays, so the compiler can tell a DMA into one from
-// reads of the other. Eight waves, each a 64 x 32 tile;
+// The DMA is inline assembly (kf_adma16): issued through the builtin, it carries no alias information, so the
+// compiler waited for every DMA in flight (the next stage's included) before the first LDS read of each stage and the
+// double buffer never overlapped. The waits are explicit instead: each stage ends with vmcnt(0) and a barrier, after
+// which the other buffer's DMA (issued at the stage's start) has landed. Eight waves, each a 64 x 32 tile;
 // blocks in XCD order. Wave tiles of 2 x 2 measured slower (their 128 x 256 block halves the blocks per CU).
 // gemm_q8_0_kernel (register staging) remains for K % 256 != 0.
 template <int WM, int WN, int TM, int TN>
@@ -550,9 +552,9 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
 
     // DMA sources: buffer resources over the tile's first rows; per-lane offsets fixed for the K loop, a stage adds
     // only a scalar offset (rows past M or N are clamped to the last one)
-    const auto rw = kf_rsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
-    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
-    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
+    const auto rw = kf_arsrc(w + (int64_t)n0 * row_bytes, (uint64_t)(N - n0) * row_bytes);
+    const auto rx = kf_arsrc(xq + (int64_t)m0 * K, (uint64_t)(M - m0) * K);
+    const auto rd = kf_arsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(M - m0) * kg * 4);
     constexpr int IA = (C::NA + C::W - 1) / C::W, IB = (C::NB + C::W - 1) / C::W, ID = (C::ND + C::W - 1) / C::W;
     int va[IA], vb[IB], vd[ID];
 #pragma unroll
@@ -571,18 +573,18 @@ __global__ void __launch_bounds__(64 * WM * WN, 8 / (WM * WN)) gemm_q8_0_dma_ker
 #pragma unroll
         for (int it = 0; it < IA; it++) {
             const int q = wave + it * C::W;
-            if (C::NA % C::W == 0 || q < C::NA) kf_bdma16(rx, va[it], st * GM_BK, buf + q * 1024);
+            if (C::NA % C::W == 0 || q < C::NA) kf_adma16(rx, va[it], st * GM_BK, buf + q * 1024);
         }
         const int wbase = (136 * st) & ~15;
 #pragma unroll
         for (int it = 0; it < IB; it++) {
             const int q = wave + it * C::W;
-            if (C::NB % C::W == 0 || q < C::NB) kf_bdma16(rw, vb[it], wbase, buf + C::B_OFF + q * 1024);
+            if (C::NB % C::W == 0 || q < C::NB) kf_adma16(rw, vb[it], wbase, buf + C::B_OFF + q * 1024);
         }
 #pragma unroll
         for (int it = 0; it < ID; it++) {
             const int q = wave + it * C::W;
-            if (q < C::ND) kf_bdma16(rd, vd[it], st * GM_G * 4, buf + C::D_OFF + q * 1024);
+            if (q < C::ND) kf_adma16(rd, vd[it], st * GM_G * 4, buf + C::D_OFF + q * 1024);
         }
     };
 

@@ -29,9 +29,12 @@
 //   * the MFMA phase runs at raised wave priority (s_setprio 1), so a SIMD's MFMA-issuing wave goes first and its
 //     rescaling neighbour fills the issue slots left (8% faster);
 //   * staging is buffer_load ... lds DMA over buffer resources based at the tile's first rows; rows past M or N read
-//     as zeros through the hardware range check. Blocks run in XCD order (each XCD a contiguous range of tiles, M
+//     as zeros through the hardware range check. The DMA is inline assembly (kf_adma16 / kf_adma4) with explicit
+//     waits (vmcnt(0) and a barrier at each stage's end): through the builtin it carries no alias information and
+//     the compiler waited for the next stage's DMA before each MFMA phase (3% slower). Blocks run in XCD order (each XCD a contiguous range of tiles, M
 //     fastest), so the blocks in flight on an XCD share their weight tiles in its L2.
-// Measured at M = 2048 (ablation builds, gate / down, us): 305-314 / 271-278 in all; the MFMA phase alone (no DMA,
+// Measured at M = 2048 (ablation builds with the builtin DMA, gate / down, us): 305-314 / 271-278 in all (300 / 268
+// with the DMA in assembly); the MFMA phase alone (no DMA,
 // rescale or plane expansion) 218-225 / 186-189, with the plane expansion 225 / 186, with the rescale 265 / 229,
 // with the DMA 245 / 216. The MFMA phase itself keeps the matrix cores about half busy, and the rescale and the DMA
 // add to it.
@@ -192,10 +195,10 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
 
     // DMA sources: buffer resources over the tile's first rows to the end of the matrix; rows past M or N read as
     // zeros (the hardware range check), and their outputs are not stored
-    const auto rw = kf_rsrc(wt, (uint64_t)(n_end - n0) * row_bytes);
-    const auto rx = kf_rsrc(xq + (int64_t)m0 * K, (uint64_t)(m_end - m0) * K);
-    const auto rs = kf_rsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(m_end - m0) * nsb * 32);
-    const auto rd = kf_rsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(m_end - m0) * kg * 4);
+    const auto rw = kf_arsrc(wt, (uint64_t)(n_end - n0) * row_bytes);
+    const auto rx = kf_arsrc(xq + (int64_t)m0 * K, (uint64_t)(m_end - m0) * K);
+    const auto rs = kf_arsrc(xa + (int64_t)m0 * nsb * 16, (uint64_t)(m_end - m0) * nsb * 32);
+    const auto rd = kf_arsrc(xd32 + (int64_t)m0 * kg, (uint64_t)(m_end - m0) * kg * 4);
     // Every DMA instruction reads whole rows: 4 activation rows of 256 bytes, or 64 consecutive 16-byte pieces of the
     // weight rows' 144-byte super-blocks (about seven rows), so each 128-byte line a stage needs crosses from L2 once
     // per instruction. Activation instruction i (rows 4 i..) is wave i % 8's; lane l takes chunk (l % 16) ^ (row % 8)
@@ -216,15 +219,15 @@ __global__ void __launch_bounds__(G4_THREADS, 1) gemm_q4k_kernel(const uint8_t* 
     // reads of the previous records would wait for)
     auto dma = [&](uint8_t* buf, int sb) __attribute__((always_inline)) {
 #pragma unroll
-        for (int k = 0; k < G4_NA / G4_WAVES; k++) kf_bdma16(rx, va, sb * 256 + 32 * K * k, buf + G4_A + (wave + G4_WAVES * k) * 1024);
+        for (int k = 0; k < G4_NA / G4_WAVES; k++) kf_adma16(rx, va, sb * 256 + 32 * K * k, buf + G4_A + (wave + G4_WAVES * k) * 1024);
 #pragma unroll
         for (int k = 0; k < (G4_NW + G4_WAVES - 1) / G4_WAVES; k++)
             if (wave + G4_WAVES * k < G4_NW)
-                kf_bdma16(rw, wpiece(wave + G4_WAVES * k), sb * KF_Q4_K_BYTES, buf + G4_W + (wave + G4_WAVES * k) * 1024);
+                kf_adma16(rw, wpiece(wave + G4_WAVES * k), sb * KF_Q4_K_BYTES, buf + G4_W + (wave + G4_WAVES * k) * 1024);
         if (!late) {
             uint8_t* rec = record(sb);
-            if (wave < 2) kf_bdma4(rd, vd, sb * 32, rec + G4_DX + wave * 256);
-            if (wave * 32 < G4_BM) kf_bdma16(rs, vs, sb * 32, rec + G4_XS + wave * 1024);
+            if (wave < 2) kf_adma4(rd, vd, sb * 32, rec + G4_DX + wave * 256);
+            if (wave * 32 < G4_BM) kf_adma16(rs, vs, sb * 32, rec + G4_XS + wave * 1024);
         }
     };
 
