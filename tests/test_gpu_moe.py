@@ -340,14 +340,17 @@ def test_moe_ffn_grouped_gemm_top_2(cuda, knobs, rows, n_exp, kq, split):
     assert np.abs(got - flt).max() <= 2e-2 * max(np.abs(flt).mean(), 1e-6)
 
 
-def test_grouped_gemm_partial_row_tiles(cuda):
-    """Slots whose rows end just past a 128-row tile (1, 17 or 32 rows in the last tile), slots of 5, 32 and 33 rows,
-    an empty slot: the tiles holding at most 32 rows run the one-tile K loop, the others the full one; every row of
-    every slot against the CPU backend's integer product for its expert."""
+@pytest.mark.parametrize("kq", ["0", "1"])
+def test_grouped_gemm_partial_row_tiles(cuda, knobs, kq):
+    """Slots whose rows end past a row tile (1, 17, 32, 62 or 72 rows in the last 128-row tile), slots of 5, 32 and 33
+    rows, an empty slot, on both grouped kernels (the one-MFMA-per-group kernel's tiles holding at most 32 rows run its
+    one-tile K loop, the others the full one); every row of every slot against the CPU backend's integer product for
+    its expert."""
     import torch
 
+    knobs.setenv("KF_MOE_KQ", kq)
     ty, n, n_out = kf.TYPE_Q4_K, 1024, 768
-    sizes = [129, 145, 32, 33, 5, 0, 160]
+    sizes = [129, 145, 32, 33, 5, 0, 160, 190, 200]
     n_exp = len(sizes)
     offs = np.concatenate([[0], np.cumsum(sizes)]).astype(np.int32)
     pairs = int(offs[-1])
