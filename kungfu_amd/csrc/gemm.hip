@@ -249,6 +249,7 @@ __global__ void __launch_bounds__(GM_THREADS, 2) gemm_q8_0_kernel(const uint8_t*
 // tree in LDS.
 typedef long v1l;
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef uint32_t v2u_sk __attribute__((ext_vector_type(2)));
 typedef int v4i_ __attribute__((ext_vector_type(4)));
 
 // The 8 bytes at a 2-byte aligned LDS address as a long: aligned dwords realigned by v_alignbyte_b32 (an LDS read
@@ -1036,9 +1037,10 @@ __global__ void __launch_bounds__(256) gemm_q8_0_sk_kernel(const uint8_t* __rest
                 const int r = 16 * t + c;
                 const int sl = (2 * g + (q >> 1)) ^ (r % Geo::P);
                 const long a = *reinterpret_cast<const long*>(b + r * Geo::RB + 16 * sl + 8 * (q & 1));
-                const _Float16 dx = (_Float16)*reinterpret_cast<const float*>(b + Geo::ACT + Geo::R * 4 * g + 4 * r);
-                v4h sa = v4h{};
-                sa[0] = q == 0 ? dx : (_Float16)0.0f;
+                // the row's scale at k = 0 of every k-block: sb is zero past k = 0, so the copies on lanes q > 0 meet
+                // zeros; Q8_0-kind activation scales are f16-rounded values, so the truncating conversion is exact
+                const float dx = *reinterpret_cast<const float*>(b + Geo::ACT + Geo::R * 4 * g + 4 * r);
+                const v4h sa = __builtin_bit_cast(v4h, v2u_sk{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(dx, 0.0f)), 0u});
 #pragma unroll
                 for (int j = 0; j < TN; j++) {
                     const v4i_ ci = __builtin_amdgcn_mfma_i32_16x16x32_i8(a, bq[j], v4i_{}, 0, 0, 0);
