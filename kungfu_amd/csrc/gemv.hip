@@ -711,13 +711,17 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
     const float* sd = reinterpret_cast<const float*>(smem + L.scales);
     const int blk = sp * PER_STEP + (TY == KF_TYPE_Q4_K ? (lane >> 2) : lane);
     float* part = reinterpret_cast<float*>(smem + L.part);
+    // the row group of iteration it: with one wave a row the grid sweeps the matrix (iteration it of every block is a
+    // contiguous stretch), with split rows each block walks a contiguous range of its own (MI355X, q4_K down 14336 x
+    // 4096: 7.42-7.47 against 7.56-7.59 us; gate+up at one wave a row 13.5 against 13.2-13.3 the other way)
+    auto grp = [&](int it) { return WPR > 1 ? (int)blockIdx.x * iters + it : it * B + (int)blockIdx.x; };
     // iterations whose row exists for this wave; loads past them reload the wave's own last row (spread over the
     // chip, unlike a clamp to the matrix's last row, which would send every such wave to the same cache lines)
     int iw = iters;
-    while (iw > 0 && ((iw - 1) * B + (int)blockIdx.x) * RPB + rg >= n_out) iw--;
+    while (iw > 0 && grp(iw - 1) * RPB + rg >= n_out) iw--;
     if (iw == 0) iw = 1;  // a wave without rows still runs the barrier; it reloads row rg of the block's first group
     auto row_ptr = [&](int it) {
-        const int o = min((min(it, iw - 1) * B + (int)blockIdx.x) * RPB + rg, n_out - 1);
+        const int o = min(grp(min(it, iw - 1)) * RPB + rg, n_out - 1);
         return gv_row_ptr(sg, w, row_bytes, o) + at;
     };
     // the wave's activation operands are the same for every row it walks (its step is fixed): read once from LDS,
@@ -774,7 +778,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         }
         __builtin_amdgcn_wave_barrier();
         acc = kf_wave_sum_dpp(acc);
-        const int o = (it * B + (int)blockIdx.x) * RPB + rg;
+        const int o = grp(it) * RPB + rg;
         if (lane == 0 && o < n_out) {
             if constexpr (WPR == 1)
                 gv_store(sg, y, bias, res, o, acc);
@@ -826,7 +830,7 @@ __global__ void __launch_bounds__(GV_THREADS) gemv_pipe_kernel(const uint8_t* __
         __syncthreads();
         for (int t = threadIdx.x; t < iters * RPB; t += GV_THREADS) {
             const int it2 = t / RPB, g = t % RPB;
-            const int o = (it2 * B + (int)blockIdx.x) * RPB + g;
+            const int o = grp(it2) * RPB + g;
             if (o >= n_out) continue;
             float acc = 0.0f;
 #pragma unroll
