@@ -272,12 +272,14 @@ def test_gemv_one_shot_variant(cuda, knobs, ty, n, n_out):
 
 
 @pytest.mark.parametrize("ty,n,n_out", [(kf.TYPE_Q4_K, 4096, 4096), (kf.TYPE_Q4_K, 4096, 6144), (kf.TYPE_Q4_K, 4096, 28672),
-                                        (kf.TYPE_Q4_K, 4096, 30000), (kf.TYPE_Q4_K, 14336, 4096), (kf.TYPE_Q4_K, 2304, 9),
+                                        (kf.TYPE_Q4_K, 4096, 30000), (kf.TYPE_Q4_K, 14336, 4096), (kf.TYPE_Q4_K, 14336, 4100),
+                                        (kf.TYPE_Q4_K, 2304, 9),
                                         (kf.TYPE_Q8_0, 4096, 4096), (kf.TYPE_Q8_0, 14336, 1030), (kf.TYPE_Q8_0, 4128, 77)])
 def test_gemv_burst_variant(cuda, knobs, ty, n, n_out):
     """The burst GEMV (every wave's rows requested at launch, activation operands loaded per lane) forced at one to
     eight rows a wave and one to eight waves a row (KF_GEMV_BURST=8) against the pipelined kernel (KF_GEMV_BURST=0),
-    bit for bit with bias and residual, and the CPU backend within the f32 bar."""
+    bit for bit with bias and residual, and the CPU backend within the f32 bar. 14336 -> 4100: the pipelined kernel's
+    split rows walk contiguous row ranges per block, the last ones partial or empty."""
     import torch
 
     w = _tensor(_weights(ty, n_out, n, seed=47), cuda)
