@@ -31,13 +31,13 @@
 //   * staging is buffer_load ... lds DMA over buffer resources based at the tile's first rows; rows past M or N read
 //     as zeros through the hardware range check. The DMA is inline assembly (kf_adma16 / kf_adma4) with explicit
 //     waits (vmcnt(0) and a barrier at each stage's end): through the builtin it carries no alias information and
-//     the compiler waited for the next stage's DMA before each MFMA phase (3% slower). Blocks run in XCD order (each XCD a contiguous range of tiles, M
-//     fastest), so the blocks in flight on an XCD share their weight tiles in its L2.
+//     the compiler waited for the next stage's DMA before each MFMA phase (3% slower). Blocks run in XCD order
+//     (each XCD a contiguous range of tiles, M fastest), so the blocks in flight on an XCD share their weight tiles
+//     in its L2.
 // Measured at M = 2048 (ablation builds with the builtin DMA, gate / down, us): 305-314 / 271-278 in all (300 / 268
-// with the DMA in assembly); the MFMA phase alone (no DMA,
-// rescale or plane expansion) 218-225 / 186-189, with the plane expansion 225 / 186, with the rescale 265 / 229,
-// with the DMA 245 / 216. The MFMA phase itself keeps the matrix cores about half busy, and the rescale and the DMA
-// add to it.
+// with the DMA in assembly); the MFMA phase alone (no DMA, rescale or plane expansion) 218-225 / 186-189, with the
+// plane expansion 225 / 186, with the rescale 265 / 229, with the DMA 245 / 216. The MFMA phase itself keeps the
+// matrix cores about half busy, and the rescale and the DMA add to it.
 #include "kf_knobs.h"
 #include "kf_blocks.h"
 #include "kf_device.h"
